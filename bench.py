@@ -1,0 +1,430 @@
+"""Benchmark of the gfx950 elementwise / broadcast / reduction kernels on one MI355X.
+
+Prints ONE JSON line. The workload (`value`, `roofline`) is BASELINE configs[1]: the SwiGLU gate with a broadcast
+bias, bf16 [2048, 9728] (xs_hip_act_bias_mul_2d); one step is one call over that batch with its inputs already in HBM.
+The per-op table `ops` times every configuration the same way (configs 0-4, the strided SwiGLU variant, Q and K RoPE
+as one call of two launches, K and V quantize / dequantize as one call of two launches).
+
+Timing: hipEvents on the stream the kernels are launched on, around one replay of a HIP graph holding `--steps`
+back-to-back calls (after `--warmup` untimed calls), median of `--repeats` replays; the same calls launched one by one
+from Python are reported beside it (`us_per_call_eager`). Every op cycles through enough copies of its buffers (>= 1 GiB in
+all) that no call finds its inputs in the 256 MiB Infinity Cache left there by the previous one.
+
+`cpu_baseline`: the reference's own cpu-ref backend (oracle/_ref/libxsref.so, compiled from the reference's sources),
+or the repository's restatement of it (oracle/liboracle.so) where that library is absent, timed single-threaded on
+this host on the same workload, for about `--cpu-seconds` seconds.
+
+Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--repeats 5] [--only OP] [--no-cpu]
+"""
+import argparse
+import ctypes as C
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "xpu-serve_amd"))
+
+import workloads as W  # noqa: E402
+import xs_hip as X  # noqa: E402
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "achieved HBM GB/s (% of ~8 TB/s peak) and µs/call per op; host CPU baseline"
+ROTATE_BYTES = 1 << 30
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def vp(t):
+    return C.c_void_p(t.ptr if isinstance(t, X.DeviceTensor) else t)
+
+
+class Op:
+    """One benchmarked call: `make_set()` builds one copy of its buffers, `launch(set, stream)` enqueues the call."""
+
+    def __init__(self, name, algo_bytes, footprint, make_set, launch, launches=1, kernel=""):
+        self.name = name
+        self.algo_bytes = algo_bytes
+        self.footprint = footprint
+        self.make_set = make_set
+        self.launch = launch
+        self.launches = launches
+        self.kernel = kernel
+
+
+def _events():
+    start, end = C.c_void_p(), C.c_void_p()
+    X.call("xs_hip_event_create", C.byref(start))
+    X.call("xs_hip_event_create", C.byref(end))
+    return start, end
+
+
+def _elapsed(start, end):
+    ms = C.c_float()
+    X.call("xs_hip_event_elapsed_ms", C.byref(ms), start, end)
+    return ms.value
+
+
+def time_op(op, steps, warmup, repeats, stream):
+    """Median ms per call over `repeats` windows of `steps` calls, two ways: replaying one HIP graph that holds the
+    `steps` calls (device time, no host launch cost between kernels), and launching them one by one from Python."""
+    nsets = max(2, math.ceil(ROTATE_BYTES / op.footprint))
+    sets = [op.make_set() for _ in range(nsets)]
+    X.synchronize()
+    for i in range(warmup):
+        op.launch(sets[i % nsets], stream)
+    X.call("xs_hip_stream_synchronize", stream)
+    start, end = _events()
+    # graph of `steps` calls
+    X.call("xs_hip_stream_begin_capture", stream)
+    for i in range(steps):
+        op.launch(sets[i % nsets], stream)
+    graph = C.c_void_p()
+    X.call("xs_hip_stream_end_capture", stream, C.byref(graph))
+    X.call("xs_hip_graph_launch", graph, stream)  # warm the graph
+    X.call("xs_hip_stream_synchronize", stream)
+    graph_ms = []
+    for _ in range(repeats):
+        X.call("xs_hip_event_record", start, stream)
+        X.call("xs_hip_graph_launch", graph, stream)
+        X.call("xs_hip_event_record", end, stream)
+        graph_ms.append(_elapsed(start, end) / steps)
+    X.call("xs_hip_graph_destroy", graph)
+    eager_ms = []
+    for _ in range(repeats):
+        X.call("xs_hip_event_record", start, stream)
+        for i in range(steps):
+            op.launch(sets[i % nsets], stream)
+        X.call("xs_hip_event_record", end, stream)
+        eager_ms.append(_elapsed(start, end) / steps)
+    X.call("xs_hip_event_destroy", start)
+    X.call("xs_hip_event_destroy", end)
+    X.call("xs_hip_stream_synchronize", stream)
+    del sets
+    ms = float(np.median(graph_ms))
+    gbs = op.algo_bytes / (ms * 1e-3) / 1e9
+    return {"us_per_call": round(ms * 1e3, 3), "gb_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
+            "us_per_call_eager": round(float(np.median(eager_ms)) * 1e3, 3),
+            "bytes": op.algo_bytes, "launches": op.launches, "kernel": op.kernel, "rotating_sets": nsets,
+            "samples_us": [round(v * 1e3, 3) for v in graph_ms]}
+
+
+def dcopy(t):
+    """A fresh device copy of device tensor t."""
+    c = X.DeviceTensor.empty(t.dtype, t.shape)
+    X.call("xs_hip_memcpy_d2d", vp(c), vp(t), C.c_size_t(t.nbytes), None)
+    return c
+
+
+def need(t, nbytes, what):
+    """Host-side check that a buffer covers what its launch will touch (the kernels cannot see buffer sizes)."""
+    size = t.nbytes if isinstance(t, X.DeviceTensor) else t.nbytes
+    if size < nbytes:
+        raise RuntimeError(f"{what}: buffer of {size} bytes, launch touches {nbytes}")
+
+
+# Each op is built in its own function, so its launcher closes over its own shapes only.
+
+def op_swiglu():
+    a = W.config1().arrays
+    rows, cols = a["gate"].shape
+    g0, u0, b0 = (X.DeviceTensor.from_numpy(a[k], X.BF16) for k in ("gate", "up", "bias"))
+
+    def mk():
+        s = (dcopy(g0), dcopy(u0), dcopy(b0), X.DeviceTensor.empty(X.BF16, (rows, cols)))
+        for t in (s[0], s[1], s[3]):
+            need(t, rows * cols * 2, "swiglu")
+        need(s[2], cols * 2, "swiglu bias")
+        return s
+
+    def go(s, stream):
+        g, u, b, y = s
+        X.call("xs_hip_act_bias_mul_2d", stream, X.SILU, X.BF16, vp(g), cols, vp(u), cols, vp(b), X.BF16, vp(y), cols,
+               rows, cols)
+    return Op("swiglu_bias", W.ALGO_BYTES["swiglu_bias"], 3 * rows * cols * 2, mk, go, 1, "ew2d_vec")
+
+
+def op_swiglu_strided():
+    a = W.config1().arrays
+    rows, cols = a["gate"].shape
+    f0 = X.DeviceTensor.from_numpy(a["fused"], X.BF16)
+    b0 = X.DeviceTensor.from_numpy(a["bias"], X.BF16)
+
+    def mk():
+        s = (dcopy(f0), dcopy(b0), X.DeviceTensor.empty(X.BF16, (rows, cols)))
+        need(s[0], rows * 2 * cols * 2, "swiglu strided")
+        need(s[2], rows * cols * 2, "swiglu strided out")
+        return s
+
+    def go(s, stream):
+        f, b, y = s
+        X.call("xs_hip_act_bias_mul_2d", stream, X.SILU, X.BF16, vp(f), 2 * cols, C.c_void_p(f.ptr + 2 * cols), 2 * cols,
+               vp(b), X.BF16, vp(y), cols, rows, cols)
+    return Op("swiglu_bias_strided", W.ALGO_BYTES["swiglu_bias_strided"], 4 * rows * cols * 2, mk, go, 1, "ew2d_vec")
+
+
+def op_rmsnorm():
+    a = W.config0().arrays
+    rows, width = a["x"].shape
+    x0, r0, w0 = (X.DeviceTensor.from_numpy(a[k]) for k in ("x", "residual", "weight"))
+
+    def mk():
+        s = (dcopy(x0), dcopy(r0), dcopy(w0), X.DeviceTensor.empty(X.F32, (rows, width)))
+        for t in (s[0], s[1], s[3]):
+            need(t, rows * width * 4, "rmsnorm")
+        return s
+
+    def go(s, stream):
+        x, r, w, y = s
+        # the updated residual goes back into r, as a decoder layer keeps it
+        X.call("xs_hip_add_rms_norm", stream, vp(x), vp(r), vp(w), None, vp(r), X.F32, vp(y), rows, width,
+               C.c_float(1e-6))
+    return Op("rmsnorm_residual", W.ALGO_BYTES["rmsnorm_residual"], 4 * rows * width * 4, mk, go, 1, "rms_norm_vec")
+
+
+def op_softmax():
+    c = W.config2a()
+    heads, _, keys = c.arrays["scores"].shape
+    s0 = X.DeviceTensor.from_numpy(c.arrays["scores"])
+    scale, valid = c.params["scale"], c.params["valid_len"]
+
+    def mk():
+        s = (dcopy(s0), X.DeviceTensor.empty(X.F32, (heads, keys)))
+        for t in s:
+            need(t, heads * keys * 4, "softmax")
+        return s
+
+    def go(s, stream):
+        x, y = s
+        X.call("xs_hip_softmax_masked", stream, vp(x), vp(y), heads, keys, keys, C.c_float(scale), None, valid)
+    return Op("softmax_masked", W.ALGO_BYTES["softmax_masked"], 2 * heads * keys * 4, mk, go, 1, "softmax_vec")
+
+
+def op_argmax():
+    c = W.config2b()
+    width = c.arrays["logits"].shape[1]
+    x0 = X.DeviceTensor.from_numpy(c.arrays["logits"])
+    nscratch = X.lib().xs_hip_topk_scratch(1, width, 1)
+
+    def mk():
+        sc = X.DeviceBuffer(nscratch)
+        X.call("xs_hip_memset", C.c_void_p(sc.ptr), 0, C.c_size_t(nscratch), None)
+        s = (dcopy(x0), X.DeviceTensor.empty(X.F32, (1, 1)), X.DeviceTensor.empty(X.I32, (1, 1)), sc)
+        need(s[0], width * 4, "argmax")
+        return s
+
+    def go(s, stream):
+        x, v, i, sc = s
+        X.call("xs_hip_topk", stream, vp(x), vp(v), vp(i), 1, width, 1, C.c_void_p(sc.ptr))
+    return Op("argmax", W.ALGO_BYTES["argmax"], width * 4, mk, go, 1, "argmax_chunks")
+
+
+def op_rope():
+    a = W.config3().arrays
+    tokens, qh, dim = a["q"].shape
+    kh = a["k"].shape[1]
+    q0 = X.DeviceTensor.from_numpy(a["q"], X.F16)
+    k0 = X.DeviceTensor.from_numpy(a["k"], X.F16)
+    p0 = X.DeviceTensor.from_numpy(a["positions"])
+    f0 = X.DeviceTensor.from_numpy(a["inv_freq"])
+
+    def mk():
+        s = (dcopy(q0), dcopy(k0), dcopy(p0), dcopy(f0), X.DeviceTensor.empty(X.F16, q0.shape),
+             X.DeviceTensor.empty(X.F16, k0.shape))
+        need(s[0], tokens * qh * dim * 2, "rope q")
+        need(s[1], tokens * kh * dim * 2, "rope k")
+        need(s[2], tokens * 4, "rope positions")
+        return s
+
+    def go(s, stream):
+        q, k, p, f, yq, yk = s
+        X.call("xs_hip_rope", stream, X.F16, vp(q), X.I32, vp(p), vp(f), X.F16, vp(yq), tokens, qh, dim, 0, 1, None)
+        X.call("xs_hip_rope", stream, X.F16, vp(k), X.I32, vp(p), vp(f), X.F16, vp(yk), tokens, kh, dim, 0, 1, None)
+    return Op("rope_qk", W.ALGO_BYTES["rope_qk"], 2 * (q0.nbytes + k0.nbytes), mk, go, 2, "rope_kernel")
+
+
+def _kv_inputs():
+    a = W.config4().arrays
+    tokens, heads, dim = a["k"].shape
+    rows = tokens * heads
+    k0 = X.DeviceTensor.from_numpy(a["k"].reshape(rows, dim), X.F16)
+    v0 = X.DeviceTensor.from_numpy(a["v"].reshape(rows, dim), X.F16)
+    return rows, dim, k0, v0
+
+
+def op_kv_quantize(inputs):
+    rows, dim, k0, v0 = inputs
+
+    def mk():
+        s = (dcopy(k0), dcopy(v0), X.DeviceTensor.empty(X.I8, (rows, dim)), X.DeviceTensor.empty(X.F32, (rows,)),
+             X.DeviceTensor.empty(X.I8, (rows, dim)), X.DeviceTensor.empty(X.F32, (rows,)))
+        need(s[0], rows * dim * 2, "kv k")
+        need(s[1], rows * dim * 2, "kv v")
+        return s
+
+    def go(s, stream):
+        k, v, kc, ks, vc, vs = s
+        X.call("xs_hip_quantize_kv", stream, X.KV_I8, X.F16, vp(k), vp(kc), vp(ks), rows, dim)
+        X.call("xs_hip_quantize_kv", stream, X.KV_I8, X.F16, vp(v), vp(vc), vp(vs), rows, dim)
+    return Op("kv_quantize", W.ALGO_BYTES["kv_quantize"], W.ALGO_BYTES["kv_quantize"], mk, go, 2, "quantize_i8_vec")
+
+
+def op_kv_dequantize(inputs):
+    rows, dim, k0, v0 = inputs
+    kc0, ks0 = X.quantize_kv(k0)
+    vc0, vs0 = X.quantize_kv(v0)
+
+    def mk():
+        s = (dcopy(kc0), dcopy(ks0), dcopy(vc0), dcopy(vs0), X.DeviceTensor.empty(X.F16, (rows, dim)),
+             X.DeviceTensor.empty(X.F16, (rows, dim)))
+        need(s[4], rows * dim * 2, "kv out")
+        return s
+
+    def go(s, stream):
+        kc, ks, vc, vs, ko, vo = s
+        X.call("xs_hip_dequantize_kv", stream, X.KV_I8, vp(kc), vp(ks), X.F16, vp(ko), rows, dim)
+        X.call("xs_hip_dequantize_kv", stream, X.KV_I8, vp(vc), vp(vs), X.F16, vp(vo), rows, dim)
+    return Op("kv_dequantize", W.ALGO_BYTES["kv_dequantize"], W.ALGO_BYTES["kv_dequantize"], mk, go, 2,
+              "dequantize_i8_vec")
+
+
+def op_copy():
+    n = 256 << 20  # bytes per call: the kernel the hardware byte counters are calibrated against
+    x0 = X.DeviceBuffer(n)
+    X.call("xs_hip_memset", C.c_void_p(x0.ptr), 1, C.c_size_t(n), None)
+
+    def mk():
+        x, y = X.DeviceBuffer(n), X.DeviceBuffer(n)
+        X.call("xs_hip_memcpy_d2d", C.c_void_p(x.ptr), C.c_void_p(x0.ptr), C.c_size_t(n), None)
+        return (x, y)
+
+    def go(s, stream):
+        x, y = s
+        X.call("xs_hip_copy", stream, C.c_void_p(x.ptr), C.c_void_p(y.ptr), C.c_size_t(n))
+    return Op("copy", 2 * n, 2 * n, mk, go, 1, "copy_kernel")
+
+
+OP_ORDER = ["swiglu_bias", "swiglu_bias_strided", "rmsnorm_residual", "softmax_masked", "argmax", "rope_qk",
+            "kv_quantize", "kv_dequantize"]
+
+
+def build_ops(only):
+    """Yields the ops one at a time, so only one op's buffers are alive at once."""
+    names = OP_ORDER if only is None else [n for n in OP_ORDER + ["copy"] if n in only]
+    kv = None
+    for name in names:
+        if name in ("kv_quantize", "kv_dequantize") and kv is None:
+            kv = _kv_inputs()
+        yield {"swiglu_bias": op_swiglu, "swiglu_bias_strided": op_swiglu_strided, "rmsnorm_residual": op_rmsnorm,
+               "softmax_masked": op_softmax, "argmax": op_argmax, "rope_qk": op_rope, "copy": op_copy,
+               "kv_quantize": lambda: op_kv_quantize(kv), "kv_dequantize": lambda: op_kv_dequantize(kv)}[name]()
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# CPU baseline (the oracle package is test infrastructure: used here only for this reported baseline leg)
+
+def cpu_baseline(seconds):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O  # noqa: E402
+    ref = O.reference()
+    kind = "reference" if ref is not None else "port"
+    impl = ref if ref is not None else O.oracle()
+    a = W.config1().arrays
+    rows, cols = a["gate"].shape
+    sample_rows = 256
+    g, u, b = a["gate"][:sample_rows], a["up"][:sample_rows], a["bias"]
+
+    def once():
+        if kind == "reference":
+            y = impl.act_bias_mul(O.SILU, g, u, b, O.BF16)
+        else:
+            y = impl.act_bias_mul(O.SILU, impl.widen(g, O.BF16), impl.widen(u, O.BF16), impl.widen(b, O.BF16))
+        return impl.narrow(y, O.BF16)
+
+    once()
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        once()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    per_call = el / n
+    sample_bytes = 3 * sample_rows * cols * 2 + cols * 2
+    cpu = open("/proc/cpuinfo").read() if os.path.exists("/proc/cpuinfo") else ""
+    model = next((l.split(":", 1)[1].strip() for l in cpu.splitlines() if l.startswith("model name")), "unknown")
+    return {"value": round(sample_bytes / per_call / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": f"SwiGLU bias bf16 rows 0..{sample_rows - 1} of configs[1] ([{sample_rows}, {cols}], "
+                      f"{sample_bytes} algorithmic bytes), {n} calls in {el:.1f} s through "
+                      + ("the reference cpu-ref backend's Session::run (Add, Silu, Mul) + f32->bf16"
+                         if kind == "reference" else "the oracle restatement"),
+            "us_per_full_call": round(per_call * (rows / sample_rows) * 1e6, 1),
+            "host_cpu": model, "nproc": os.cpu_count()}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--repeats", type=int, default=5)
+    ap.add_argument("--only", type=str, default=None, help="comma-separated op names (or 'copy')")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": f"--gpus {args.gpus}: this path is built and measured on one GPU; the kernels "
+                                   "shard by rows with no exchange (see DESIGN.md), and no multi-GPU figure is "
+                                   "produced"}))
+        sys.exit(2)
+    only = None if args.only is None else set(args.only.split(","))
+    X.call("xs_hip_set_device", 0)
+    dev_name = X.device_name(0)
+    log(f"device {dev_name}")
+    stream = C.c_void_p()
+    X.call("xs_hip_stream_create", C.byref(stream))
+    results = {}
+    for op in build_ops(only):
+        log(f"timing {op.name}")
+        results[op.name] = time_op(op, args.steps, args.warmup, args.repeats, stream)
+        log(f"  {op.name}: {results[op.name]['us_per_call']} us/call, {results[op.name]['gb_s']} GB/s")
+    X.call("xs_hip_stream_destroy", stream)
+
+    head = results.get("swiglu_bias") or next(iter(results.values()))
+    line = {
+        "metric": METRIC,
+        "value": head["gb_s"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us_per_call"] / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: splitmix64 + Box-Muller (f64), seed 0x5EED0001, gate/up ~ N(0,1), bias ~ N(0,0.02)",
+        "config": {"workload": "configs[1]: SwiGLU gate with broadcast bias, out = bf16(silu(gate + bias) * up), "
+                               "gate/up/out bf16 [2048, 9728], bias bf16 [9728]",
+                   "entry_point": "xs_hip_act_bias_mul_2d", "algorithmic_bytes_per_call": W.ALGO_BYTES["swiglu_bias"]},
+        "roofline": {"bound": "hbm", "achieved": head["gb_s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": head["frac_of_peak"], "traffic": None,
+                     "kernel": head["kernel"], "avg_launch_us": head["us_per_call"] / head["launches"]},
+        "device": dev_name,
+        "ops": results,
+    }
+    if not args.no_cpu and only is None:
+        log("cpu baseline")
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,231 @@
+/*
+ * xs_hip.h -- the C-ABI of the MI355X (gfx950) device for xpu-serve's elementwise, broadcast and reduction ops.
+ *
+ * Each entry point replaces one launcher of the reference's device-dispatch surface, `xs::sycl_be::*` in
+ * src/backend/sycl/sycl_kernels.h, with a plain-C function:
+ *   - `sycl::queue&` becomes an opaque stream handle (`void*`, a hipStream_t; NULL is the null stream);
+ *   - template parameters (X, Y, CT, I) become `xs_dtype` arguments whose values are the reference's `DType`
+ *     enumerators (src/tensor/dtype.h:17);
+ *   - the reference's C++ exceptions (`xs::Error`, src/util/error.h:12-35) become an `int` status: XS_HIP_OK, or a
+ *     code whose message `xs_hip_last_error()` returns (thread-local, naming the op and what is wrong).
+ * Every launcher enqueues on the stream and returns without waiting, as the reference's do (sycl_kernels.h:3).
+ * Pointers are device pointers; sizes and strides are element counts (int64). No torch, SYCL or HIP types appear here.
+ *
+ * Numerical contract (checked by the repository's parity tests against the reference's CPU path, cpu-ref):
+ * f32 outputs within 1e-5 relative, f16/bf16 outputs within one unit in the last place of the output dtype (inputs
+ * widened exactly, arithmetic in f32 or f64), argmax indices, int8 codes and scales bit-exact.
+ */
+#ifndef XS_HIP_H
+#define XS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- Status, errors, version -------------------------------------------------------------------------------- */
+
+enum {
+    XS_HIP_OK = 0,
+    XS_HIP_EINVAL = 1,       /* a bad argument: shape, dtype, pointer, alignment or option */
+    XS_HIP_EUNSUPPORTED = 2, /* a valid request this device does not implement (e.g. a TurboQuant KV format) */
+    XS_HIP_ERUNTIME = 3      /* the HIP runtime refused a launch or a memory operation */
+};
+
+/* The message of the calling thread's last failed call ("" when none failed). Replaces the text of the xs::Error the
+ * reference throws (src/util/error.h:25-28). */
+const char* xs_hip_last_error(void);
+/* 1 for this version of the ABI. */
+int xs_hip_abi_version(void);
+
+/* ---- Types --------------------------------------------------------------------------------------------------- */
+
+/* Values of the reference's `enum class DType : uint8_t` (src/tensor/dtype.h:17), in its order. The kernels accept
+ * F32, F16, BF16 for floats, I32 and I64 for positions, I8 for KV codes. */
+typedef enum {
+    XS_F32 = 0,
+    XS_F16 = 1,
+    XS_BF16 = 2,
+    XS_I64 = 3,
+    XS_I32 = 4,
+    XS_I8 = 5,
+    XS_U8 = 6,
+    XS_BOOL = 7
+} xs_dtype;
+
+/* `xs::sycl_be::UnaryOp` (src/backend/sycl/sycl_kernels.h:21), in its order. The act_* entry points take SILU,
+ * GELU_TANH, SIGMOID and GELU. */
+typedef enum {
+    XS_UNARY_SCALE = 0,
+    XS_UNARY_TANH = 1,
+    XS_UNARY_GELU_TANH = 2,
+    XS_UNARY_SOFTCAP = 3,
+    XS_UNARY_SIGMOID = 4,
+    XS_UNARY_SILU = 5,
+    XS_UNARY_SOFTPLUS = 6,
+    XS_UNARY_CLAMP = 7,
+    XS_UNARY_GELU = 8
+} xs_unary_op;
+
+/* `xs::sycl_be::BinaryOp` (sycl_kernels.h:34). */
+typedef enum { XS_BINARY_ADD = 0, XS_BINARY_MUL = 1, XS_BINARY_DIV = 2 } xs_binary_op;
+
+/* `xs::quant::KvFormat` (src/quant/kv_format.h:11-17). Only XS_KV_I8 is implemented. */
+typedef enum { XS_KV_FLOAT = 0, XS_KV_I8 = 1, XS_KV_TURBO4 = 2, XS_KV_TURBO3 = 3, XS_KV_TURBO2 = 4 } xs_kv_format;
+
+/* numpy broadcasting over at most XS_MAX_RANK dims: the out shape and the element strides of a, b and y per out dim.
+ * A stride of 0 is a broadcast dim; any other stride (including a column slice's row stride) is honoured. Replaces
+ * `xs::sycl_be::Broadcast` (sycl_kernels.h:37-42), which has no y strides (its y is always contiguous: pass the
+ * row-major strides of `out`, or let xs_hip_broadcast_fill set them). */
+#define XS_MAX_RANK 6
+typedef struct {
+    int32_t rank;
+    int64_t out[XS_MAX_RANK];
+    int64_t stride_a[XS_MAX_RANK];
+    int64_t stride_b[XS_MAX_RANK];
+    int64_t stride_y[XS_MAX_RANK];
+} xs_broadcast;
+
+/* Fills `bc` for row-major contiguous a [a_rank dims] and b [b_rank dims] broadcast like numpy (shapes right-aligned,
+ * a dim of 1 stretches) into a contiguous y: the host half of cpu_ref::broadcast_shape / broadcast_strides
+ * (src/backend/cpu_ref/ops.cpp:42-66). Fails (XS_HIP_EINVAL) on shapes that do not broadcast. */
+int xs_hip_broadcast_fill(xs_broadcast* bc, const int64_t* a_shape, int32_t a_rank, const int64_t* b_shape,
+                          int32_t b_rank);
+
+/* ---- Device, memory, streams, events (the session's plumbing: sycl_backend.cpp:64-107 DeviceBuffer) ---------- */
+
+int xs_hip_device_count(int* count);
+/* name: at least 256 bytes. */
+int xs_hip_device_info(int device, char* name, size_t name_len, uint64_t* memory_bytes, int* compute_units);
+int xs_hip_set_device(int device);
+int xs_hip_malloc(void** ptr, size_t bytes);
+int xs_hip_free(void* ptr);
+int xs_hip_memset(void* ptr, int value, size_t bytes, void* stream);
+int xs_hip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream); /* synchronous w.r.t. the host */
+int xs_hip_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream); /* synchronous w.r.t. the host */
+int xs_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream); /* asynchronous */
+int xs_hip_stream_create(void** stream);
+int xs_hip_stream_destroy(void* stream);
+int xs_hip_stream_synchronize(void* stream);
+int xs_hip_device_synchronize(void);
+int xs_hip_event_create(void** event);
+int xs_hip_event_destroy(void* event);
+int xs_hip_event_record(void* event, void* stream);
+/* Milliseconds between two recorded events (waits for `end`). */
+int xs_hip_event_elapsed_ms(float* ms, void* start, void* end);
+/* Stream capture into a HIP graph (relaxed capture mode): begin, launch the calls to record, end -> an executable
+ * graph; replay it with xs_hip_graph_launch; free it with xs_hip_graph_destroy. The launchers above record no memset
+ * or allocation, so any sequence of them can be captured. */
+int xs_hip_stream_begin_capture(void* stream);
+int xs_hip_stream_end_capture(void* stream, void** graph_exec);
+int xs_hip_graph_launch(void* graph_exec, void* stream);
+int xs_hip_graph_destroy(void* graph_exec);
+
+/* ---- Elementwise and broadcast ------------------------------------------------------------------------------- */
+
+/* y = a op b under `bc` (any strides), a/b/y each F32, F16 or BF16; arithmetic in f32 on exactly widened operands,
+ * rounded once to y's dtype. Replaces sycl_be::binary (sycl_kernels.h:43-44); semantics cpu_ref::add / mul / div
+ * (ops.cpp:68-93, 201-207, 401-403). In-place (y == a or y == b with the same strides) is allowed. */
+int xs_hip_binary(void* stream, xs_binary_op op, xs_dtype a_dtype, const void* a, xs_dtype b_dtype, const void* b,
+                  xs_dtype y_dtype, void* y, const xs_broadcast* bc);
+/* Contiguous fast paths: same shape (sycl_kernels.h:46-47) and b repeating every `period` elements of a, a row vector
+ * over the leading dims (sycl_kernels.h:48-49). n % period == 0. */
+int xs_hip_binary_same(void* stream, xs_binary_op op, xs_dtype dtype, const void* a, const void* b, xs_dtype y_dtype,
+                       void* y, int64_t n);
+int xs_hip_binary_period(void* stream, xs_binary_op op, xs_dtype dtype, const void* a, const void* b,
+                         xs_dtype y_dtype, void* y, int64_t n, int64_t period);
+/* Fused residuals (sycl_kernels.h:51-55), f32 in: y = a + b * c[i % period] and y = a + (b + c[i % period]); the
+ * result equals the two unfused f32 ops cpu-ref evaluates in graph order. */
+int xs_hip_add_mul(void* stream, const float* a, const float* b, const float* c, xs_dtype y_dtype, void* y, int64_t n,
+                   int64_t period);
+int xs_hip_add3(void* stream, const float* a, const float* b, const float* c, xs_dtype y_dtype, void* y, int64_t n,
+                int64_t period);
+
+/* y = act(x) * b, same shapes, x/b in x_dtype (F32, F16, BF16), y in y_dtype; act is SILU, GELU_TANH, SIGMOID or
+ * GELU. Replaces sycl_be::act_mul (sycl_kernels.h:28-29), the fused Mul(Silu(gate), up) of gated_mlp
+ * (src/models/common/blocks.cpp:23-27); semantics cpu_ref::silu etc. then cpu_ref::mul (ops.cpp:201-247). */
+int xs_hip_act_mul(void* stream, xs_unary_op act, xs_dtype x_dtype, const void* x, const void* b, xs_dtype y_dtype,
+                   void* y, int64_t n);
+/* y = act(x + bias[i % period]), x f32. Replaces sycl_be::unary_bias (sycl_kernels.h:31-32). */
+int xs_hip_unary_bias(void* stream, xs_unary_op act, const float* x, const float* bias, xs_dtype y_dtype, void* y,
+                      int64_t n, int64_t period);
+/* The gated MLP activation on 2-D operands with row strides (column slices of a fused gate|up buffer allowed):
+ * y[r, c] = act(x[r, c] + bias[c]) * b[r, c] for r < rows, c < cols; bias may be NULL. x, b, bias in x_dtype.
+ * One kernel for what the reference launches as unary_bias then act_mul (sycl_backend.cpp:1004-1047, 1899-1907);
+ * the value equals cpu-ref's Add, Silu, Mul in f32 (ops.cpp:201-247) rounded to y_dtype. */
+int xs_hip_act_bias_mul_2d(void* stream, xs_unary_op act, xs_dtype x_dtype, const void* x, int64_t x_row_stride,
+                           const void* b, int64_t b_row_stride, const void* bias, xs_dtype y_dtype, void* y,
+                           int64_t y_row_stride, int64_t rows, int64_t cols);
+/* y = x converted to y_dtype (F32/F16/BF16 both ways): round to nearest even, f16 overflow to inf, NaN stays NaN
+ * (src/util/half.h:19-25, half.cpp:36-56). Replaces sycl_be::to_half (sycl_kernels.h:130). */
+int xs_hip_convert(void* stream, xs_dtype x_dtype, const void* x, xs_dtype y_dtype, void* y, int64_t n);
+
+/* ---- Row reductions ------------------------------------------------------------------------------------------ */
+
+/* Rows of `width`: y = x / rms(x) [* w] [+ bias], w and bias f32 [width] or NULL, the mean of squares in f32 and then
+ * f64, eps added in f64. x f32, F16 or BF16; y F32, F16 or BF16. Replaces sycl_be::rms_norm (sycl_kernels.h:88-90);
+ * semantics cpu_ref::rms_norm (ops.cpp:260-281). */
+int xs_hip_rms_norm(void* stream, xs_dtype x_dtype, const void* x, const float* w, const float* bias, xs_dtype y_dtype,
+                    void* y, int64_t rows, int64_t width, float eps);
+/* The residual stream's add-and-norm in one pass: h = x + residual (f32, exact as cpu_ref::add), h_out = h (may be
+ * `residual` or `x` itself, in place), y = rms_norm(h) [* w] [+ bias]. The graph pattern
+ * h = add(h, f(rms_norm(h))) (src/models/qwen3/qwen3_decoder.cpp:101-102) evaluated by cpu-ref as Add then RmsNorm. */
+int xs_hip_add_rms_norm(void* stream, const float* x, const float* residual, const float* w, const float* bias,
+                        float* h_out, xs_dtype y_dtype, void* y, int64_t rows, int64_t width, float eps);
+/* Row softmax, f32, rows of `width`. Replaces sycl_be::softmax (sycl_kernels.h:58); semantics cpu_ref::softmax
+ * (ops.cpp:644-661): max, sum of exp, exp / sum. */
+int xs_hip_softmax(void* stream, const float* x, float* y, int64_t rows, int64_t width);
+/* The masked attention-score form: per row r, s = fl32(x * scale) for keys c < valid_len[r] (or `valid_len_all` when
+ * valid_len is NULL) and -inf beyond, then softmax; masked keys come out exactly 0. x/y rows `row_stride` apart.
+ * Equals cpu-ref's Scale (ops.cpp:209-211), Add of a 0/-inf mask, Softmax (ops.cpp:644-661). */
+int xs_hip_softmax_masked(void* stream, const float* x, float* y, int64_t rows, int64_t width, int64_t row_stride,
+                          float scale, const int64_t* valid_len, int64_t valid_len_all);
+/* Bytes of scratch xs_hip_topk needs (0: none, NULL allowed). Replaces sycl_be::topk_scratch (sycl_kernels.h:61). */
+size_t xs_hip_topk_scratch(int64_t rows, int64_t width, int64_t k);
+/* The k largest per row of x [rows, width] f32: values f32 and indices i32 [rows, k], largest first, equal values keep
+ * the lower index first (cpu_ref::topk, ops.cpp:663-684; spec graph.h:70-71). k = 1 is argmax (blocks::argmax_rows,
+ * blocks.cpp:36-38). `scratch` (256-byte aligned) holds at least xs_hip_topk_scratch bytes and must be ZERO-FILLED once
+ * before its first use: its head holds per-row arrival counters that every call leaves zero again, so one scratch
+ * serves calls of any shape in stream order; concurrent calls must not share one. Replaces sycl_be::topk
+ * (sycl_kernels.h:62-63). */
+int xs_hip_topk(void* stream, const float* x, float* values, int32_t* indices, int64_t rows, int64_t width, int64_t k,
+                void* scratch);
+
+/* ---- RoPE ---------------------------------------------------------------------------------------------------- */
+
+/* Rotate-half (NeoX) RoPE of x [tokens, heads, dim] into y (y may be x). positions [tokens] or [tokens, sections]
+ * (pos_dtype I32 or I64), inv_freq f32 [rotary / (2 sections)] (or [rotary / 2] with pair_axes); rotary 0 = dim;
+ * channels past `rotary` pass through. With pair_axes (i32 [rotary / 2], device) one section whose pair i reads
+ * positions[:, pair_axes[i]]. Angles pos * inv_freq and their cos/sin in f64, rotation in f64, rounded to f32 and then
+ * to y's dtype -- cpu_ref::rope (ops.cpp:343-399). Replaces sycl_be::rope (sycl_kernels.h:114-116). */
+int xs_hip_rope(void* stream, xs_dtype x_dtype, const void* x, xs_dtype pos_dtype, const void* positions,
+                const float* inv_freq, xs_dtype y_dtype, void* y, int64_t tokens, int64_t heads, int64_t dim,
+                int64_t rotary, int64_t sections, const int32_t* pair_axes);
+
+/* ---- int8 KV cache ------------------------------------------------------------------------------------------- */
+
+/* Codes and scales of x [rows, width] (x_dtype F32, F16 or BF16): per row amax = max |x|, inv = 127 / amax (f32,
+ * correctly rounded; 0 for an all-zero row), code = clamp(round-half-even(x * inv), -127, 127), scale = amax / 127.
+ * codes int8 [rows, width], scales f32 [rows] (kv_row_bytes I8, src/quant/kv_format.cpp:47-48). Replaces
+ * sycl_be::quantize_kv (sycl_kernels.h:213-214); semantics quant::quantize_kv_row_i8 (src/quant/quant.cpp:259-267).
+ * Only XS_KV_I8. */
+int xs_hip_quantize_kv(void* stream, xs_kv_format format, xs_dtype x_dtype, const void* x, void* codes, void* scales,
+                       int64_t rows, int64_t width);
+/* out [rows, width] (F32, F16 or BF16) = fl32(code * scale[row]) rounded to out's dtype: quant::round_trip_kv_i8
+ * (quant.cpp:269-277). Replaces sycl_be::dequantize_kv (sycl_kernels.h:217-218). Only XS_KV_I8. */
+int xs_hip_dequantize_kv(void* stream, xs_kv_format format, const void* codes, const void* scales, xs_dtype out_dtype,
+                         void* out, int64_t rows, int64_t width);
+
+/* ---- Measurement helper -------------------------------------------------------------------------------------- */
+
+/* y = x, `bytes` bytes (a multiple of 16, 16-byte aligned), with the 128-bit streaming loads and stores of the
+ * kernels above: the known-size kernel hardware byte counters are calibrated against. No reference counterpart. */
+int xs_hip_copy(void* stream, const void* x, void* y, size_t bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XS_HIP_H */

@@ -1,0 +1,507 @@
+"""Parity of the gfx950 kernels with the reference CPU path, through the C ABI.
+
+Each op is checked against (a) the golden vectors the reference's own cpu-ref backend wrote, (b) the oracle
+(oracle/oracle.cpp) on seeded inputs at odd shapes, dtypes and alignments, and (c) the oracle at the full size of its
+BASELINE configuration, plus size-independent properties there. Bars: f32 within 1e-5 relative, f16/bf16 within one
+ulp of the output dtype, int8 codes, scales, indices and argmax values bit-exact.
+"""
+import ctypes as C
+import math
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import workloads as W
+import xs_hip as X
+from oracle import BF16, F16, F32, GELU, GELU_TANH, SIGMOID, SILU, oracle
+from tol import assert_exact, assert_f32_close, assert_ulp
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def golden(name):
+    return np.load(os.path.join(GOLDEN, name + ".npz"), allow_pickle=False)
+
+
+def step(msg):
+    """Names the case before its GPU work, so a run that dies still says where."""
+    print(f"[gpu] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ora():
+    return oracle()
+
+
+def dev(a, dtype=None):
+    return X.DeviceTensor.from_numpy(a, dtype)
+
+
+def fmt(dtype):
+    return "f16" if dtype == F16 else "bf16"
+
+
+def check_out(got, want_f32, dtype, ora, what, atol=0.0):
+    """got: device output in `dtype`; want_f32: the oracle's f32 result before narrowing."""
+    if dtype == F32:
+        assert_f32_close(got, want_f32, what=what, atol=atol)
+    else:
+        assert_ulp(got, ora.narrow(want_f32, dtype), fmt(dtype), what=what, atol=atol)
+
+
+def gelu_noise(x, b):
+    """cpu-ref's own f64 rounding noise in 0.5 x (1 + tanh u) / 0.5 x (1 + erf z) where the sum cancels: the device's
+    f64 tanh / erf may differ from the host libm's by an ulp there (2^-53 of 1), which is |x b| 2^-53 of output."""
+    return np.abs(x.astype(np.float64)) * np.abs(b.astype(np.float64)) * 2.0 ** -50
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# int8 KV
+
+def test_kv_quantize_goldens(ora):
+    g = golden("kv_i8")
+    step("kv quantize goldens f32 [64, 128]")
+    codes, scales = X.quantize_kv(dev(g["x"]))
+    assert_exact(codes.numpy(), g["codes"], "codes")
+    assert_exact(scales.numpy(), g["scales"], "scales")
+    finite = np.where(np.isfinite(g["x"]), g["x"], 0.0).astype(np.float32)
+    c2, s2 = X.quantize_kv(dev(finite))
+    assert_exact(X.dequantize_kv(c2, s2, F32).numpy(), g["round_trip"], "round trip")
+    for t in ("k16", "v16"):
+        step(f"kv quantize goldens {t} f16 KvCache append")
+        x = g[t].reshape(-1, 128)
+        c, s = X.quantize_kv(dev(x, F16))
+        back = X.dequantize_kv(c, s, F32).numpy().reshape(g[t].shape)
+        assert_exact(back, g[f"{t}_rt"], t)
+        back16 = X.dequantize_kv(c, s, F16).numpy().reshape(g[t].shape)
+        assert_exact(back16.view(np.uint16), ora.narrow(g[f"{t}_rt"], F16).view(np.uint16), t + " f16")
+
+
+@pytest.mark.parametrize("dtype", [F32, F16, BF16])
+@pytest.mark.parametrize("width", [16, 64, 128, 256, 96, 100, 1000])
+def test_kv_quantize_shapes(ora, dtype, width):
+    rng = np.random.default_rng(width)
+    rows = 37
+    x = (rng.standard_normal((rows, width)) * rng.uniform(0.01, 100, (rows, 1))).astype(np.float32)
+    x[3] = 0.0
+    xs = ora.narrow(x, dtype)
+    step(f"kv quantize {DT[dtype]} [{rows}, {width}]")
+    codes, scales = X.quantize_kv(dev(xs, dtype))
+    wc, ws = ora.quantize_kv(ora.widen(xs, dtype))
+    assert_exact(codes.numpy(), wc, "codes")
+    assert_exact(scales.numpy(), ws, "scales")
+    for od in (F32, F16, BF16):
+        out = X.dequantize_kv(codes, scales, od).numpy()
+        want = ora.narrow(ora.dequantize_kv(wc, ws), od)
+        assert_exact(out.view(np.uint16) if od != F32 else out, want.view(np.uint16) if od != F32 else want)
+
+
+DT = {F32: "f32", F16: "f16", BF16: "bf16"}
+
+
+def test_kv_config4_full(ora):
+    cfg = W.config4()
+    for name in ("k", "v"):
+        x = cfg.arrays[name].reshape(-1, 128)
+        step(f"kv quantize config 4 {name} [{x.shape[0]}, 128] f16")
+        codes, scales = X.quantize_kv(dev(x, F16))
+        wc, ws = ora.quantize_kv(ora.widen(x, F16))
+        assert_exact(scales.numpy(), ws, name + " scales")
+        assert_exact(codes.numpy(), wc, name + " codes")
+        step(f"kv dequantize config 4 {name}")
+        back = X.dequantize_kv(codes, scales, F16).numpy()
+        want = ora.narrow(ora.dequantize_kv(wc, ws), F16)
+        assert_exact(back.view(np.uint16), want.view(np.uint16), name + " dequant")
+        # size-independent: |x - dequant| <= scale / 2 (+ the f16 rounding of the dequantized value)
+        xf = ora.widen(x, F16)
+        bf = back.astype(np.float32)
+        bound = ws[:, None] * 0.5 + np.abs(bf) * 2.0 ** -11
+        assert (np.abs(xf - bf) <= bound * (1 + 1e-6)).all()
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# activation times gate (SwiGLU)
+
+@pytest.mark.parametrize("tag,dtype", [("f32", F32), ("f16", F16), ("bf16", BF16)])
+def test_act_goldens(ora, tag, dtype):
+    g = golden("act_mul")
+    gate, up, bias = g[f"{tag}_gate"], g[f"{tag}_up"], g[f"{tag}_bias"]
+    xg, xu, xb = ora.widen(gate, dtype), ora.widen(up, dtype), ora.widen(bias, dtype)
+    for act in (SILU, GELU_TANH, SIGMOID, GELU):
+        gelu = act in (GELU, GELU_TANH)
+        nb = gelu_noise(ora.binary(0, xg, xb), xu) if gelu else 0.0
+        nn = gelu_noise(xg, xu) if gelu else 0.0
+        step(f"act_bias_mul golden {tag} act {act}")
+        y = X.swiglu(dev(gate, dtype), dev(up, dtype), dev(bias, dtype), dtype, act).numpy()
+        check_out(y, g[f"{tag}_act{act}_bias"], dtype, ora, f"{tag} act {act} bias", nb)
+        y = X.act_mul(act, dev(gate, dtype), dev(up, dtype), dtype).numpy()
+        check_out(y, g[f"{tag}_act{act}_nobias"], dtype, ora, f"{tag} act {act}", nn)
+        y = X.act_mul(act, dev(gate, dtype), dev(up, dtype), F32).numpy()
+        assert_f32_close(y, g[f"{tag}_act{act}_nobias"], what=f"{tag} act {act} -> f32", atol=nn)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 8), (3, 24), (7, 100), (64, 9728), (5, 13)])
+def test_swiglu_shapes(ora, rows, cols):
+    rng = np.random.default_rng(rows * 1000 + cols)
+    gate = ora.narrow(rng.standard_normal((rows, cols)).astype(np.float32) * 4, BF16)
+    up = ora.narrow(rng.standard_normal((rows, cols)).astype(np.float32), BF16)
+    bias = ora.narrow(rng.standard_normal(cols).astype(np.float32) * 0.02, BF16)
+    step(f"swiglu bf16 [{rows}, {cols}]")
+    y = X.swiglu(dev(gate, BF16), dev(up, BF16), dev(bias, BF16), BF16).numpy()
+    want = ora.act_bias_mul(SILU, ora.widen(gate, BF16), ora.widen(up, BF16), ora.widen(bias, BF16))
+    assert_ulp(y, ora.narrow(want, BF16), "bf16", what="swiglu")
+
+
+def test_unary_bias(ora):
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((9, 40)).astype(np.float32) * 3
+    bias = rng.standard_normal(40).astype(np.float32)
+    dx, db = dev(x), dev(bias)  # held for the calls: a temporary's buffer would be freed before the kernel runs
+    for act in (SILU, SIGMOID, GELU_TANH, GELU):
+        step(f"unary_bias act {act}")
+        y = X.DeviceTensor.empty(F32, x.shape)
+        X.call("xs_hip_unary_bias", None, act, C.c_void_p(dx.ptr), C.c_void_p(db.ptr), F32, C.c_void_p(y.ptr), x.size,
+               40)
+        xb = ora.binary(0, x, bias)
+        want = ora.unary(act, xb)
+        noise = gelu_noise(xb, np.ones_like(xb)) if act in (GELU, GELU_TANH) else 0.0
+        assert_f32_close(y.numpy(), want, what=f"unary_bias {act}", atol=noise)
+
+
+def swiglu_strided(fused_dev, bias_dev, rows, cols, y_dtype=BF16):
+    y = X.DeviceTensor.empty(y_dtype, (rows, cols))
+    X.call("xs_hip_act_bias_mul_2d", None, SILU, BF16, C.c_void_p(fused_dev.ptr), 2 * cols,
+           C.c_void_p(fused_dev.ptr + cols * 2), 2 * cols, C.c_void_p(bias_dev.ptr), y_dtype, C.c_void_p(y.ptr),
+           cols, rows, cols)
+    return y
+
+
+def test_swiglu_config1_full(ora):
+    cfg = W.config1()
+    a = cfg.arrays
+    rows, cols = a["gate"].shape
+    step("swiglu config 1 contiguous [2048, 9728] bf16")
+    y = X.swiglu(dev(a["gate"], BF16), dev(a["up"], BF16), dev(a["bias"], BF16), BF16).numpy()
+    want = ora.narrow(ora.act_bias_mul(SILU, ora.widen(a["gate"], BF16), ora.widen(a["up"], BF16),
+                                       ora.widen(a["bias"], BF16)), BF16)
+    n_diff = assert_ulp(y, want, "bf16", what="swiglu config 1")
+    assert n_diff <= y.size * 1e-3  # a 1-ulp difference only where f32 silu straddles a bf16 rounding boundary
+    step("swiglu config 1 strided (column slices of [2048, 19456])")
+    ys = swiglu_strided(dev(a["fused"], BF16), dev(a["bias"], BF16), rows, cols).numpy()
+    assert_exact(ys, y, "strided == contiguous")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# binary broadcast
+
+def test_binary_goldens(ora):
+    g = golden("binary")
+    for i in range(8):
+        a, b = g[f"c{i}_a"], g[f"c{i}_b"]
+        for op in range(3):
+            step(f"binary golden case {i} {a.shape} op {op} {b.shape}")
+            for yd in (F32, F16, BF16):
+                y = X.binary(op, dev(a), dev(b), yd).numpy()
+                want = g[f"c{i}_op{op}"]
+                if yd == F32:
+                    assert_exact(y, want, f"case {i} op {op}")
+                else:
+                    assert_exact(y.view(np.uint16), ora.narrow(want, yd).view(np.uint16), f"case {i} op {op} {yd}")
+    step("binary golden f16 / bf16 operands")
+    assert_exact(X.add(dev(g["h_a"], F16), dev(g["h_b"], F16)).numpy(), g["h_add"])
+    assert_exact(X.mul(dev(g["b_a"], BF16), dev(g["b_b"], BF16)).numpy(), g["b_mul"])
+    # mixed operand dtypes take the general kernel
+    assert_exact(X.add(dev(g["h_a"], F16), dev(ora.widen(g["h_b"], F16))).numpy(), g["h_add"])
+
+
+@pytest.mark.parametrize("sa,sb", [((2048, 9728), (9728,)), ((512, 2560), (512, 2560)), ((33, 17), (17,)),
+                                   ((8, 1, 64), (1, 16, 64)), ((4, 3, 5, 8), (3, 1, 8)), ((1000,), (1,)),
+                                   ((6, 1), (1, 7)), ((2, 3, 4, 5, 6, 8), (4, 1, 6, 8))])
+def test_binary_broadcast_shapes(ora, sa, sb):
+    rng = np.random.default_rng(len(sa) * 31 + sb[-1])
+    a = rng.standard_normal(sa).astype(np.float32)
+    b = (rng.standard_normal(sb) + 3).astype(np.float32)
+    for op in range(3):
+        step(f"binary {sa} op {op} {sb}")
+        assert_exact(X.binary(op, dev(a), dev(b)).numpy(), ora.binary(op, a, b), f"{sa} op {op} {sb}")
+        assert_exact(X.binary(op, dev(b), dev(a)).numpy(), ora.binary(op, b, a), f"{sb} op {op} {sa}")
+
+
+def test_binary_arbitrary_strides(ora):
+    """A transposed operand and a column slice: strides the reference expresses with a Transpose / Slice copy."""
+    rng = np.random.default_rng(13)
+    base = rng.standard_normal((64, 48)).astype(np.float32)
+    other = rng.standard_normal((48, 64)).astype(np.float32)
+    d_base, d_other = dev(base), dev(other)
+    y = X.DeviceTensor.empty(F32, (48, 64))
+    bc = X.Broadcast()
+    bc.rank = 2
+    bc.out[0], bc.out[1] = 48, 64
+    bc.stride_a[0], bc.stride_a[1] = 1, 48     # base transposed
+    bc.stride_b[0], bc.stride_b[1] = 64, 1
+    bc.stride_y[0], bc.stride_y[1] = 64, 1
+    step("binary with a transposed operand")
+    X.call("xs_hip_binary", None, X.ADD, F32, C.c_void_p(d_base.ptr), F32, C.c_void_p(d_other.ptr), F32,
+           C.c_void_p(y.ptr), C.byref(bc))
+    assert_exact(y.numpy(), ora.binary(0, np.ascontiguousarray(base.T), other))
+    # y into a column slice of a wider buffer (row stride 96)
+    wide = X.DeviceTensor.from_numpy(np.full((48, 96), 7.0, np.float32))
+    bc.stride_y[0] = 96
+    step("binary into a column slice")
+    X.call("xs_hip_binary", None, X.MUL, F32, C.c_void_p(d_base.ptr), F32, C.c_void_p(d_other.ptr), F32,
+           C.c_void_p(wide.ptr + 32 * 4), C.byref(bc))
+    w = wide.numpy()
+    assert_exact(w[:, 32:96], ora.binary(1, np.ascontiguousarray(base.T), other))
+    assert (w[:, :32] == 7.0).all()
+
+
+def test_fused_residuals(ora):
+    rng = np.random.default_rng(14)
+    a, b = (rng.standard_normal((16, 96)).astype(np.float32) for _ in range(2))
+    c = rng.standard_normal(96).astype(np.float32)
+    da, db, dc = dev(a), dev(b), dev(c)
+    for name, want in (("xs_hip_add_mul", ora.binary(0, a, ora.binary(1, b, c))),
+                       ("xs_hip_add3", ora.binary(0, a, ora.binary(0, b, c)))):
+        step(name)
+        y = X.DeviceTensor.empty(F32, a.shape)
+        X.call(name, None, C.c_void_p(da.ptr), C.c_void_p(db.ptr), C.c_void_p(dc.ptr), F32, C.c_void_p(y.ptr), a.size,
+               96)
+        assert_exact(y.numpy(), want, name)
+
+
+def test_convert(ora):
+    g = golden("half")
+    x = g["x"]
+    step("convert f32 -> f16 / bf16 goldens")
+    num = ~np.isnan(x)
+    h16 = X.convert(dev(x), F16).numpy()
+    assert_exact(h16.view(np.uint16)[num], g["f16"][num], "f16")
+    assert np.isnan(h16[~num]).all()
+    b = X.convert(dev(x), BF16).numpy()
+    assert_exact(b, g["bf16"], "bf16")
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    step("convert f16 -> f32 exhaustive")
+    f = X.convert(dev(h.view(np.float16), F16), F32).numpy()
+    assert_exact(f, ora.widen(h.view(np.float16), F16), "f16 widen")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# RMSNorm
+
+def test_rms_norm_goldens(ora):
+    g = golden("rms_norm")
+    step("rms_norm goldens")
+    assert_f32_close(X.rms_norm(dev(g["x"]), dev(g["w"]), 1e-6).numpy(), g["out_w"], what="weighted")
+    assert_f32_close(X.rms_norm(dev(g["x"]), None, 1e-6).numpy(), g["out_now"], what="unweighted")
+    assert_f32_close(X.rms_norm(dev(g["xb"], BF16), None, 1e-5).numpy(), g["out_bf16_in"], what="bf16 in")
+    y, h = X.add_rms_norm(dev(g["res_x"]), dev(g["res_r"]), dev(g["res_w"]), 1e-6)
+    assert_exact(h.numpy(), g["res_h"], "residual sum")
+    assert_f32_close(y.numpy(), g["res_out"], what="residual norm")
+    assert_f32_close(X.rms_norm(dev(g["odd_x"]), None, 1e-6).numpy(), g["odd_out"], what="odd width")
+
+
+@pytest.mark.parametrize("rows,width", [(1, 16), (5, 48), (7, 100), (3, 2560), (9, 4096), (2, 8192), (4, 32768),
+                                        (2, 40000), (33, 512)])
+@pytest.mark.parametrize("xdt,ydt", [(F32, F32), (BF16, BF16), (F16, F32), (F32, F16)])
+def test_rms_norm_shapes(ora, rows, width, xdt, ydt):
+    rng = np.random.default_rng(rows * width)
+    x = ora.narrow(rng.standard_normal((rows, width)).astype(np.float32) * 3, xdt)
+    w = (1 + 0.1 * rng.standard_normal(width)).astype(np.float32)
+    step(f"rms_norm [{rows}, {width}] {DT[xdt]} -> {DT[ydt]}")
+    y = X.rms_norm(dev(x, xdt), dev(w), 1e-6, ydt).numpy()
+    check_out(y, ora.rms_norm(ora.widen(x, xdt), w, 1e-6), ydt, ora, f"rms_norm {rows}x{width}")
+
+
+def test_add_rms_norm_config0_full(ora):
+    cfg = W.config0()
+    a = cfg.arrays
+    step("add_rms_norm config 0 [512, 2560]")
+    y, h = X.add_rms_norm(dev(a["x"]), dev(a["residual"]), dev(a["weight"]), 1e-6)
+    wy, wh = ora.add_rms_norm(a["x"], a["residual"], a["weight"], 1e-6)
+    assert_exact(h.numpy(), wh, "updated residual")
+    assert_f32_close(y.numpy(), wy, what="normed")
+    # in place: the sum overwrites the residual buffer
+    step("add_rms_norm config 0 in place")
+    r = dev(a["residual"])
+    y2, h2 = X.add_rms_norm(dev(a["x"]), r, dev(a["weight"]), 1e-6, in_place=True)
+    assert h2 is r
+    assert_exact(r.numpy(), wh, "in-place residual")
+    assert_exact(y2.numpy(), y.numpy(), "in-place normed")
+    # property: without weight every row has unit rms (eps small against mean(h^2) ~ 2)
+    y3, _ = X.add_rms_norm(dev(a["x"]), dev(a["residual"]), None, 1e-6)
+    rms = np.sqrt((y3.numpy().astype(np.float64) ** 2).mean(axis=1))
+    assert np.allclose(rms, 1.0, rtol=1e-5)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# softmax
+
+def test_softmax_goldens(ora):
+    g = golden("softmax")
+    step("softmax goldens")
+    assert_f32_close(X.softmax(dev(g["big"])).numpy(), g["big_out"], what="+-40")
+    vl = dev(g["valid"].astype(np.int64), X.I64)
+    assert_f32_close(X.softmax_masked(dev(g["s"]), float(g["scale"]), vl).numpy(), g["s_out"], what="masked")
+    assert_f32_close(X.softmax_masked(dev(g["s2"]), float(g["scale"]), 3000).numpy(), g["s2_out"], what="masked 4096")
+
+
+@pytest.mark.parametrize("rows,width", [(6, 9), (3, 64), (5, 1000), (2, 4096), (4, 32768), (2, 40000), (300, 128)])
+def test_softmax_shapes(ora, rows, width):
+    rng = np.random.default_rng(rows + width)
+    x = (rng.standard_normal((rows, width)) * 5).astype(np.float32)
+    step(f"softmax [{rows}, {width}]")
+    assert_f32_close(X.softmax(dev(x)).numpy(), ora.softmax(x), what=f"softmax {rows}x{width}")
+    valid = rng.integers(1, width + 1, rows).astype(np.int64)
+    step(f"softmax masked [{rows}, {width}]")
+    got = X.softmax_masked(dev(x), 0.125, dev(valid, X.I64)).numpy()
+    assert_f32_close(got, ora.softmax_masked(x, 0.125, valid), what=f"masked {rows}x{width}")
+
+
+def test_softmax_edge_rows(ora):
+    x = np.zeros((3, 64), np.float32)
+    x[1, 5] = np.nan
+    x[2, :] = -np.inf
+    step("softmax edge rows (NaN, all -inf, all masked)")
+    got = X.softmax(dev(x)).numpy()
+    want = ora.softmax(x)
+    assert_f32_close(got, want, what="edge rows")
+    got = X.softmax_masked(dev(np.ones((2, 64), np.float32)), 1.0, 0).numpy()
+    assert np.isnan(got).all()
+
+
+def test_softmax_config2a_full(ora):
+    cfg = W.config2a()
+    s = cfg.arrays["scores"]
+    p = cfg.params
+    step("softmax config 2a [32, 1, 32768] masked at 30000")
+    got = X.softmax_masked(dev(s), p["scale"], p["valid_len"]).numpy()
+    want = ora.softmax_masked(s, p["scale"], p["valid_len"])
+    assert_f32_close(got, want, what="config 2a")
+    assert (got[..., p["valid_len"]:] == 0).all()
+    assert np.allclose(got.astype(np.float64).sum(axis=-1), 1.0, atol=1e-5)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# top-k / argmax
+
+def test_topk_goldens(ora):
+    g = golden("topk")
+    for tag, k in (("t1", 4), ("t2", 32), ("t3", 64)):
+        step(f"topk golden {tag} k {k}")
+        v, i = X.topk(dev(g[f"{tag}_x"]), k)
+        assert_exact(i.numpy(), g[f"{tag}_i"], tag)
+        assert_exact(v.numpy(), g[f"{tag}_v"], tag)
+    step("argmax goldens")
+    v, i = X.topk(dev(g["t3_x"]), 1)
+    assert_exact(i.numpy(), g["a1_i"])
+    assert_exact(v.numpy(), g["a1_v"])
+    v, i = X.topk(dev(g["a2_x"]), 1)
+    assert_exact(i.numpy(), g["a2_i"])
+    assert_exact(v.numpy(), g["a2_v"])  # bits too: +0 at index 1 loses to -0 at index 0
+
+
+def test_argmax_config2b_full(ora):
+    cfg = W.config2b()
+    x = cfg.arrays["logits"]
+    scratch = X.TopkScratch()
+    for rep in range(3):  # the self-resetting arrival counters across calls
+        step(f"argmax config 2b [1, 151936] call {rep}")
+        v, i = X.topk(dev(x), 1, scratch)
+        assert int(i.numpy()[0, 0]) == cfg.params["ties"][0]
+        assert float(v.numpy()[0, 0]) == cfg.params["top"]
+    wv, wi = ora.topk(x, 1)
+    assert_exact(i.numpy(), wi)
+
+
+@pytest.mark.parametrize("rows,width", [(64, 151936), (3, 1025), (7, 4096), (2, 1023), (5, 3)])
+def test_argmax_rows(ora, rows, width):
+    rng = np.random.default_rng(rows * 7 + width)
+    x = rng.integers(-50, 50, (rows, width)).astype(np.float32)  # many ties
+    step(f"argmax [{rows}, {width}]")
+    v, i = X.topk(dev(x), 1)
+    wv, wi = ora.topk(x, 1)
+    assert_exact(i.numpy(), wi)
+    assert_exact(v.numpy(), wv)
+
+
+def test_topk_k_gt_1(ora):
+    rng = np.random.default_rng(15)
+    x = rng.integers(-20, 20, (6, 3000)).astype(np.float32)
+    for k in (2, 8, 50):
+        step(f"topk k {k} [6, 3000]")
+        v, i = X.topk(dev(x), k)
+        wv, wi = ora.topk(x, k)
+        assert_exact(i.numpy(), wi)
+        assert_exact(v.numpy(), wv)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# RoPE
+
+def test_rope_goldens(ora):
+    g = golden("rope")
+    step("rope golden cpu_ops case (i64 positions, zero inv_freq tail)")
+    assert_f32_close(X.rope(dev(g["r1_x"]), dev(g["r1_pos"]), dev(g["r1_f"])).numpy(), g["r1_out"], what="r1")
+    step("rope golden f16 config shape")
+    y = X.rope(dev(g["r2_x"], F16), dev(g["r2_pos"]), dev(g["r2_f"])).numpy()
+    assert_ulp(y, ora.narrow(g["r2_out"], F16), "f16", what="r2")
+    yf = X.rope(dev(g["r2_x"], F16), dev(g["r2_pos"]), dev(g["r2_f"]), y_dtype=F32).numpy()
+    assert_f32_close(yf, g["r2_out"], what="r2 f32 out")
+    step("rope golden axial")
+    assert_f32_close(X.rope(dev(g["r3_x"]), dev(g["r3_pos"]), dev(g["r3_f"])).numpy(), g["r3_out"], what="r3")
+    step("rope golden pair_axes")
+    y = X.rope(dev(g["r4_x"]), dev(g["r4_pos"]), dev(g["r4_f"]), 0, dev(g["r4_axes"])).numpy()
+    assert_f32_close(y, g["r4_out"], what="r4")
+    step("rope golden partial rotary")
+    assert_f32_close(X.rope(dev(g["r5_x"]), dev(g["r5_pos"]), dev(g["r5_f"]), 32).numpy(), g["r5_out"], what="r5")
+
+
+def test_rope_config3_full(ora):
+    cfg = W.config3()
+    a = cfg.arrays
+    pos = dev(a["positions"])
+    f = dev(a["inv_freq"])
+    for name in ("q", "k"):
+        x = a[name]
+        step(f"rope config 3 {name} {x.shape} f16")
+        y = X.rope(dev(x, F16), pos, f).numpy()
+        want = ora.rope(ora.widen(x, F16), a["positions"], a["inv_freq"])
+        n_diff = assert_ulp(y, ora.narrow(want, F16), "f16", what=f"rope {name}")
+        assert n_diff <= y.size * 1e-4
+        step(f"rope config 3 {name} in place")
+        d = dev(x, F16)
+        X.rope(d, pos, f, in_place=True)
+        assert_exact(d.numpy().view(np.uint16), y.view(np.uint16), "in place")
+        # property: each rotated pair keeps its norm (to f16 rounding)
+        if name == "k":
+            xf = x.astype(np.float64)
+            yf = y.astype(np.float64)
+            n0 = xf[..., :64] ** 2 + xf[..., 64:] ** 2
+            n1 = yf[..., :64] ** 2 + yf[..., 64:] ** 2
+            assert np.allclose(n0, n1, rtol=5e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("xdt,ydt", [(F32, F32), (F16, F16), (BF16, BF16), (F32, F16), (BF16, F32)])
+def test_rope_dtypes(ora, xdt, ydt):
+    rng = np.random.default_rng(16)
+    x = ora.narrow(rng.standard_normal((33, 5, 64)).astype(np.float32), xdt)
+    pos = rng.integers(0, 9000, 33).astype(np.int64)
+    f = ora.rope_inv_freq(10000.0, 64, 32, 32)
+    step(f"rope [33, 5, 64] {DT[xdt]} -> {DT[ydt]}")
+    y = X.rope(dev(x, xdt), dev(pos), dev(f), y_dtype=ydt).numpy()
+    check_out(y, ora.rope(ora.widen(x, xdt), pos, f), ydt, ora, "rope dtypes")
+
+
+def test_rope_scalar_path(ora):
+    """A head whose half is no multiple of a vector takes the per-pair kernel."""
+    rng = np.random.default_rng(17)
+    x = rng.standard_normal((9, 3, 20)).astype(np.float32)
+    pos = np.arange(9, dtype=np.int32) * 1000
+    f = ora.rope_inv_freq(10000.0, 20, 10, 10)
+    step("rope [9, 3, 20] scalar path")
+    assert_f32_close(X.rope(dev(x), dev(pos), dev(f)).numpy(), ora.rope(x, pos, f), what="scalar rope")

@@ -1,0 +1,389 @@
+"""Pins the oracle (oracle/oracle.cpp) before anything is checked against it.
+
+Each restated function is checked three ways where the domain allows: bit for bit against the golden vectors the
+reference's own cpu-ref backend wrote (tests/golden/, see gen_golden.py), against the reference's known-answer tests
+(tests/unit/test_half.cpp, moe_ops_cases.h, cpu_ops.cpp), and against what the mathematics fixes (brute force,
+closed forms, invariants) -- chosen so that a dropped term, a wrong index or a transposed operand fails one of them.
+CPU only.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+
+from oracle import BF16, F16, F32, GELU, GELU_TANH, SIGMOID, SILU, oracle, reference
+from tol import assert_exact, assert_f32_close
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def golden(name):
+    return np.load(os.path.join(GOLDEN, name + ".npz"), allow_pickle=False)
+
+
+@pytest.fixture(scope="module")
+def ora():
+    return oracle()
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# half conversions (util/half)
+
+def test_f16_round_trip_exhaustive(ora):
+    """tests/unit/test_half.cpp:9-19: every finite f16 survives f16 -> f32 -> f16; NaN stays NaN."""
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = ora.widen(h.view(np.float16), F16)
+    # the widening is exact: numpy's own IEEE conversion agrees on every pattern
+    assert_exact(f, h.view(np.float16).astype(np.float32), "f16 widen")
+    back = ora.narrow(f, F16).view(np.uint16)
+    nan = np.isnan(f)
+    assert (back[~nan] == h[~nan]).all()
+    assert np.isnan(ora.widen(back[nan].view(np.float16), F16)).all()
+
+
+def test_f16_rounding_kats(ora):
+    """tests/unit/test_half.cpp:21-30."""
+    to, fr = ora.f32_to_f16, ora.f16_to_f32
+    assert fr(to(65504.0)) == 65504.0
+    assert math.isinf(fr(to(65520.0)))
+    assert fr(to(65519.0)) == 65504.0
+    assert to(1.0 + 0.5 / 1024) == to(1.0)
+    assert to(1.0 + 1.5 / 1024) == 0x3C00 + 2
+    assert fr(to(math.ldexp(1.0, -24))) == math.ldexp(1.0, -24)
+    assert to(math.ldexp(1.0, -25)) == 0
+    assert fr(to(math.ldexp(1.5, -25))) == math.ldexp(1.0, -24)
+
+
+def test_f16_narrow_matches_ieee_rne(ora):
+    """numpy's float32 -> float16 is IEEE round-to-nearest-even with overflow to inf: an independent oracle."""
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.standard_normal(100000).astype(np.float32) * s for s in (1e-6, 1e-3, 1.0, 1e3, 7e4)])
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    assert_exact(ora.narrow(x, F16).view(np.uint16), want, "f16 narrow")
+
+
+def test_bf16_kats(ora):
+    """tests/unit/test_half.cpp:33-38."""
+    assert ora.bf16_to_f32(ora.f32_to_bf16(1.0)) == 1.0
+    assert ora.bf16_to_f32(ora.f32_to_bf16(39.191836)) == 39.25
+    assert math.isnan(ora.bf16_to_f32(ora.f32_to_bf16(float("nan"))))
+
+
+def test_bf16_narrow_rounds_to_nearest_even(ora):
+    """Closed form: the nearest bf16 (ties to the even mantissa) of a float is found by comparing the two
+    neighbouring bf16 values in f64."""
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal(50000).astype(np.float32) * 3.0
+    lo = (x.view(np.uint32) & 0xFFFF0000).view(np.float32)  # truncation toward zero
+    hi_bits = (x.view(np.uint32) & 0xFFFF0000) + 0x10000
+    hi = hi_bits.astype(np.uint32).view(np.float32)
+    dlo = np.abs(x.astype(np.float64) - lo)
+    dhi = np.abs(hi.astype(np.float64) - x)
+    lo_even = ((lo.view(np.uint32) >> 16) & 1) == 0
+    pick_lo = (dlo < dhi) | ((dlo == dhi) & lo_even)
+    want = np.where(pick_lo, lo.view(np.uint32) >> 16, hi_bits >> 16).astype(np.uint16)
+    assert_exact(ora.narrow(x, BF16), want, "bf16 narrow")
+
+
+def test_half_goldens(ora):
+    g = golden("half")
+    assert_exact(ora.narrow(g["x"], F16).view(np.uint16), g["f16"], "f16 golden")
+    assert_exact(ora.narrow(g["x"], BF16), g["bf16"], "bf16 golden")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# binary broadcast
+
+def test_binary_brute_force(ora):
+    """The odometer walk against numpy's broadcasting (an independent implementation): f32 add / mul / div are
+    single IEEE operations, so the results must agree bit for bit."""
+    rng = np.random.default_rng(3)
+    for sa, sb in [((4, 6), (4, 6)), ((4, 6), (6,)), ((4, 1, 6), (3, 1)), ((1,), (2, 3)), ((2, 1, 5), (1, 4, 1)),
+                   ((3, 1, 2, 8), (5, 1, 8)), ((7,), (1,)), ((2, 3, 1, 1, 4), (3, 5, 1, 4))]:
+        a = rng.standard_normal(sa).astype(np.float32)
+        b = rng.standard_normal(sb).astype(np.float32) + 3.0
+        with np.errstate(all="ignore"):
+            for op, fn in ((0, np.add), (1, np.multiply), (2, np.divide)):
+                assert_exact(ora.binary(op, a, b), fn(a, b).astype(np.float32), f"{sa} op{op} {sb}")
+
+
+def test_binary_goldens(ora):
+    g = golden("binary")
+    for i in range(8):
+        for op in range(3):
+            assert_exact(ora.binary(op, g[f"c{i}_a"], g[f"c{i}_b"]), g[f"c{i}_op{op}"], f"case {i} op {op}")
+    assert_exact(ora.binary(0, ora.widen(g["h_a"], F16), ora.widen(g["h_b"], F16)), g["h_add"], "f16 add")
+    assert_exact(ora.binary(1, ora.widen(g["b_a"], BF16), ora.widen(g["b_b"], BF16)), g["b_mul"], "bf16 mul")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# activations
+
+def test_activation_closed_forms(ora):
+    x = np.array([0.0, 1.0, -1.0, 30.0, -30.0, 2.0], np.float32)
+    s = ora.unary(SILU, x)
+    assert s[0] == 0.0 and s[3] == 30.0                     # silu(0) = 0; silu(x) = x once exp(-x) vanishes in f32
+    assert abs(s[1] - 1.0 / (1.0 + math.exp(-1.0))) < 1e-7  # silu(1) = sigmoid(1)
+    assert abs(s[1] - s[2] - 1.0) < 1e-7                     # silu(x) - silu(-x) = x
+    sg = ora.unary(SIGMOID, x)
+    assert sg[0] == 0.5 and abs(sg[1] + sg[2] - 1.0) < 1e-7  # sigmoid(-x) = 1 - sigmoid(x)
+    ge = ora.unary(GELU, x)
+    assert ge[0] == 0.0 and abs(ge[1] - 0.8413447460685429) < 1e-7  # Phi(1) = 0.841344746...
+    gt = ora.unary(GELU_TANH, x)
+    assert gt[0] == 0.0 and abs(gt[1] - ge[1]) < 1e-3 and gt[3] == 30.0
+
+
+def test_act_goldens(ora):
+    g = golden("act_mul")
+    for dt, tag in ((F32, "f32"), (F16, "f16"), (BF16, "bf16")):
+        x = ora.widen(g[f"{tag}_gate"], dt)
+        u = ora.widen(g[f"{tag}_up"], dt)
+        bias = ora.widen(g[f"{tag}_bias"], dt)
+        for act in (SILU, GELU_TANH, SIGMOID, GELU):
+            assert_exact(ora.act_bias_mul(act, x, u, bias), g[f"{tag}_act{act}_bias"], f"{tag} act {act} bias")
+            assert_exact(ora.act_bias_mul(act, x, u, None), g[f"{tag}_act{act}_nobias"], f"{tag} act {act}")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# rms_norm
+
+def test_rms_norm_invariants(ora):
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((16, 300)).astype(np.float32) * 5.0
+    y = ora.rms_norm(x, None, 0.0)
+    rms = np.sqrt((y.astype(np.float64) ** 2).mean(axis=1))
+    assert np.allclose(rms, 1.0, rtol=1e-6)                             # unit rms with eps 0
+    assert_f32_close(ora.rms_norm(x * np.float32(4.0), None, 0.0), y)   # scale invariance (4 is exact)
+    w = rng.standard_normal(300).astype(np.float32)
+    assert_f32_close(ora.rms_norm(x, w, 0.0), y * w)                    # the weight multiplies per column
+    # eps enters under the root: a constant row c gives c / sqrt(c^2 + eps)
+    c = np.full((1, 64), 0.01, np.float32)
+    assert abs(ora.rms_norm(c, None, 1e-4)[0, 0] - 0.01 / math.sqrt(1e-4 + 1e-4)) < 1e-6
+
+
+def test_rms_norm_goldens(ora):
+    g = golden("rms_norm")
+    assert_exact(ora.rms_norm(g["x"], g["w"], 1e-6), g["out_w"], "weighted")
+    assert_exact(ora.rms_norm(g["x"], None, 1e-6), g["out_now"], "unweighted")
+    assert_exact(ora.rms_norm(ora.widen(g["xb"], BF16), None, 1e-5), g["out_bf16_in"], "bf16 input")
+    y, h = ora.add_rms_norm(g["res_x"], g["res_r"], g["res_w"], 1e-6)
+    assert_exact(h, g["res_h"], "residual sum")
+    assert_exact(y, g["res_out"], "residual norm")
+    assert_exact(ora.rms_norm(g["odd_x"], None, 1e-6), g["odd_out"], "odd width")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# softmax
+
+def test_softmax_against_f64(ora):
+    """moe_ops_cases.h:44-73: +-40 inputs against an f64 evaluation; rows sum to 1; shift invariance."""
+    rng = np.random.default_rng(5)
+    x = (rng.uniform(-1, 1, (6, 9)) * 40).astype(np.float32)
+    y = ora.softmax(x)
+    e = np.exp(x.astype(np.float64) - x.max(axis=1, keepdims=True))
+    assert_f32_close(y, (e / e.sum(axis=1, keepdims=True)).astype(np.float32), 1e-6)
+    assert np.allclose(y.astype(np.float64).sum(axis=1), 1.0, atol=1e-6)
+    assert_f32_close(ora.softmax(x + np.float32(8.0)), y, 1e-5)
+
+
+def test_softmax_masked(ora):
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((3, 100)).astype(np.float32) * 3
+    y = ora.softmax_masked(x, 0.125, np.array([100, 37, 1]))
+    assert (y[1, 37:] == 0).all() and (y[2, 1:] == 0).all() and y[2, 0] == 1.0
+    assert_f32_close(y[1, :37], ora.softmax(x[1:2, :37] * np.float32(0.125))[0])
+    assert np.isnan(ora.softmax_masked(x[:1], 0.125, 0)).all()  # every key masked: exp(-inf - -inf) is NaN
+
+
+def test_softmax_goldens(ora):
+    g = golden("softmax")
+    assert_exact(ora.softmax(g["big"]), g["big_out"], "+-40")
+    assert_exact(ora.softmax_masked(g["s"], float(g["scale"]), g["valid"]), g["s_out"], "masked")
+    assert_exact(ora.softmax_masked(g["s2"], float(g["scale"]), 3000), g["s2_out"], "masked 4096")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# top-k
+
+def test_topk_kats(ora):
+    """The tie KATs of moe_ops_cases.h:76-122."""
+    rng = np.random.default_rng(32)
+    x = rng.uniform(-1, 1, (5, 16)).astype(np.float32)
+    x[0, 3] = x[0, 11] = 2.0
+    v, i = ora.topk(x, 4)
+    assert i[0, 0] == 3 and i[0, 1] == 11 and v[0, 0] == 2.0
+    wide = rng.uniform(-1, 1, (2, 2048)).astype(np.float32)
+    wide[0, [100, 1900, 700]] = 3.0
+    _, i = ora.topk(wide, 32)
+    assert list(i[0, :3]) == [100, 700, 1900]
+    huge = rng.uniform(-1, 1, (2, 40000)).astype(np.float32)
+    huge[0, [5, 6, 300, 39999, 20000]] = 4.0
+    _, i = ora.topk(huge, 64)
+    assert list(i[0, :5]) == [5, 6, 300, 20000, 39999]
+
+
+def test_topk_brute_force(ora):
+    """A stable sort on (-value, index) is the same order."""
+    rng = np.random.default_rng(7)
+    x = rng.integers(-5, 5, (4, 300)).astype(np.float32)  # many ties
+    v, i = ora.topk(x, 17)
+    for r in range(4):
+        order = np.lexsort((np.arange(300), -x[r]))[:17]
+        assert list(i[r]) == list(order)
+        assert_exact(v[r], x[r, order])
+
+
+def test_topk_goldens(ora):
+    g = golden("topk")
+    for tag, k in (("t1", 4), ("t2", 32), ("t3", 64)):
+        v, i = ora.topk(g[f"{tag}_x"], k)
+        assert_exact(i, g[f"{tag}_i"], tag)
+        assert_exact(v, g[f"{tag}_v"], tag)
+    v, i = ora.topk(g["t3_x"], 1)
+    assert_exact(i, g["a1_i"])
+    v, i = ora.topk(g["a2_x"], 1)
+    assert_exact(i, g["a2_i"])
+    assert_exact(v, g["a2_v"])
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# RoPE
+
+def test_rope_identities(ora):
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((5, 3, 16)).astype(np.float32)
+    f = ora.rope_inv_freq(10000.0, 16, 8, 8)
+    f[5:] = 0.0
+    y = ora.rope(x, np.array([0, 7, 100, 4095, 12], np.int64), f)
+    assert_exact(y[0], x[0], "position 0 is the identity")
+    assert_exact(y[:, :, [5, 6, 7, 13, 14, 15]], x[:, :, [5, 6, 7, 13, 14, 15]], "inv_freq 0 is the identity")
+    n_in = x[..., :8].astype(np.float64) ** 2 + x[..., 8:].astype(np.float64) ** 2
+    n_out = y[..., :8].astype(np.float64) ** 2 + y[..., 8:].astype(np.float64) ** 2
+    assert np.allclose(n_in, n_out, rtol=1e-6)  # each (c, c + D/2) pair keeps its norm
+    # rotations compose: rotating by a then by b is rotating by a + b
+    a = ora.rope(x, np.full(5, 3, np.int32), f)
+    ab = ora.rope(a, np.full(5, 4, np.int32), f)
+    assert_f32_close(ab, ora.rope(x, np.full(5, 7, np.int32), f), 1e-5)
+    # angle = pos * inv_freq: pair 1 at position 1 is cos/sin of inv_freq[1]
+    c, s = math.cos(float(f[1])), math.sin(float(f[1]))
+    assert abs(y[1, 0, 1] - 0) >= 0  # shape check of indexing below
+    p1 = ora.rope(x[:1], np.array([1], np.int32), f)
+    assert abs(p1[0, 0, 1] - (x[0, 0, 1] * c - x[0, 0, 9] * s)) < 1e-6
+    assert abs(p1[0, 0, 9] - (x[0, 0, 9] * c + x[0, 0, 1] * s)) < 1e-6
+
+
+def test_rope_planted_interleaved_bug(ora):
+    """cpu_ops.cpp:246-250: an interleaved-layout (GPT-J) rotation must not match the half-split one."""
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((4, 3, 16)).astype(np.float32)
+    f = ora.rope_inv_freq(10000.0, 16, 8, 8)
+    pos = np.array([7, 100, 4095, 12], np.int64)
+    y = ora.rope(x, pos, f)
+    ang = pos[:, None].astype(np.float64) * f[None, :].astype(np.float64)
+    c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    wrong = x.astype(np.float64).copy()
+    wrong[..., 0::2] = x[..., 0::2] * c - x[..., 1::2] * s
+    wrong[..., 1::2] = x[..., 1::2] * c + x[..., 0::2] * s
+    assert not np.allclose(y, wrong, rtol=1e-5, atol=1e-5)
+    right = x.astype(np.float64).copy()
+    right[..., :8] = x[..., :8] * c - x[..., 8:] * s
+    right[..., 8:] = x[..., 8:] * c + x[..., :8] * s
+    assert np.allclose(y, right, rtol=1e-6, atol=1e-6)
+
+
+def test_rope_goldens(ora):
+    g = golden("rope")
+    assert_exact(ora.rope(g["r1_x"], g["r1_pos"], g["r1_f"]), g["r1_out"], "cpu_ops case")
+    assert_exact(ora.rope(ora.widen(g["r2_x"], F16), g["r2_pos"], g["r2_f"]), g["r2_out"], "f16 config shape")
+    assert_exact(ora.rope(g["r3_x"], g["r3_pos"], g["r3_f"]), g["r3_out"], "axial")
+    assert_exact(ora.rope(g["r4_x"], g["r4_pos"], g["r4_f"], 0, g["r4_axes"]), g["r4_out"], "pair_axes")
+    assert_exact(ora.rope(g["r5_x"], g["r5_pos"], g["r5_f"], 32), g["r5_out"], "partial rotary")
+    for j in range(4):
+        theta, dim, pairs, length = g[f"inv{j}_args"]
+        assert_exact(ora.rope_inv_freq(theta, int(dim), int(pairs), int(length)), g[f"inv{j}"], f"inv_freq {j}")
+
+
+def test_rope_inv_freq_closed_form(ora):
+    f = ora.rope_inv_freq(10000.0, 8, 4, 6)
+    assert list(f) == [1.0, np.float32(0.1), np.float32(0.01), np.float32(0.001), 0.0, 0.0]
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# int8 KV
+
+def test_quantize_invariants(ora):
+    rng = np.random.default_rng(10)
+    x = rng.standard_normal((200, 128)).astype(np.float32)
+    x[:, 7] *= 10
+    codes, scales = ora.quantize_kv(x)
+    assert (np.abs(codes.astype(np.int32)) <= 127).all()
+    amax = np.abs(x).max(axis=1)
+    assert_exact(scales, (amax / np.float32(127.0)).astype(np.float32))
+    # the largest magnitude of a row maps to +-127
+    assert (np.abs(codes[np.arange(200), np.abs(x).argmax(axis=1)]) == 127).all()
+    back = ora.dequantize_kv(codes, scales)
+    assert (np.abs(back - x) <= scales[:, None] * 0.5 * (1 + 1e-5) + 1e-30).all()
+    z_codes, z_scales = ora.quantize_kv(np.zeros((2, 16), np.float32))
+    assert (z_codes == 0).all() and (z_scales == 0).all()
+
+
+def test_quantize_rounds_half_to_even(ora):
+    """amax = 127 makes inv exactly 1: codes are rint(x), ties to even."""
+    x = np.zeros((1, 16), np.float32)
+    x[0, :7] = [127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5]
+    codes, scales = ora.quantize_kv(x)
+    assert list(codes[0, :7]) == [127, 0, 2, 2, 0, -2, -2]
+    assert scales[0] == 1.0
+
+
+def test_kv_goldens(ora):
+    g = golden("kv_i8")
+    codes, scales = ora.quantize_kv(g["x"])
+    assert_exact(codes, g["codes"], "codes")
+    assert_exact(scales, g["scales"], "scales")
+    finite = np.where(np.isfinite(g["x"]), g["x"], 0.0).astype(np.float32)
+    c2, s2 = ora.quantize_kv(finite)
+    assert_exact(ora.dequantize_kv(c2, s2), g["round_trip"], "round trip")
+    for t in ("k16", "v16"):
+        x = ora.widen(g[t], F16).reshape(-1, 128)
+        c, s = ora.quantize_kv(x)
+        assert_exact(ora.dequantize_kv(c, s).reshape(g[t].shape), g[f"{t}_rt"], f"{t} KvCache append")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Cross-check with the compiled reference on larger random inputs (only where the reference tree was built here).
+
+@pytest.mark.skipif(reference() is None, reason="oracle/_ref not built (no reference tree on this host)")
+def test_oracle_matches_compiled_reference(ora):
+    ref = reference()
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((64, 1024)) * 3).astype(np.float32)
+    r = rng.standard_normal((64, 1024)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(1024)).astype(np.float32)
+    assert_exact(ora.rms_norm(x, w, 1e-6), ref.rms_norm(x, w, 1e-6))
+    y, h = ora.add_rms_norm(x, r, w, 1e-6)
+    ry, rh = ref.add_rms_norm(x, r, w, 1e-6)
+    assert_exact(y, ry)
+    assert_exact(h, rh)
+    assert_exact(ora.softmax_masked(x, 0.0883883461356163, 1000), ref.softmax_masked(x, 0.0883883461356163, 1000))
+    v, i = ora.topk(x, 5)
+    rv, ri = ref.topk(x, 5)
+    assert_exact(i, ri)
+    assert_exact(v, rv)
+    gb = ora.narrow(x, BF16)
+    ub = ora.narrow(r, BF16)
+    bb = ora.narrow(w[:1024] - 1, BF16)
+    want = ref.act_bias_mul(SILU, gb, ub, bb, BF16)
+    got = ora.act_bias_mul(SILU, ora.widen(gb, BF16), ora.widen(ub, BF16), ora.widen(bb, BF16))
+    assert_exact(got, want)
+    q = ora.narrow(rng.standard_normal((64, 8, 128)).astype(np.float32), F16)
+    pos = np.arange(64, dtype=np.int32) * 127
+    f = ora.rope_inv_freq(1e6, 128, 64, 64)
+    assert_exact(ora.rope(ora.widen(q, F16), pos, f), ref.rope(q, pos, f, x_dtype=F16))
+    kv = (rng.standard_normal((512, 128)) * 2).astype(np.float32)
+    c, s = ora.quantize_kv(kv)
+    rc, rs = ref.quantize_kv(kv)
+    assert_exact(c, rc)
+    assert_exact(s, rs)

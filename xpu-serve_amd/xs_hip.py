@@ -1,0 +1,395 @@
+"""Python host side of the gfx950 elementwise / broadcast / reduction kernels.
+
+Two layers over the C ABI of ``include/xs_hip.h`` (``libxs_hip.so``, loaded with ctypes):
+
+* ``lib()`` -- the raw entry points with their C signatures (the ctypes binding a maintainer of the reference's host
+  code would call; every call's status is checked and turned into ``XsError``).
+* Op functions named after the reference CPU path (``cpu_ref::add``, ``mul``, ``silu``, ``rms_norm``, ``softmax``,
+  ``topk``, ``rope``; ``quant::quantize_kv_row_i8`` / ``round_trip_kv_i8``; reference
+  ``src/backend/cpu_ref/ops.h:16-76``, ``src/quant/quant.h:81-85``) over ``DeviceTensor``: a device buffer with a
+  dtype and a row-major shape. Like cpu-ref's functions they return freshly allocated outputs and raise on misuse;
+  unlike cpu-ref they run on the GPU and leave outputs on the device.
+
+There is no CPU fallback: if the shared library is missing, importing works but the first call raises ``XsError``
+naming the missing file, so a GPU run can never silently compute on the host.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+from typing import Optional, Sequence, Tuple
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libxs_hip.so")
+
+# The reference's DType values (src/tensor/dtype.h:17).
+F32, F16, BF16, I64, I32, I8, U8, BOOL = 0, 1, 2, 3, 4, 5, 6, 7
+DTYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", I64: "i64", I32: "i32", I8: "i8", U8: "u8", BOOL: "bool"}
+DTYPE_SIZE = {F32: 4, F16: 2, BF16: 2, I64: 8, I32: 4, I8: 1, U8: 1, BOOL: 1}
+# numpy storage of each dtype (bf16 is held as its uint16 bit pattern).
+NP_STORAGE = {F32: np.float32, F16: np.float16, BF16: np.uint16, I64: np.int64, I32: np.int32, I8: np.int8,
+              U8: np.uint8, BOOL: np.bool_}
+
+# xs::sycl_be::UnaryOp / BinaryOp and quant::KvFormat values.
+SCALE, TANH, GELU_TANH, SOFTCAP, SIGMOID, SILU, SOFTPLUS, CLAMP, GELU = range(9)
+ADD, MUL, DIV = 0, 1, 2
+KV_FLOAT, KV_I8, KV_TURBO4, KV_TURBO3, KV_TURBO2 = range(5)
+MAX_RANK = 6
+
+
+class XsError(RuntimeError):
+    """The device's diagnosis of a refused or failed call (the reference throws xs::Error, src/util/error.h:12-35)."""
+
+
+class Broadcast(C.Structure):
+    _fields_ = [("rank", C.c_int32), ("out", C.c_int64 * MAX_RANK), ("stride_a", C.c_int64 * MAX_RANK),
+                ("stride_b", C.c_int64 * MAX_RANK), ("stride_y", C.c_int64 * MAX_RANK)]
+
+
+_P = C.c_void_p
+_I64 = C.c_int64
+_I32 = C.c_int32
+_INT = C.c_int
+_F = C.c_float
+
+# name -> argtypes; every function returns int status except where noted.
+_SIGS = {
+    "xs_hip_abi_version": [],
+    "xs_hip_broadcast_fill": [C.POINTER(Broadcast), C.POINTER(_I64), _I32, C.POINTER(_I64), _I32],
+    "xs_hip_device_count": [C.POINTER(_INT)],
+    "xs_hip_device_info": [_INT, C.c_char_p, C.c_size_t, C.POINTER(C.c_uint64), C.POINTER(_INT)],
+    "xs_hip_set_device": [_INT],
+    "xs_hip_malloc": [C.POINTER(_P), C.c_size_t],
+    "xs_hip_free": [_P],
+    "xs_hip_memset": [_P, _INT, C.c_size_t, _P],
+    "xs_hip_memcpy_h2d": [_P, _P, C.c_size_t, _P],
+    "xs_hip_memcpy_d2h": [_P, _P, C.c_size_t, _P],
+    "xs_hip_memcpy_d2d": [_P, _P, C.c_size_t, _P],
+    "xs_hip_stream_create": [C.POINTER(_P)],
+    "xs_hip_stream_destroy": [_P],
+    "xs_hip_stream_synchronize": [_P],
+    "xs_hip_device_synchronize": [],
+    "xs_hip_event_create": [C.POINTER(_P)],
+    "xs_hip_event_destroy": [_P],
+    "xs_hip_event_record": [_P, _P],
+    "xs_hip_event_elapsed_ms": [C.POINTER(_F), _P, _P],
+    "xs_hip_stream_begin_capture": [_P],
+    "xs_hip_stream_end_capture": [_P, C.POINTER(_P)],
+    "xs_hip_graph_launch": [_P, _P],
+    "xs_hip_graph_destroy": [_P],
+    "xs_hip_binary": [_P, _INT, _INT, _P, _INT, _P, _INT, _P, C.POINTER(Broadcast)],
+    "xs_hip_binary_same": [_P, _INT, _INT, _P, _P, _INT, _P, _I64],
+    "xs_hip_binary_period": [_P, _INT, _INT, _P, _P, _INT, _P, _I64, _I64],
+    "xs_hip_add_mul": [_P, _P, _P, _P, _INT, _P, _I64, _I64],
+    "xs_hip_add3": [_P, _P, _P, _P, _INT, _P, _I64, _I64],
+    "xs_hip_act_mul": [_P, _INT, _INT, _P, _P, _INT, _P, _I64],
+    "xs_hip_unary_bias": [_P, _INT, _P, _P, _INT, _P, _I64, _I64],
+    "xs_hip_act_bias_mul_2d": [_P, _INT, _INT, _P, _I64, _P, _I64, _P, _INT, _P, _I64, _I64, _I64],
+    "xs_hip_convert": [_P, _INT, _P, _INT, _P, _I64],
+    "xs_hip_rms_norm": [_P, _INT, _P, _P, _P, _INT, _P, _I64, _I64, _F],
+    "xs_hip_add_rms_norm": [_P, _P, _P, _P, _P, _P, _INT, _P, _I64, _I64, _F],
+    "xs_hip_softmax": [_P, _P, _P, _I64, _I64],
+    "xs_hip_softmax_masked": [_P, _P, _P, _I64, _I64, _I64, _F, _P, _I64],
+    "xs_hip_topk_scratch": [_I64, _I64, _I64],
+    "xs_hip_topk": [_P, _P, _P, _P, _I64, _I64, _I64, _P],
+    "xs_hip_rope": [_P, _INT, _P, _INT, _P, _P, _INT, _P, _I64, _I64, _I64, _I64, _I64, _P],
+    "xs_hip_quantize_kv": [_P, _INT, _INT, _P, _P, _P, _I64, _I64],
+    "xs_hip_dequantize_kv": [_P, _INT, _P, _P, _INT, _P, _I64, _I64],
+    "xs_hip_copy": [_P, _P, _P, C.c_size_t],
+}
+_RESTYPES = {"xs_hip_topk_scratch": C.c_size_t, "xs_hip_last_error": C.c_char_p}
+
+_lib_handle = None
+
+
+def lib():
+    """The loaded C ABI; raises XsError when libxs_hip.so has not been built."""
+    global _lib_handle
+    if _lib_handle is None:
+        if not os.path.exists(LIB_PATH):
+            raise XsError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() (or make -C xpu-serve_amd)")
+        h = C.CDLL(LIB_PATH)
+        for name, args in _SIGS.items():
+            f = getattr(h, name)
+            f.argtypes = args
+            f.restype = _RESTYPES.get(name, C.c_int)
+        h.xs_hip_last_error.argtypes = []
+        h.xs_hip_last_error.restype = C.c_char_p
+        _lib_handle = h
+    return _lib_handle
+
+
+def check(status: int, what: str = "") -> None:
+    if status != 0:
+        msg = lib().xs_hip_last_error().decode(errors="replace")
+        raise XsError(msg or f"{what}: status {status}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Device memory
+
+class DeviceBuffer:
+    """An owned device allocation (the session's DeviceBuffer, reference sycl_backend.cpp:64-107)."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        call("xs_hip_malloc", C.byref(p), C.c_size_t(max(self.nbytes, 0)))
+        self.ptr = p.value or 0
+
+    def free(self) -> None:
+        if self.ptr:
+            lib().xs_hip_free(C.c_void_p(self.ptr))
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+@dataclass
+class DeviceTensor:
+    """A dense row-major tensor in device memory: dtype (reference DType value), shape, and its buffer."""
+    buf: DeviceBuffer
+    dtype: int
+    shape: Tuple[int, ...]
+    offset: int = 0  # bytes into buf
+
+    @property
+    def ptr(self) -> int:
+        return self.buf.ptr + self.offset
+
+    @property
+    def numel(self) -> int:
+        return int(np.prod(self.shape, dtype=np.int64)) if self.shape else 1
+
+    @property
+    def nbytes(self) -> int:
+        return self.numel * DTYPE_SIZE[self.dtype]
+
+    @staticmethod
+    def empty(dtype: int, shape: Sequence[int]) -> "DeviceTensor":
+        shape = tuple(int(s) for s in shape)
+        n = int(np.prod(shape, dtype=np.int64)) if shape else 1
+        return DeviceTensor(DeviceBuffer(max(n * DTYPE_SIZE[dtype], 1)), dtype, shape)
+
+    @staticmethod
+    def from_numpy(a: np.ndarray, dtype: Optional[int] = None) -> "DeviceTensor":
+        """Uploads a; dtype defaults from a's numpy dtype (pass BF16 for uint16 bf16 bit patterns)."""
+        if dtype is None:
+            dtype = {np.dtype(np.float32): F32, np.dtype(np.float16): F16, np.dtype(np.int64): I64,
+                     np.dtype(np.int32): I32, np.dtype(np.int8): I8, np.dtype(np.uint8): U8}[a.dtype]
+        a = np.ascontiguousarray(a, dtype=NP_STORAGE[dtype])
+        t = DeviceTensor.empty(dtype, a.shape)
+        if a.nbytes:
+            call("xs_hip_memcpy_h2d", C.c_void_p(t.ptr), a.ctypes.data_as(C.c_void_p), C.c_size_t(a.nbytes), None)
+        return t
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, dtype=NP_STORAGE[self.dtype])
+        if out.nbytes:
+            call("xs_hip_memcpy_d2h", out.ctypes.data_as(C.c_void_p), C.c_void_p(self.ptr), C.c_size_t(out.nbytes), None)
+        return out
+
+
+def synchronize() -> None:
+    call("xs_hip_device_synchronize")
+
+
+def device_name(device: int = 0) -> str:
+    name = C.create_string_buffer(256)
+    mem = C.c_uint64()
+    cus = C.c_int()
+    call("xs_hip_device_info", device, name, 256, C.byref(mem), C.byref(cus))
+    return name.value.decode()
+
+
+def device_count() -> int:
+    n = C.c_int()
+    call("xs_hip_device_count", C.byref(n))
+    return n.value
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Ops named after the reference CPU path. `stream` is a hipStream_t value (None: the null stream).
+
+def broadcast_desc(a_shape: Sequence[int], b_shape: Sequence[int]) -> Broadcast:
+    bc = Broadcast()
+    A = (C.c_int64 * max(len(a_shape), 1))(*a_shape)
+    B = (C.c_int64 * max(len(b_shape), 1))(*b_shape)
+    call("xs_hip_broadcast_fill", C.byref(bc), A, len(a_shape), B, len(b_shape))
+    return bc
+
+
+def binary(op: int, a: DeviceTensor, b: DeviceTensor, y_dtype: int = F32, stream=None) -> DeviceTensor:
+    """numpy-broadcast a op b (cpu_ref::add / mul / div, ops.cpp:68-93, 201-207); output f32 unless y_dtype."""
+    bc = broadcast_desc(a.shape, b.shape)
+    y = DeviceTensor.empty(y_dtype, tuple(bc.out[i] for i in range(bc.rank)))
+    call("xs_hip_binary", stream, op, a.dtype, C.c_void_p(a.ptr), b.dtype, C.c_void_p(b.ptr), y_dtype,
+         C.c_void_p(y.ptr), C.byref(bc))
+    return y
+
+
+def add(a, b, y_dtype=F32, stream=None):
+    return binary(ADD, a, b, y_dtype, stream)
+
+
+def mul(a, b, y_dtype=F32, stream=None):
+    return binary(MUL, a, b, y_dtype, stream)
+
+
+def div(a, b, y_dtype=F32, stream=None):
+    return binary(DIV, a, b, y_dtype, stream)
+
+
+def act_mul(act: int, x: DeviceTensor, b: DeviceTensor, y_dtype: Optional[int] = None, stream=None) -> DeviceTensor:
+    """y = act(x) * b, same shapes (sycl_be::act_mul; cpu-ref Silu then Mul)."""
+    if x.shape != b.shape or x.dtype != b.dtype:
+        raise XsError(f"act_mul: x {x.shape} {DTYPE_NAMES[x.dtype]} and b {b.shape} {DTYPE_NAMES[b.dtype]} differ")
+    y = DeviceTensor.empty(x.dtype if y_dtype is None else y_dtype, x.shape)
+    call("xs_hip_act_mul", stream, act, x.dtype, C.c_void_p(x.ptr), C.c_void_p(b.ptr), y.dtype, C.c_void_p(y.ptr),
+         x.numel)
+    return y
+
+
+def swiglu(gate: DeviceTensor, up: DeviceTensor, bias: Optional[DeviceTensor] = None,
+           y_dtype: Optional[int] = None, act: int = SILU, stream=None) -> DeviceTensor:
+    """y = act(gate + bias) * up over [rows, cols] (gated_mlp, reference src/models/common/blocks.cpp:23-27)."""
+    if gate.shape != up.shape or len(gate.shape) != 2:
+        raise XsError(f"swiglu: gate {gate.shape} and up {up.shape} must be the same 2-D shape")
+    rows, cols = gate.shape
+    y = DeviceTensor.empty(gate.dtype if y_dtype is None else y_dtype, gate.shape)
+    call("xs_hip_act_bias_mul_2d", stream, act, gate.dtype, C.c_void_p(gate.ptr), cols, C.c_void_p(up.ptr), cols,
+         C.c_void_p(bias.ptr if bias is not None else 0), y.dtype, C.c_void_p(y.ptr), cols, rows, cols)
+    return y
+
+
+def rms_norm(x: DeviceTensor, weight: Optional[DeviceTensor], eps: float, y_dtype: int = F32,
+             stream=None) -> DeviceTensor:
+    """cpu_ref::rms_norm (ops.cpp:260-281) over the last dim; weight f32 [width] or None."""
+    width = x.shape[-1]
+    rows = x.numel // width
+    y = DeviceTensor.empty(y_dtype, x.shape)
+    call("xs_hip_rms_norm", stream, x.dtype, C.c_void_p(x.ptr), C.c_void_p(weight.ptr if weight else 0), None,
+         y_dtype, C.c_void_p(y.ptr), rows, width, C.c_float(eps))
+    return y
+
+
+def add_rms_norm(x: DeviceTensor, residual: DeviceTensor, weight: Optional[DeviceTensor], eps: float,
+                 y_dtype: int = F32, in_place: bool = False, stream=None) -> Tuple[DeviceTensor, DeviceTensor]:
+    """(rms_norm(x + residual) * weight, x + residual); with in_place the sum overwrites residual."""
+    width = x.shape[-1]
+    rows = x.numel // width
+    h = residual if in_place else DeviceTensor.empty(F32, x.shape)
+    y = DeviceTensor.empty(y_dtype, x.shape)
+    call("xs_hip_add_rms_norm", stream, C.c_void_p(x.ptr), C.c_void_p(residual.ptr),
+         C.c_void_p(weight.ptr if weight else 0), None, C.c_void_p(h.ptr), y_dtype, C.c_void_p(y.ptr), rows, width,
+         C.c_float(eps))
+    return y, h
+
+
+def softmax(x: DeviceTensor, stream=None) -> DeviceTensor:
+    """cpu_ref::softmax (ops.cpp:644-661) over the last dim, f32."""
+    width = x.shape[-1]
+    y = DeviceTensor.empty(F32, x.shape)
+    call("xs_hip_softmax", stream, C.c_void_p(x.ptr), C.c_void_p(y.ptr), x.numel // width, width)
+    return y
+
+
+def softmax_masked(x: DeviceTensor, scale: float, valid_len, stream=None) -> DeviceTensor:
+    """softmax(x * scale) with keys >= valid_len masked to -inf (exactly 0 out); valid_len an int for every row or
+    a DeviceTensor of i64 per row."""
+    width = x.shape[-1]
+    rows = x.numel // width
+    y = DeviceTensor.empty(F32, x.shape)
+    if isinstance(valid_len, DeviceTensor):
+        call("xs_hip_softmax_masked", stream, C.c_void_p(x.ptr), C.c_void_p(y.ptr), rows, width, width,
+             C.c_float(scale), C.c_void_p(valid_len.ptr), 0)
+    else:
+        call("xs_hip_softmax_masked", stream, C.c_void_p(x.ptr), C.c_void_p(y.ptr), rows, width, width,
+             C.c_float(scale), None, int(valid_len))
+    return y
+
+
+class TopkScratch:
+    """Zero-filled scratch for xs_hip_topk, grown on demand (sycl_backend.cpp:286-292 keeps one per session)."""
+
+    def __init__(self):
+        self.buf: Optional[DeviceBuffer] = None
+
+    def get(self, rows: int, width: int, k: int) -> int:
+        need = lib().xs_hip_topk_scratch(rows, width, k)
+        if need == 0:
+            return 0
+        if self.buf is None or self.buf.nbytes < need:
+            self.buf = DeviceBuffer(need)
+            call("xs_hip_memset", C.c_void_p(self.buf.ptr), 0, C.c_size_t(need), None)
+        return self.buf.ptr
+
+
+_default_scratch = TopkScratch()
+
+
+def topk(x: DeviceTensor, k: int, scratch: Optional[TopkScratch] = None,
+         stream=None) -> Tuple[DeviceTensor, DeviceTensor]:
+    """cpu_ref::topk (ops.cpp:663-684): (values f32, indices i32) [..., k], ties to the lower index."""
+    width = x.shape[-1]
+    rows = x.numel // width
+    shape = tuple(x.shape[:-1]) + (k,)
+    values = DeviceTensor.empty(F32, shape)
+    indices = DeviceTensor.empty(I32, shape)
+    s = (scratch or _default_scratch).get(rows, width, k)
+    call("xs_hip_topk", stream, C.c_void_p(x.ptr), C.c_void_p(values.ptr), C.c_void_p(indices.ptr), rows, width, k,
+         C.c_void_p(s))
+    return values, indices
+
+
+def rope(x: DeviceTensor, positions: DeviceTensor, inv_freq: DeviceTensor, rotary_dim: int = 0,
+         pair_axes: Optional[DeviceTensor] = None, y_dtype: Optional[int] = None, in_place: bool = False,
+         stream=None) -> DeviceTensor:
+    """cpu_ref::rope (ops.cpp:343-399) of x [T, H, D]; positions [T] or [T, S] (i32/i64)."""
+    tokens, heads, dim = x.shape
+    sections = 1 if len(positions.shape) == 1 else positions.shape[1]
+    if pair_axes is None and len(positions.shape) == 2:
+        sections = positions.shape[1]
+    y = x if in_place else DeviceTensor.empty(x.dtype if y_dtype is None else y_dtype, x.shape)
+    call("xs_hip_rope", stream, x.dtype, C.c_void_p(x.ptr), positions.dtype, C.c_void_p(positions.ptr),
+         C.c_void_p(inv_freq.ptr), y.dtype, C.c_void_p(y.ptr), tokens, heads, dim, rotary_dim, sections,
+         C.c_void_p(pair_axes.ptr if pair_axes is not None else 0))
+    return y
+
+
+def quantize_kv(x: DeviceTensor, stream=None) -> Tuple[DeviceTensor, DeviceTensor]:
+    """Per-row int8 codes [rows, width] and f32 scales [rows] of x [..., width] (quant::quantize_kv_row_i8)."""
+    width = x.shape[-1]
+    rows = x.numel // width
+    codes = DeviceTensor.empty(I8, (rows, width))
+    scales = DeviceTensor.empty(F32, (rows,))
+    call("xs_hip_quantize_kv", stream, KV_I8, x.dtype, C.c_void_p(x.ptr), C.c_void_p(codes.ptr),
+         C.c_void_p(scales.ptr), rows, width)
+    return codes, scales
+
+
+def dequantize_kv(codes: DeviceTensor, scales: DeviceTensor, out_dtype: int = F16, stream=None) -> DeviceTensor:
+    """fl32(code * scale) per row, rounded to out_dtype (quant::round_trip_kv_i8, quant.cpp:269-277)."""
+    rows, width = codes.shape
+    out = DeviceTensor.empty(out_dtype, (rows, width))
+    call("xs_hip_dequantize_kv", stream, KV_I8, C.c_void_p(codes.ptr), C.c_void_p(scales.ptr), out_dtype,
+         C.c_void_p(out.ptr), rows, width)
+    return out
+
+
+def convert(x: DeviceTensor, y_dtype: int, stream=None) -> DeviceTensor:
+    """x rounded to y_dtype (RNE; util/half.h:19-25, half.cpp:36-56)."""
+    y = DeviceTensor.empty(y_dtype, x.shape)
+    call("xs_hip_convert", stream, x.dtype, C.c_void_p(x.ptr), y_dtype, C.c_void_p(y.ptr), x.numel)
+    return y
