@@ -193,6 +193,8 @@ def op_softmax():
     heads, _, keys = c.arrays["scores"].shape
     s0 = X.DeviceTensor.from_numpy(c.arrays["scores"])
     scale, valid = c.params["scale"], c.params["valid_len"]
+    scratch = X.Scratch()  # one zero-filled scratch: the calls run one after another on one stream
+    sp = scratch.ptr(X.lib().xs_hip_softmax_scratch(heads, keys))
 
     def mk():
         s = (dcopy(s0), X.DeviceTensor.empty(X.F32, (heads, keys)))
@@ -202,8 +204,9 @@ def op_softmax():
 
     def go(s, stream):
         x, y = s
-        X.call("xs_hip_softmax_masked", stream, vp(x), vp(y), heads, keys, keys, C.c_float(scale), None, valid)
-    return Op("softmax_masked", W.ALGO_BYTES["softmax_masked"], 2 * heads * keys * 4, mk, go, 1, "softmax_vec")
+        X.call("xs_hip_softmax_masked", stream, vp(x), vp(y), heads, keys, keys, C.c_float(scale), None, valid,
+               C.c_void_p(sp))
+    return Op("softmax_masked", W.ALGO_BYTES["softmax_masked"], 2 * heads * keys * 4, mk, go, 2, "softmax_partials")
 
 
 def op_argmax():
@@ -214,7 +217,6 @@ def op_argmax():
 
     def mk():
         sc = X.DeviceBuffer(nscratch)
-        X.call("xs_hip_memset", C.c_void_p(sc.ptr), 0, C.c_size_t(nscratch), None)
         s = (dcopy(x0), X.DeviceTensor.empty(X.F32, (1, 1)), X.DeviceTensor.empty(X.I32, (1, 1)), sc)
         need(s[0], width * 4, "argmax")
         return s
@@ -222,10 +224,10 @@ def op_argmax():
     def go(s, stream):
         x, v, i, sc = s
         X.call("xs_hip_topk", stream, vp(x), vp(v), vp(i), 1, width, 1, C.c_void_p(sc.ptr))
-    return Op("argmax", W.ALGO_BYTES["argmax"], width * 4, mk, go, 1, "argmax_chunks")
+    return Op("argmax", W.ALGO_BYTES["argmax"], width * 4, mk, go, 2, "argmax_chunks")
 
 
-def op_rope():
+def op_rope(separate=False):
     a = W.config3().arrays
     tokens, qh, dim = a["q"].shape
     kh = a["k"].shape[1]
@@ -244,9 +246,17 @@ def op_rope():
 
     def go(s, stream):
         q, k, p, f, yq, yk = s
+        X.call("xs_hip_rope2", stream, X.F16, vp(q), vp(yq), qh, vp(k), vp(yk), kh, X.I32, vp(p), vp(f), X.F16, tokens,
+               dim, 0, 1, None)
+
+    def go_separate(s, stream):
+        q, k, p, f, yq, yk = s
         X.call("xs_hip_rope", stream, X.F16, vp(q), X.I32, vp(p), vp(f), X.F16, vp(yq), tokens, qh, dim, 0, 1, None)
         X.call("xs_hip_rope", stream, X.F16, vp(k), X.I32, vp(p), vp(f), X.F16, vp(yk), tokens, kh, dim, 0, 1, None)
-    return Op("rope_qk", W.ALGO_BYTES["rope_qk"], 2 * (q0.nbytes + k0.nbytes), mk, go, 2, "rope_kernel")
+    if separate:
+        return Op("rope_qk_separate", W.ALGO_BYTES["rope_qk"], 2 * (q0.nbytes + k0.nbytes), mk, go_separate, 2,
+                  "rope_kernel")
+    return Op("rope_qk", W.ALGO_BYTES["rope_qk"], 2 * (q0.nbytes + k0.nbytes), mk, go, 1, "rope_kernel")
 
 
 def _kv_inputs():
@@ -311,7 +321,7 @@ def op_copy():
 
 
 OP_ORDER = ["swiglu_bias", "swiglu_bias_strided", "rmsnorm_residual", "softmax_masked", "argmax", "rope_qk",
-            "kv_quantize", "kv_dequantize"]
+            "rope_qk_separate", "kv_quantize", "kv_dequantize"]
 
 
 def build_ops(only):
@@ -322,7 +332,8 @@ def build_ops(only):
         if name in ("kv_quantize", "kv_dequantize") and kv is None:
             kv = _kv_inputs()
         yield {"swiglu_bias": op_swiglu, "swiglu_bias_strided": op_swiglu_strided, "rmsnorm_residual": op_rmsnorm,
-               "softmax_masked": op_softmax, "argmax": op_argmax, "rope_qk": op_rope, "copy": op_copy,
+               "softmax_masked": op_softmax, "argmax": op_argmax, "rope_qk": op_rope,
+               "rope_qk_separate": lambda: op_rope(True), "copy": op_copy,
                "kv_quantize": lambda: op_kv_quantize(kv), "kv_dequantize": lambda: op_kv_dequantize(kv)}[name]()
 
 

@@ -179,16 +179,21 @@ int xs_hip_add_rms_norm(void* stream, const float* x, const float* residual, con
 int xs_hip_softmax(void* stream, const float* x, float* y, int64_t rows, int64_t width);
 /* The masked attention-score form: per row r, s = fl32(x * scale) for keys c < valid_len[r] (or `valid_len_all` when
  * valid_len is NULL) and -inf beyond, then softmax; masked keys come out exactly 0. x/y rows `row_stride` apart.
- * Equals cpu-ref's Scale (ops.cpp:209-211), Add of a 0/-inf mask, Softmax (ops.cpp:644-661). */
+ * Equals cpu-ref's Scale (ops.cpp:209-211), Add of a 0/-inf mask, Softmax (ops.cpp:644-661).
+ * With `scratch` (xs_hip_softmax_scratch bytes, 16-byte aligned, any contents), a few wide rows are split over several
+ * workgroups in two launches that pass each chunk's (max, sum) through it; with NULL each row is one workgroup.
+ * Concurrent calls must not share one scratch. */
 int xs_hip_softmax_masked(void* stream, const float* x, float* y, int64_t rows, int64_t width, int64_t row_stride,
-                          float scale, const int64_t* valid_len, int64_t valid_len_all);
+                          float scale, const int64_t* valid_len, int64_t valid_len_all, void* scratch);
+/* Bytes of scratch xs_hip_softmax_masked can use for rows of `width` (0: it would not split them). No reference
+ * counterpart (cpu-ref's softmax needs none). */
+size_t xs_hip_softmax_scratch(int64_t rows, int64_t width);
 /* Bytes of scratch xs_hip_topk needs (0: none, NULL allowed). Replaces sycl_be::topk_scratch (sycl_kernels.h:61). */
 size_t xs_hip_topk_scratch(int64_t rows, int64_t width, int64_t k);
 /* The k largest per row of x [rows, width] f32: values f32 and indices i32 [rows, k], largest first, equal values keep
  * the lower index first (cpu_ref::topk, ops.cpp:663-684; spec graph.h:70-71). k = 1 is argmax (blocks::argmax_rows,
- * blocks.cpp:36-38). `scratch` (256-byte aligned) holds at least xs_hip_topk_scratch bytes and must be ZERO-FILLED once
- * before its first use: its head holds per-row arrival counters that every call leaves zero again, so one scratch
- * serves calls of any shape in stream order; concurrent calls must not share one. Replaces sycl_be::topk
+ * blocks.cpp:36-38). `scratch` (8-byte aligned, any contents) holds xs_hip_topk_scratch bytes: the per-chunk partials of
+ * wide rows, reduced by a second launch; concurrent calls must not share one. Replaces sycl_be::topk
  * (sycl_kernels.h:62-63). */
 int xs_hip_topk(void* stream, const float* x, float* values, int32_t* indices, int64_t rows, int64_t width, int64_t k,
                 void* scratch);
@@ -203,6 +208,14 @@ int xs_hip_topk(void* stream, const float* x, float* values, int32_t* indices, i
 int xs_hip_rope(void* stream, xs_dtype x_dtype, const void* x, xs_dtype pos_dtype, const void* positions,
                 const float* inv_freq, xs_dtype y_dtype, void* y, int64_t tokens, int64_t heads, int64_t dim,
                 int64_t rotary, int64_t sections, const int32_t* pair_axes);
+
+/* RoPE of two tensors of the same tokens in one launch -- the Q and K of a step, which share positions and inv_freq:
+ * xa/ya [tokens, heads_a, dim] and xb/yb [tokens, heads_b, dim], same dtypes; each rotated exactly as xs_hip_rope
+ * rotates it (each y may be its x). One launch computes each (token, pair) angle once for both tensors' heads. No
+ * reference counterpart: the reference launches rope once per tensor (sycl_backend.cpp:2187-2206). */
+int xs_hip_rope2(void* stream, xs_dtype x_dtype, const void* xa, void* ya, int64_t heads_a, const void* xb, void* yb,
+                 int64_t heads_b, xs_dtype pos_dtype, const void* positions, const float* inv_freq, xs_dtype y_dtype,
+                 int64_t tokens, int64_t dim, int64_t rotary, int64_t sections, const int32_t* pair_axes);
 
 /* ---- int8 KV cache ------------------------------------------------------------------------------------------- */
 

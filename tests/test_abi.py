@@ -84,7 +84,7 @@ def test_refusals_name_the_problem():
     assert "act must be" in err()
     assert L().xs_hip_act_bias_mul_2d(None, xs_hip.SILU, xs_hip.BF16, 1, 5, 1, 5, None, xs_hip.BF16, 1, 5, 2, 8) == 1
     assert "row strides" in err()
-    assert L().xs_hip_softmax_masked(None, None, None, 2, 8, 4, 1.0, None, 8) == 1
+    assert L().xs_hip_softmax_masked(None, None, None, 2, 8, 4, 1.0, None, 8, None) == 1
     assert L().xs_hip_copy(None, None, None, 17) == 1
 
 
@@ -94,6 +94,12 @@ def test_empty_work_is_a_no_op():
     assert L().xs_hip_act_mul(None, xs_hip.SILU, xs_hip.F32, None, None, xs_hip.F32, None, 0) == 0
     assert L().xs_hip_softmax(None, None, None, 0, 8) == 0
     assert L().xs_hip_topk(None, None, None, None, 0, 8, 1, None) == 0
+
+
+def test_softmax_scratch_sizes():
+    assert L().xs_hip_softmax_scratch(32, 32768) > 0        # few wide rows split
+    assert L().xs_hip_softmax_scratch(4096, 32768) == 0     # many rows fill the chip one row per workgroup
+    assert L().xs_hip_softmax_scratch(32, 4096) == 0        # one chunk
 
 
 def test_topk_scratch_sizes():

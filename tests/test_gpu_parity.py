@@ -374,6 +374,25 @@ def test_softmax_edge_rows(ora):
     assert np.isnan(got).all()
 
 
+def test_softmax_split_edges(ora):
+    """Rows split over several workgroups: a chunk of -inf keys beside finite ones, chunks past valid_len, a row of
+    nothing but -inf (NaN out, as cpu-ref), a width that is no multiple of a chunk; then the same scratch again."""
+    rng = np.random.default_rng(18)
+    x = (rng.standard_normal((4, 20000)) * 4).astype(np.float32)
+    x[0, 4096:8192] = -np.inf
+    x[2, :] = -np.inf
+    valid = np.array([20000, 5000, 20000, 12289], np.int64)
+    scratch = X.Scratch()
+    for rep in range(3):
+        step(f"softmax split [4, 20000] call {rep}")
+        got = X.softmax_masked(dev(x), 0.25, dev(valid, X.I64), scratch).numpy()
+        assert_f32_close(got, ora.softmax_masked(x, 0.25, valid), what="split edges")
+    assert np.isnan(got[2]).all() and (got[1, 5000:] == 0).all() and (got[0, 4096:8192] == 0).all()
+    step("softmax without scratch (one workgroup per row) agrees")
+    one = X.softmax_masked(dev(x), 0.25, dev(valid, X.I64), None).numpy()
+    assert_f32_close(one, got, what="split vs unsplit")
+
+
 def test_softmax_config2a_full(ora):
     cfg = W.config2a()
     s = cfg.arrays["scores"]
@@ -484,6 +503,33 @@ def test_rope_config3_full(ora):
             n0 = xf[..., :64] ** 2 + xf[..., 64:] ** 2
             n1 = yf[..., :64] ** 2 + yf[..., 64:] ** 2
             assert np.allclose(n0, n1, rtol=5e-3, atol=1e-3)
+
+
+def test_rope_qk_fused(ora):
+    """xs_hip_rope2 (Q and K in one launch) rotates each tensor exactly as xs_hip_rope does, at the config 3 shape,
+    in place, and with partial rotary (pass-through channels)."""
+    cfg = W.config3(tokens=1024)
+    a = cfg.arrays
+    pos, f = dev(a["positions"]), dev(a["inv_freq"])
+    q, k = dev(a["q"], F16), dev(a["k"], F16)
+    step("rope2 q+k [1024, 32+8, 128] f16")
+    yq, yk = X.rope_qk(q, k, pos, f)
+    assert_exact(yq.numpy().view(np.uint16), X.rope(q, pos, f).numpy().view(np.uint16), "fused q")
+    assert_exact(yk.numpy().view(np.uint16), X.rope(k, pos, f).numpy().view(np.uint16), "fused k")
+    step("rope2 in place")
+    q2, k2 = dev(a["q"], F16), dev(a["k"], F16)
+    X.rope_qk(q2, k2, pos, f, in_place=True)
+    assert_exact(q2.numpy().view(np.uint16), yq.numpy().view(np.uint16), "in place q")
+    assert_exact(k2.numpy().view(np.uint16), yk.numpy().view(np.uint16), "in place k")
+    rng = np.random.default_rng(19)
+    xq = rng.standard_normal((7, 3, 64)).astype(np.float32)
+    xk = rng.standard_normal((7, 2, 64)).astype(np.float32)
+    p7 = np.arange(7, dtype=np.int32) * 311
+    f32f = ora.rope_inv_freq(10000.0, 32, 16, 16)
+    step("rope2 partial rotary 32 of 64, f32")
+    yq, yk = X.rope_qk(dev(xq), dev(xk), dev(p7), dev(f32f), rotary_dim=32)
+    assert_f32_close(yq.numpy(), ora.rope(xq, p7, f32f, 32), what="partial q")
+    assert_f32_close(yk.numpy(), ora.rope(xk, p7, f32f, 32), what="partial k")
 
 
 @pytest.mark.parametrize("xdt,ydt", [(F32, F32), (F16, F16), (BF16, BF16), (F32, F16), (BF16, F32)])

@@ -33,16 +33,17 @@ const char* dtype_name(xs_dtype t);
 int device_cus();
 
 // ---------------------------------------------------------------------------------------------------------------
-// Scalar conversions. f16 <-> f32 use the hardware converts (v_cvt_f32_f16 is exact; v_cvt_f16_f32 rounds to nearest
-// even, overflows to inf and keeps NaN a NaN). bf16 narrowing is the integer round-to-nearest-even of
-// src/util/half.h:19-25 (NaN -> quiet NaN with the high bits kept), so it matches the reference bit for bit.
+// Scalar conversions, all in hardware: v_cvt_f32_f16 widens exactly; v_cvt_pk_f16_f32 and v_cvt_pk_bf16_f32 (gfx950)
+// narrow two values at a time with round-to-nearest-even, overflow to inf and NaN kept a quiet NaN -- the rounding of
+// the reference's util/half.h:19-25 and half.cpp:36-56. bf16 widening is a shift.
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t v) { return __uint_as_float(static_cast<uint32_t>(v) << 16); }
 
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    const uint32_t bits = __float_as_uint(f);
-    if ((bits & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((bits >> 16) | 0x0040u);
-    return static_cast<uint16_t>((bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16);
+    const __bf16 h = static_cast<__bf16>(f);
+    uint16_t v;
+    __builtin_memcpy(&v, &h, 2);
+    return v;
 }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t v) {
@@ -84,13 +85,6 @@ constexpr int vec_elems() {
     return 16 / static_cast<int>(sizeof(typename T::storage));
 }
 
-// One 128-bit vector of T, widened to f32.
-template <typename T>
-struct Vec {
-    static constexpr int N = vec_elems<T>();
-    float v[N];
-};
-
 using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
 
 // 128-bit global loads and stores (global_load_dwordx4 / global_store_dwordx4). `nt` marks streaming data that is
@@ -116,16 +110,27 @@ __device__ __forceinline__ void unpack(u32x4 raw, float* out) {
     }
 }
 
+// Two values narrowed to T in one 32-bit word (one v_cvt_pk_{f16,bf16}_f32), the first in the low half.
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    if constexpr (T::dtype == XS_F16) {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        const h2 v = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
+        return __builtin_bit_cast(uint32_t, v);
+    } else {
+        typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+        const b2 v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+        return __builtin_bit_cast(uint32_t, v);
+    }
+}
+
 template <typename T>
 __device__ __forceinline__ u32x4 pack(const float* in) {
     u32x4 raw;
     if constexpr (sizeof(typename T::storage) == 4) {
         for (int i = 0; i < 4; ++i) raw[i] = __float_as_uint(in[i]);
     } else {
-        for (int i = 0; i < 4; ++i) {
-            raw[i] = static_cast<uint32_t>(T::store(in[2 * i])) |
-                     (static_cast<uint32_t>(T::store(in[2 * i + 1])) << 16);
-        }
+        for (int i = 0; i < 4; ++i) raw[i] = pack2<T>(in[2 * i], in[2 * i + 1]);
     }
     return raw;
 }
@@ -188,6 +193,24 @@ __device__ __forceinline__ double group_sum_f64(double v) {
     for (int off = 1; off < W; off <<= 1) v += __shfl_xor(v, off, 64);
     return v;
 }
+
+// ---------------------------------------------------------------------------------------------------------------
+// Index arithmetic.
+
+// Granlund-Montgomery division by a run-time constant: floor(n / d) = (umulhi(n, m) + n) >> s for every n < 2^32,
+// with s = ceil(log2 d) and m = floor(2^32 (2^s - d) / d) + 1.
+struct FastDiv32 {
+    uint32_t m = 1, s = 0;
+    FastDiv32() = default;
+    explicit FastDiv32(uint32_t d) {
+        s = 0;
+        while ((uint64_t{1} << s) < d) ++s;
+        m = static_cast<uint32_t>(((uint64_t{1} << 32) * ((uint64_t{1} << s) - d)) / d + 1);
+    }
+    __device__ __forceinline__ uint32_t div(uint32_t n) const {
+        return static_cast<uint32_t>((static_cast<uint64_t>(__umulhi(n, m)) + n) >> s);
+    }
+};
 
 // ---------------------------------------------------------------------------------------------------------------
 // Launch geometry.

@@ -4,18 +4,26 @@
 // layout quant::kv_row_bytes(I8) = {width codes, one f32 scale} (src/quant/kv_format.cpp:47-48), launchers
 // sycl_be::quantize_kv / dequantize_kv (src/backend/sycl/sycl_kv_cache.cpp:33-49, 87-93, 119-150).
 //
-// Quantize layout: a row of `width` values is spread over LPR lanes (LPR = row bytes / 16, a power of two <= 64), each
-// lane holding one 128-bit vector; rows per wave = 64 / LPR. The row's |x| maximum is a DPP reduction inside the LPR
-// lanes, so a row never touches LDS. Each lane keeps U rows in flight (U independent 128-bit loads) to cover HBM
-// latency. Rounding is the reference's: inv = 127.0f / amax (correctly rounded f32 division), code =
-// rint(x * inv) (v_rndne_f32, round half to even) clamped to [-127, 127], scale = amax / 127.0f.
+// Quantize layout: a row of `width` values is spread over L lanes (L = min(16, 128-bit vectors per row)), lane l
+// holding the row's vectors l, l + L, ... (VPL of them), so every load instruction reads whole contiguous 256-byte
+// runs of a row and every store instruction writes whole contiguous runs of codes -- no partial cache lines, which
+// would cost a read of the line before the write. A row's |x| maximum is a DPP reduction inside its L lanes (no LDS).
+// Each lane keeps U rows in flight (U * VPL independent 128-bit loads). Rounding is the reference's:
+// inv = 127.0f / amax (correctly rounded f32 division), code = rint(x * inv) round half to even,
+// scale = amax / 127.0f. rint is taken by adding 1.5 * 2^23 in f32 (the FPU's own round-to-nearest-even) and keeping
+// the low byte, which is the code in two's complement since |x * inv| <= 127 (the clamp of the reference can never
+// bind); a NaN product (a NaN input, or an infinite row's 0 * inf) leaves a quiet NaN, whose low byte is 0 for every
+// f16/bf16 input and for the canonical NaN -- the value x86-64 gives the reference's cast of NaN.
+//
+// Dequantize layout: a unit is 8 codes (one 64-bit load) and their 8 outputs (one 128-bit store for f16/bf16, two
+// for f32); consecutive lanes take consecutive units, so loads and stores are contiguous across the wave, and each
+// lane keeps U units (codes and row scales) in flight.
 #include "common.h"
 
 namespace xs_hip {
 namespace {
 
-// A NaN product has no defined int8 value in the reference (a float-to-int cast of NaN); on the x86-64 host the
-// conversion yields INT_MIN whose low byte is 0, so a NaN code is 0 here as there.
+// Scalar form of the rounding above (the any-width kernel).
 __device__ __forceinline__ int quantize_code(float x, float inv) {
     float q = rintf(x * inv);
     if (q != q) return 0;
@@ -23,52 +31,66 @@ __device__ __forceinline__ int quantize_code(float x, float inv) {
     return static_cast<int>(q);
 }
 
-template <typename T, int LPR, int U>
+// x * inv + 1.5 * 2^23: the low byte of the sum's bits is rint(x * inv) (|x * inv| <= 127), or 0 for NaN.
+__device__ __forceinline__ uint32_t code_bits(float x, float inv) {
+    return __float_as_uint(x * inv + 12582912.0f);
+}
+
+// The low bytes of four words, packed in order into one word.
+__device__ __forceinline__ uint32_t pack_low_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);  // a.b0 | b.b0 << 8
+    const uint32_t cd = __builtin_amdgcn_perm(d, c, 0x04000c0cu);  // c.b0 << 16 | d.b0 << 24
+    return ab | cd;
+}
+
+template <typename T, int L, int VPL, int U>
 __global__ __launch_bounds__(kBlock) void quantize_i8_vec(const typename T::storage* __restrict__ x,
                                                           int8_t* __restrict__ codes, float* __restrict__ scales,
                                                           int64_t rows, int64_t width) {
     constexpr int VEC = vec_elems<T>();
-    constexpr int RPW = 64 / LPR;
+    constexpr int RPW = 64 / L;  // rows per wave
     const int lane = threadIdx.x & 63;
-    const int sub = lane / LPR;
-    const int l = lane % LPR;
+    const int sub = lane / L;
+    const int l = lane % L;
     const int64_t waves = static_cast<int64_t>(gridDim.x) * (kBlock / 64);
     const int64_t wave_id = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
     const int64_t stride = waves * RPW;
-    for (int64_t base = wave_id * RPW + sub; base < rows + 0 * stride; base += U * stride) {
-        u32x4 raw[U];
+    for (int64_t base = wave_id * RPW + sub; base < rows; base += U * stride) {
+        u32x4 raw[U][VPL];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int64_t r = base + u * stride;
-            if (r < rows) raw[u] = ld128_nt(x + r * width + l * VEC);
-            else raw[u] = u32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int k = 0; k < VPL; ++k)
+                raw[u][k] = r < rows ? ld128_nt(x + r * width + (l + k * L) * VEC) : u32x4{0, 0, 0, 0};
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int64_t r = base + u * stride;
-            float f[VEC];
-            unpack<T>(raw[u], f);
+            float f[VPL][VEC];
+#pragma unroll
+            for (int k = 0; k < VPL; ++k) unpack<T>(raw[u][k], f[k]);
             float amax = 0.0f;
 #pragma unroll
-            for (int i = 0; i < VEC; ++i) amax = fmaxf(amax, fabsf(f[i]));
-            amax = group_reduce<LPR, OpMax>(amax);
+            for (int k = 0; k < VPL; ++k)
+#pragma unroll
+                for (int i = 0; i < VEC; ++i) amax = fmaxf(amax, fabsf(f[k][i]));
+            amax = group_reduce<L, OpMax>(amax);
             const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
             if (r < rows) {
-                if constexpr (VEC == 8) {
-                    uint32_t lo = 0, hi = 0;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) lo |= (static_cast<uint32_t>(quantize_code(f[i], inv)) & 0xffu) << (8 * i);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        hi |= (static_cast<uint32_t>(quantize_code(f[4 + i], inv)) & 0xffu) << (8 * i);
-                    uint2 packed = make_uint2(lo, hi);
-                    __builtin_nontemporal_store(packed.x, reinterpret_cast<uint32_t*>(codes + r * width + l * VEC));
-                    __builtin_nontemporal_store(packed.y, reinterpret_cast<uint32_t*>(codes + r * width + l * VEC) + 1);
-                } else {
-                    uint32_t w = 0;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) w |= (static_cast<uint32_t>(quantize_code(f[i], inv)) & 0xffu) << (8 * i);
-                    __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(codes + r * width + l * VEC));
+                for (int k = 0; k < VPL; ++k) {
+                    int8_t* out = codes + r * width + (l + k * L) * VEC;
+                    const uint32_t w0 = pack_low_bytes(code_bits(f[k][0], inv), code_bits(f[k][1], inv),
+                                                       code_bits(f[k][2], inv), code_bits(f[k][3], inv));
+                    if constexpr (VEC == 8) {
+                        const uint32_t w1 = pack_low_bytes(code_bits(f[k][4], inv), code_bits(f[k][5], inv),
+                                                           code_bits(f[k][6], inv), code_bits(f[k][7], inv));
+                        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                        __builtin_nontemporal_store(u32x2{w0, w1}, reinterpret_cast<u32x2*>(out));
+                    } else {
+                        __builtin_nontemporal_store(w0, reinterpret_cast<uint32_t*>(out));
+                    }
                 }
                 if (l == 0) scales[r] = amax / 127.0f;
             }
@@ -95,45 +117,43 @@ __global__ __launch_bounds__(kBlock) void quantize_i8_any(const typename T::stor
     }
 }
 
-// Unsigned 32-bit division by a run-time constant: q = (umulhi(n, m) + n) >> s with s = ceil(log2 d),
-// m = floor(2^32 (2^s - d) / d) + 1 (Granlund and Montgomery, "Division by invariant integers using
-// multiplication", 1994), exact for every n < 2^32.
-struct FastDiv {
-    uint32_t d = 1, m = 1, s = 0;
-    FastDiv() = default;
-    explicit FastDiv(uint32_t div) : d(div) {
-        s = 0;
-        while ((uint64_t{1} << s) < div) ++s;
-        m = static_cast<uint32_t>(((uint64_t{1} << 32) * ((uint64_t{1} << s) - div)) / div + 1);
-    }
-    __device__ __forceinline__ uint32_t div(uint32_t n) const {
-        return static_cast<uint32_t>((static_cast<uint64_t>(__umulhi(n, m)) + n) >> s);
-    }
-};
-
-// out = fl32(code * scale[row]), 16 codes per lane (one 128-bit load), 16 outputs stored as 128-bit vectors.
-template <typename Y>
-__global__ __launch_bounds__(kBlock) void dequantize_i8_vec(const u32x4* __restrict__ codes,
+// out = fl32(code * scale[row]) for units of 8 codes.
+template <typename Y, int U>
+__global__ __launch_bounds__(kBlock) void dequantize_i8_vec(const uint64_t* __restrict__ codes,
                                                             const float* __restrict__ scales,
-                                                            typename Y::storage* __restrict__ out, uint32_t nvec,
-                                                            FastDiv vecs_per_row) {
-    constexpr int OV = vec_elems<Y>();  // outputs per 128-bit store
+                                                            typename Y::storage* __restrict__ out, uint32_t units,
+                                                            FastDiv32 units_per_row) {
     const uint32_t stride = gridDim.x * kBlock;
-    for (uint32_t v = blockIdx.x * kBlock + threadIdx.x; v < nvec; v += stride) {
-        const u32x4 raw = ld128_nt(codes + v);
-        const float scale = scales[vecs_per_row.div(v)];
-        float f[16];
+    for (uint32_t v0 = blockIdx.x * kBlock + threadIdx.x; v0 < units; v0 += U * stride) {
+        uint64_t raw[U];
+        float scale[U];
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const int8_t c = static_cast<int8_t>((raw[w] >> (8 * b)) & 0xffu);
-                f[4 * w + b] = static_cast<float>(c) * scale;
+        for (int u = 0; u < U; ++u) {
+            const uint32_t v = v0 + u * stride;
+            if (v < units) {
+                raw[u] = __builtin_nontemporal_load(codes + v);
+                scale[u] = scales[units_per_row.div(v)];
             }
         }
-        typename Y::storage* o = out + static_cast<int64_t>(v) * 16;
 #pragma unroll
-        for (int k = 0; k < 16 / OV; ++k) st128_nt(o + k * OV, pack<Y>(f + k * OV));
+        for (int u = 0; u < U; ++u) {
+            const uint32_t v = v0 + u * stride;
+            if (v < units) {
+                float f[8];
+#pragma unroll
+                for (int b = 0; b < 8; ++b) {
+                    const int code = static_cast<int>(static_cast<int8_t>((raw[u] >> (8 * b)) & 0xffu));
+                    f[b] = static_cast<float>(code) * scale[u];
+                }
+                typename Y::storage* o = out + static_cast<int64_t>(v) * 8;
+                if constexpr (sizeof(typename Y::storage) == 2) {
+                    st128_nt(o, pack<Y>(f));
+                } else {
+                    st128_nt(o, pack<Y>(f));
+                    st128_nt(o + 4, pack<Y>(f + 4));
+                }
+            }
+        }
     }
 }
 
@@ -151,26 +171,26 @@ template <typename T>
 int launch_quantize(hipStream_t s, const void* x, int8_t* codes, float* scales, int64_t rows, int64_t width) {
     using S = typename T::storage;
     const int64_t row_bytes = width * static_cast<int64_t>(sizeof(S));
+    const int64_t nvr = row_bytes / 16;  // 128-bit vectors per row
     const bool vec_ok = row_bytes % 16 == 0 && aligned16(x) && (reinterpret_cast<uintptr_t>(codes) % 8 == 0) &&
-                        ((width * 1) % 4 == 0);
-    const int64_t lpr = row_bytes / 16;
+                        (nvr & (nvr - 1)) == 0 && nvr >= 1 && nvr <= 64;
     const auto* xs = static_cast<const S*>(x);
     constexpr int U = 4;
-    auto go = [&](auto kernel, int rpw) {
-        const int64_t slots_per_block = (kBlock / 64) * rpw;
-        const unsigned grid = grid_for(rows, static_cast<int>(slots_per_block * U));
+    auto go = [&](auto kernel, int lanes) {
+        const int64_t rows_per_block = (kBlock / 64) * (64 / lanes);
+        const unsigned grid = grid_for(rows, static_cast<int>(rows_per_block * U));
         kernel<<<grid, kBlock, 0, s>>>(xs, codes, scales, rows, width);
         return check_launch("xs_hip_quantize_kv");
     };
     if (vec_ok) {
-        switch (lpr) {
-            case 1: return go(quantize_i8_vec<T, 1, U>, 64);
-            case 2: return go(quantize_i8_vec<T, 2, U>, 32);
-            case 4: return go(quantize_i8_vec<T, 4, U>, 16);
-            case 8: return go(quantize_i8_vec<T, 8, U>, 8);
-            case 16: return go(quantize_i8_vec<T, 16, U>, 4);
-            case 32: return go(quantize_i8_vec<T, 32, U>, 2);
-            case 64: return go(quantize_i8_vec<T, 64, U>, 1);
+        switch (nvr) {
+            case 1: return go(quantize_i8_vec<T, 1, 1, U>, 1);
+            case 2: return go(quantize_i8_vec<T, 2, 1, U>, 2);
+            case 4: return go(quantize_i8_vec<T, 4, 1, U>, 4);
+            case 8: return go(quantize_i8_vec<T, 8, 1, U>, 8);
+            case 16: return go(quantize_i8_vec<T, 16, 1, U>, 16);
+            case 32: return go(quantize_i8_vec<T, 16, 2, U>, 16);
+            case 64: return go(quantize_i8_vec<T, 16, 4, U>, 16);
             default: break;
         }
     }
@@ -185,10 +205,10 @@ int launch_dequantize(hipStream_t s, const int8_t* codes, const float* scales, v
     using S = typename Y::storage;
     const int64_t n = rows * width;
     auto* o = static_cast<S*>(out);
-    if (width % 16 == 0 && aligned16(codes) && aligned16(out) && n / 16 < (int64_t{1} << 32)) {
-        const uint32_t nvec = static_cast<uint32_t>(n / 16);
-        dequantize_i8_vec<Y><<<grid_for(nvec, kBlock * 4), kBlock, 0, s>>>(
-            reinterpret_cast<const u32x4*>(codes), scales, o, nvec, FastDiv(static_cast<uint32_t>(width / 16)));
+    if (width % 8 == 0 && reinterpret_cast<uintptr_t>(codes) % 8 == 0 && aligned16(out) && n / 8 < (int64_t{1} << 32)) {
+        const uint32_t units = static_cast<uint32_t>(n / 8);
+        dequantize_i8_vec<Y, 4><<<grid_for(units, kBlock * 4), kBlock, 0, s>>>(
+            reinterpret_cast<const uint64_t*>(codes), scales, o, units, FastDiv32(static_cast<uint32_t>(width / 8)));
     } else {
         dequantize_i8_any<Y><<<grid_for(n, kBlock * 4), kBlock, 0, s>>>(codes, scales, o, n, width);
     }

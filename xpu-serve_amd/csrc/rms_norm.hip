@@ -116,8 +116,8 @@ __global__ __launch_bounds__(LPR > kBlock ? LPR : kBlock) void rms_norm_vec(Norm
             if constexpr (sizeof(SY) == 2 && VEC == 4) {
                 // four 16-bit outputs: one 64-bit store
                 uint2 packed;
-                packed.x = static_cast<uint32_t>(TY::store(o[0])) | (static_cast<uint32_t>(TY::store(o[1])) << 16);
-                packed.y = static_cast<uint32_t>(TY::store(o[2])) | (static_cast<uint32_t>(TY::store(o[3])) << 16);
+                packed.x = pack2<TY>(o[0], o[1]);
+                packed.y = pack2<TY>(o[2], o[3]);
                 *reinterpret_cast<uint2*>(yr + v * VEC) = packed;
             } else if constexpr (sizeof(SY) == 4 && VEC == 8) {
                 st128_nt(yr + v * VEC, pack<TY>(o));
@@ -180,9 +180,11 @@ int go_vec(hipStream_t s, const NormArgs& p, int nv) {
     return check_launch("xs_hip_rms_norm");
 }
 
-// Lanes per row: the smallest power of two (>= 16) that keeps at most kMaxNv vectors per lane; rows wider than
-// 1024 lanes * kMaxNv vectors take the two-pass kernel.
+// Lanes per row: the smallest power of two (>= 16) that keeps at most kMaxNv vectors per lane and puts at least
+// kTargetWaves waves on the chip (few rows get more lanes each, so the whole chip pulls on HBM), or keeps at most two
+// vectors per lane; rows wider than 1024 lanes * kMaxNv vectors take the two-pass kernel.
 constexpr int kMaxNv = 8;
+constexpr int64_t kTargetWaves = 2048;  // 8 per CU on 256 CUs
 
 template <typename TX, typename TY>
 int launch_norm(hipStream_t s, const NormArgs& p) {
@@ -196,6 +198,7 @@ int launch_norm(hipStream_t s, const NormArgs& p) {
         for (int lpr = 16; lpr <= 1024; lpr *= 2) {
             const int64_t nv = (nvec + lpr - 1) / lpr;
             if (nv > kMaxNv) continue;
+            if (lpr < 1024 && nv > 2 && p.rows * lpr / 64 < kTargetWaves) continue;
             const int n = static_cast<int>(nv);
             switch (lpr) {
                 case 16: return go_vec<TX, TY, 16>(s, p, n);

@@ -9,9 +9,11 @@
 // reference CPU path's f64 angle, so its outputs round from the same f64 values cpu-ref computes.
 //
 // Layout: a block takes a tile of TT tokens. Its threads first fill an LDS table of (cos, sin) in f64 for the tile's
-// TT x pairs entries -- one sincos per (token, pair), shared by every head of the token -- then each unit of work
-// (token, head, VEC consecutive pairs) loads VEC values of x1 and of x2 with 128-bit loads, rotates them in f64, and
-// stores the two 128-bit (or narrower, by output dtype) vectors.
+// TT x pairs entries -- one sincos per (token, pair), shared by every head of the token; one f64 pair of padding every
+// 8 entries spreads the 8 entries a wave reads at once over distinct LDS banks. Then each thread owns one unit slot
+// (head, VEC consecutive pairs) for the whole tile and walks the tile's tokens two at a time, issuing both tokens'
+// 128-bit loads of x1 and x2 before rotating; the rotation is an f64 FMA of the exactly widened inputs, rounded to f32
+// and then to y's dtype, as cpu-ref's f64 expression is.
 #include <cmath>
 
 #include "common.h"
@@ -27,7 +29,25 @@ struct RopeArgs {
     const int32_t* pair_axes;
     int64_t tokens, heads, dim, rotary, sections;
     int tile_tokens;
+    // An optional second tensor of the same tokens (K beside Q): x2 / y2 [tokens, heads2, dim]; heads2 = 0 for none.
+    const void* x2;
+    void* y2;
+    int64_t heads2;
 };
+
+// The element offset of (token t, head h) and the tensor it lies in: heads [0, heads) are x / y, heads
+// [heads, heads + heads2) the second tensor.
+template <typename SX, typename SY>
+__device__ __forceinline__ int64_t head_at(const RopeArgs& a, int64_t t, int h, const SX*& x, SY*& y) {
+    if (h < a.heads) {
+        x = static_cast<const SX*>(a.x);
+        y = static_cast<SY*>(a.y);
+        return (t * a.heads + h) * a.dim;
+    }
+    x = static_cast<const SX*>(a.x2);
+    y = static_cast<SY*>(a.y2);
+    return (t * a.heads2 + (h - a.heads)) * a.dim;
+}
 
 template <typename I>
 __device__ __forceinline__ int64_t pos_at(const void* p, int64_t i) {
@@ -46,8 +66,8 @@ __device__ __forceinline__ void store_n(typename T::storage* p, const float* f) 
         st128(p + 16 / sizeof(typename T::storage), pack<T>(f + 16 / sizeof(typename T::storage)));
     } else {  // 4 x 16-bit = 8 bytes
         uint2 v;
-        v.x = static_cast<uint32_t>(T::store(f[0])) | (static_cast<uint32_t>(T::store(f[1])) << 16);
-        v.y = static_cast<uint32_t>(T::store(f[2])) | (static_cast<uint32_t>(T::store(f[3])) << 16);
+        v.x = pack2<T>(f[0], f[1]);
+        v.y = pack2<T>(f[2], f[3]);
         *reinterpret_cast<uint2*>(p) = v;
     }
 }
@@ -62,13 +82,27 @@ __device__ __forceinline__ void load_n(const typename T::storage* p, float* f) {
     }
 }
 
-constexpr int kMaxTableEntries = 2048;  // (cos, sin) f64 pairs: 32 KiB of LDS
+constexpr int kMaxTableEntries = 1024;  // (cos, sin) f64 pairs per block, before padding: 18 KiB of LDS
+constexpr int kTableSlots = kMaxTableEntries + kMaxTableEntries / 8;
+
+__device__ __forceinline__ int table_slot(int e) { return e + (e >> 3); }
+
+// y1 = x1 c - x2 s, y2 = x2 c + x1 s in f64, each rounded to f32.
+template <int VEC>
+__device__ __forceinline__ void rotate(const float* x1, const float* x2, const double2* cs, float* y1, float* y2) {
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+        const double d1 = x1[k], d2 = x2[k];
+        y1[k] = static_cast<float>(fma(d1, cs[k].x, -(d2 * cs[k].y)));
+        y2[k] = static_cast<float>(fma(d2, cs[k].x, d1 * cs[k].y));
+    }
+}
 
 template <typename TX, typename TY, typename I, int VEC>
 __global__ __launch_bounds__(kBlock) void rope_kernel(RopeArgs a) {
     using SX = typename TX::storage;
     using SY = typename TY::storage;
-    __shared__ double2 table[kMaxTableEntries];
+    __shared__ double2 table[kTableSlots];
 
     const int64_t pairs = a.rotary / 2;
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * a.tile_tokens;
@@ -98,50 +132,95 @@ __global__ __launch_bounds__(kBlock) void rope_kernel(RopeArgs a) {
         const double angle = pos * static_cast<double>(a.inv_freq[i]);
         double s, c;
         sincos(angle, &s, &c);
-        table[e] = make_double2(c, s);
+        table[table_slot(e)] = make_double2(c, s);
     }
     __syncthreads();
 
-    const SX* x = static_cast<const SX*>(a.x);
-    SY* y = static_cast<SY*>(a.y);
+    const int heads = static_cast<int>(a.heads + a.heads2);
     const int pv_per_head = static_cast<int>(pairs / VEC);
-    const int rot_units = tt_n * static_cast<int>(a.heads) * pv_per_head;
-    for (int u = threadIdx.x; u < rot_units; u += kBlock) {
-        const int tt = u / (static_cast<int>(a.heads) * pv_per_head);
-        const int rem = u - tt * static_cast<int>(a.heads) * pv_per_head;
-        const int h = rem / pv_per_head;
-        const int p0 = (rem - h * pv_per_head) * VEC;
-        int64_t c1;
-        if (axes) {
-            c1 = p0;
-        } else {
-            const int64_t sec = p0 / half;
-            c1 = sec * width + (p0 - sec * half);
-        }
-        const int64_t base = ((t0 + tt) * a.heads + h) * a.dim;
-        float x1[VEC], x2[VEC], y1[VEC], y2[VEC];
-        load_n<TX, VEC>(x + base + c1, x1);
-        load_n<TX, VEC>(x + base + c1 + half, x2);
+    const int upt = heads * pv_per_head;  // rotation units per token
+    if (upt <= kBlock) {
+        // Each thread owns one (head, pair vector) slot; the block's threads cover tpp tokens per pass.
+        const int tpp = kBlock / upt;
+        const int slot = threadIdx.x % upt;
+        const int t_off = threadIdx.x / upt;
+        if (t_off < tpp) {
+            const int h = slot / pv_per_head;
+            const int p0 = (slot - h * pv_per_head) * VEC;
+            int64_t c1 = p0;
+            if (!axes) {
+                const int64_t sec = p0 / half;
+                c1 = sec * width + (p0 - sec * half);
+            }
+            for (int tt = t_off; tt < tt_n; tt += 2 * tpp) {
+                const int tt2 = tt + tpp;
+                const bool two = tt2 < tt_n;
+                const SX* x;
+                SY* y;
+                const int64_t base = head_at(a, t0 + tt, h, x, y) + c1;
+                const int64_t base2 = head_at(a, t0 + tt2, h, x, y) + c1;
+                float x1[VEC], x2[VEC], z1[VEC], z2[VEC];
+                load_n<TX, VEC>(x + base, x1);
+                load_n<TX, VEC>(x + base + half, x2);
+                if (two) {
+                    load_n<TX, VEC>(x + base2, z1);
+                    load_n<TX, VEC>(x + base2 + half, z2);
+                }
+                double2 cs[VEC];
 #pragma unroll
-        for (int k = 0; k < VEC; ++k) {
-            const double2 cs = table[tt * pairs + p0 + k];
-            const double d1 = x1[k], d2 = x2[k];
-            y1[k] = static_cast<float>(d1 * cs.x - d2 * cs.y);
-            y2[k] = static_cast<float>(d2 * cs.x + d1 * cs.y);
+                for (int k = 0; k < VEC; ++k) cs[k] = table[table_slot(tt * static_cast<int>(pairs) + p0 + k)];
+                float y1[VEC], y2[VEC];
+                rotate<VEC>(x1, x2, cs, y1, y2);
+                store_n<TY, VEC>(y + base, y1);
+                store_n<TY, VEC>(y + base + half, y2);
+                if (two) {
+#pragma unroll
+                    for (int k = 0; k < VEC; ++k) cs[k] = table[table_slot(tt2 * static_cast<int>(pairs) + p0 + k)];
+                    rotate<VEC>(z1, z2, cs, y1, y2);
+                    store_n<TY, VEC>(y + base2, y1);
+                    store_n<TY, VEC>(y + base2 + half, y2);
+                }
+            }
         }
-        store_n<TY, VEC>(y + base + c1, y1);
-        store_n<TY, VEC>(y + base + c1 + half, y2);
+    } else {
+        const int rot_units = tt_n * upt;
+        for (int u = threadIdx.x; u < rot_units; u += kBlock) {
+            const int tt = u / upt;
+            const int rem = u - tt * upt;
+            const int h = rem / pv_per_head;
+            const int p0 = (rem - h * pv_per_head) * VEC;
+            int64_t c1 = p0;
+            if (!axes) {
+                const int64_t sec = p0 / half;
+                c1 = sec * width + (p0 - sec * half);
+            }
+            const SX* x;
+            SY* y;
+            const int64_t base = head_at(a, t0 + tt, h, x, y) + c1;
+            float x1[VEC], x2[VEC], y1[VEC], y2[VEC];
+            load_n<TX, VEC>(x + base, x1);
+            load_n<TX, VEC>(x + base + half, x2);
+            double2 cs[VEC];
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) cs[k] = table[table_slot(tt * static_cast<int>(pairs) + p0 + k)];
+            rotate<VEC>(x1, x2, cs, y1, y2);
+            store_n<TY, VEC>(y + base, y1);
+            store_n<TY, VEC>(y + base + half, y2);
+        }
     }
 
     // Channels past the rotary dims pass through (unless y is x).
-    if (a.rotary < a.dim && static_cast<const void*>(a.x) != a.y) {
+    if (a.rotary < a.dim) {
         const int64_t rest = a.dim - a.rotary;
-        const int64_t units = static_cast<int64_t>(tt_n) * a.heads * rest;
+        const int64_t units = static_cast<int64_t>(tt_n) * heads * rest;
         for (int64_t u = threadIdx.x; u < units; u += kBlock) {
-            const int64_t row = u / rest;
-            const int64_t c = a.rotary + (u - row * rest);
-            const int64_t at = (t0 * a.heads + row) * a.dim + c;
-            y[at] = TY::store(TX::load(x[at]));
+            const int64_t th = u / rest;
+            const int64_t tt = th / heads;
+            const int h = static_cast<int>(th - tt * heads);
+            const SX* x;
+            SY* y;
+            const int64_t at = head_at(a, t0 + tt, h, x, y) + a.rotary + (u - th * rest);
+            if (static_cast<const void*>(x) != static_cast<const void*>(y)) y[at] = TY::store(TX::load(x[at]));
         }
     }
 }
@@ -153,10 +232,10 @@ int launch_rope(hipStream_t s, RopeArgs a) {
     const bool axes = a.pair_axes != nullptr;
     const int64_t half = axes ? pairs : (a.rotary / a.sections) / 2;
     const bool vec = half % VEC == 0 && a.dim % VEC == 0 && aligned16(a.x) && aligned16(a.y) &&
-                     (sizeof(typename TY::storage) * VEC >= 16 || reinterpret_cast<uintptr_t>(a.y) % 8 == 0);
-    // Tokens per block: enough rotation units for two per thread, within the LDS table.
-    const int64_t units_per_token = a.heads * (pairs / (vec ? VEC : 1));
-    int64_t tt = units_per_token > 0 ? (2 * kBlock + units_per_token - 1) / units_per_token : 1;
+                     (a.heads2 == 0 || (aligned16(a.x2) && aligned16(a.y2)));
+    // Tokens per block: four rotation units per thread, within the LDS table.
+    const int64_t units_per_token = (a.heads + a.heads2) * (pairs / (vec ? VEC : 1));
+    int64_t tt = units_per_token > 0 ? (4 * kBlock + units_per_token - 1) / units_per_token : 1;
     if (tt < 1) tt = 1;
     const int64_t max_tt = pairs > 0 ? kMaxTableEntries / pairs : 64;
     if (tt > max_tt) tt = max_tt;
@@ -194,44 +273,73 @@ std::string i2s(int64_t v) { return std::to_string(v); }
 
 using namespace xs_hip;
 
-extern "C" {
+namespace xs_hip {
+namespace {
 
-int xs_hip_rope(void* stream, xs_dtype x_dtype, const void* x, xs_dtype pos_dtype, const void* positions,
+int check_overlap(const void* x, const void* y, int64_t n, xs_dtype xt, xs_dtype yt, const char* what) {
+    if (x == y) return XS_HIP_OK;
+    const int esx = float_size(xt), esy = float_size(yt);
+    const char* xb = static_cast<const char*>(x);
+    const char* yb = static_cast<const char*>(y);
+    if (esx > 0 && esy > 0 && xb < yb + n * esy && yb < xb + n * esx)
+        return fail(XS_HIP_EINVAL, std::string(what) + ": y overlaps x without being x");
+    return XS_HIP_OK;
+}
+
+int rope_common(void* stream, xs_dtype x_dtype, const void* x, xs_dtype pos_dtype, const void* positions,
                 const float* inv_freq, xs_dtype y_dtype, void* y, int64_t tokens, int64_t heads, int64_t dim,
-                int64_t rotary, int64_t sections, const int32_t* pair_axes) {
+                int64_t rotary, int64_t sections, const int32_t* pair_axes, const void* x2, void* y2, int64_t heads2,
+                const char* what) {
     if (rotary == 0) rotary = dim;
-    if (tokens < 0 || heads <= 0 || dim <= 0 || rotary < 0 || rotary > dim || sections <= 0)
-        return fail(XS_HIP_EINVAL, "xs_hip_rope: x [" + i2s(tokens) + ", " + i2s(heads) + ", " + i2s(dim) + "], rotary " +
-                                       i2s(rotary) + ", sections " + i2s(sections));
+    if (tokens < 0 || heads <= 0 || heads2 < 0 || dim <= 0 || rotary < 0 || rotary > dim || sections <= 0)
+        return fail(XS_HIP_EINVAL, std::string(what) + ": x [" + i2s(tokens) + ", " + i2s(heads) + ", " + i2s(dim) +
+                                       "], rotary " + i2s(rotary) + ", sections " + i2s(sections));
     if (pair_axes == nullptr && (rotary % (2 * sections) != 0))
-        return fail(XS_HIP_EINVAL, "xs_hip_rope: rotary dims " + i2s(rotary) + " do not split into " + i2s(sections) +
-                                       " sections of pairs");
+        return fail(XS_HIP_EINVAL, std::string(what) + ": rotary dims " + i2s(rotary) + " do not split into " +
+                                       i2s(sections) + " sections of pairs");
     if (pair_axes != nullptr && rotary % 2 != 0)
-        return fail(XS_HIP_EINVAL, "xs_hip_rope: rotary dims " + i2s(rotary) + " are odd");
+        return fail(XS_HIP_EINVAL, std::string(what) + ": rotary dims " + i2s(rotary) + " are odd");
     if (tokens == 0) return XS_HIP_OK;
-    if (x == nullptr || positions == nullptr || inv_freq == nullptr || y == nullptr)
-        return fail(XS_HIP_EINVAL, "xs_hip_rope: null buffer");
+    if (x == nullptr || positions == nullptr || inv_freq == nullptr || y == nullptr ||
+        (heads2 > 0 && (x2 == nullptr || y2 == nullptr)))
+        return fail(XS_HIP_EINVAL, std::string(what) + ": null buffer");
     if (rotary / 2 > kMaxTableEntries)
-        return fail(XS_HIP_EUNSUPPORTED, "xs_hip_rope: " + i2s(rotary / 2) + " pairs per head exceed " + i2s(kMaxTableEntries));
-    if (tokens > 0x7fffffffLL || heads * (rotary / 2) > (int64_t{1} << 24))
-        return fail(XS_HIP_EUNSUPPORTED, "xs_hip_rope: shape too large");
-    if (x != y) {
-        // y may be x, but may not overlap it otherwise.
-        const int esx = float_size(x_dtype), esy = float_size(y_dtype);
-        const char* xb = static_cast<const char*>(x);
-        const char* yb = static_cast<const char*>(y);
-        const int64_t n = tokens * heads * dim;
-        if (esx > 0 && esy > 0 && xb < yb + n * esy && yb < xb + n * esx)
-            return fail(XS_HIP_EINVAL, "xs_hip_rope: y overlaps x without being x");
-    }
-    const RopeArgs a{x, positions, inv_freq, y, pair_axes, tokens, heads, dim, rotary, sections, 1};
+        return fail(XS_HIP_EUNSUPPORTED, std::string(what) + ": " + i2s(rotary / 2) + " pairs per head exceed " +
+                                             i2s(kMaxTableEntries));
+    if (tokens > 0x7fffffffLL || (heads + heads2) * (rotary / 2) > (int64_t{1} << 24))
+        return fail(XS_HIP_EUNSUPPORTED, std::string(what) + ": shape too large");
+    int rc = check_overlap(x, y, tokens * heads * dim, x_dtype, y_dtype, what);
+    if (rc == XS_HIP_OK && heads2 > 0) rc = check_overlap(x2, y2, tokens * heads2 * dim, x_dtype, y_dtype, what);
+    if (rc != XS_HIP_OK) return rc;
+    const RopeArgs a{x, positions, inv_freq, y, pair_axes, tokens, heads, dim, rotary, sections, 1, x2, y2, heads2};
     const hipStream_t s = as_stream(stream);
     switch (x_dtype) {
         case XS_F32: return rope_y<F32>(s, a, pos_dtype, y_dtype);
         case XS_F16: return rope_y<F16>(s, a, pos_dtype, y_dtype);
         case XS_BF16: return rope_y<BF16>(s, a, pos_dtype, y_dtype);
-        default: return fail(XS_HIP_EINVAL, std::string("xs_hip_rope: x must be f32, f16 or bf16, got ") + dtype_name(x_dtype));
+        default:
+            return fail(XS_HIP_EINVAL, std::string(what) + ": x must be f32, f16 or bf16, got " + dtype_name(x_dtype));
     }
+}
+
+}  // namespace
+}  // namespace xs_hip
+
+extern "C" {
+
+int xs_hip_rope(void* stream, xs_dtype x_dtype, const void* x, xs_dtype pos_dtype, const void* positions,
+                const float* inv_freq, xs_dtype y_dtype, void* y, int64_t tokens, int64_t heads, int64_t dim,
+                int64_t rotary, int64_t sections, const int32_t* pair_axes) {
+    return rope_common(stream, x_dtype, x, pos_dtype, positions, inv_freq, y_dtype, y, tokens, heads, dim, rotary,
+                       sections, pair_axes, nullptr, nullptr, 0, "xs_hip_rope");
+}
+
+int xs_hip_rope2(void* stream, xs_dtype x_dtype, const void* xa, void* ya, int64_t heads_a, const void* xb, void* yb,
+                 int64_t heads_b, xs_dtype pos_dtype, const void* positions, const float* inv_freq, xs_dtype y_dtype,
+                 int64_t tokens, int64_t dim, int64_t rotary, int64_t sections, const int32_t* pair_axes) {
+    if (heads_b <= 0) return fail(XS_HIP_EINVAL, "xs_hip_rope2: the second tensor has no heads");
+    return rope_common(stream, x_dtype, xa, pos_dtype, positions, inv_freq, y_dtype, ya, tokens, heads_a, dim, rotary,
+                       sections, pair_axes, xb, yb, heads_b, "xs_hip_rope2");
 }
 
 }  // extern "C"

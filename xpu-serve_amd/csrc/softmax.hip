@@ -11,6 +11,13 @@
 // in f32 (exact) by DPP within a wave and one LDS stage across waves; x - peak carries its rounding error (TwoSum) into
 // exp; the sum is accumulated in f64; y = e * (1 / sum) in f64, rounded once. Masked keys are neither loaded nor
 // exponentiated.
+//
+// Few wide rows (the decode step's [heads, 1, keys] scores) would leave most of the chip idle with one workgroup per
+// row, so with caller scratch a row is split over `chunks` workgroups of kChunk keys, in two launches that need no
+// atomics or cross-workgroup waits: the first writes each chunk's (max m_j, sum s_j of exp(x - m_j)) to scratch; the
+// second reads the row's partials (one lane per chunk: M = max m_j, S = sum s_j exp(m_j - M) in f64), reads its chunk
+// again -- from the L2 of the same XCD, since both launches map a chunk to the same workgroup id -- and writes
+// exp(x - M) / S.
 #include <cmath>
 
 #include "common.h"
@@ -164,6 +171,153 @@ __global__ __launch_bounds__(kBlock) void softmax_any(SoftmaxArgs p) {
     }
 }
 
+constexpr int kChunkVpt = 4;                      // 128-bit vectors per lane in a chunk
+constexpr int64_t kChunk = kBlock * kChunkVpt * 4;  // keys per chunk: 4096
+constexpr int64_t kMaxRows = 65535;
+constexpr int kMaxChunks = 64;                      // the second launch combines a row's partials in one wave
+
+// Max over the block; every thread gets it.
+__device__ __forceinline__ float block_max(float v, float* lds) {
+    v = group_reduce<64, OpMax>(v);
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float m = lds[0];
+    for (int i = 1; i < kBlock / 64; ++i) m = fmaxf(m, lds[i]);
+    __syncthreads();
+    return m;
+}
+
+__device__ __forceinline__ double block_sum(double v, double* lds) {
+    v = group_sum_f64<64>(v);
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+    __syncthreads();
+    double s = 0.0;
+    for (int i = 0; i < kBlock / 64; ++i) s += lds[i];
+    __syncthreads();
+    return s;
+}
+
+__device__ __forceinline__ int64_t row_valid(const SoftmaxArgs& p, int64_t row) {
+    const int64_t v = p.valid_len != nullptr ? p.valid_len[row] : p.valid_all;
+    return v < 0 ? 0 : (v > p.width ? p.width : v);
+}
+
+// Loads the chunk's valid keys scaled (-inf for masked ones) and returns how many of its vectors are in range.
+__device__ __forceinline__ void load_chunk(const SoftmaxArgs& p, int64_t row, int chunk, int64_t valid,
+                                           float (&s)[kChunkVpt][4]) {
+    const float* xr = p.x + row * p.row_stride;
+    const int64_t v0 = chunk * (kChunk / 4);
+    const int64_t nvec = p.width / 4;
+    u32x4 raw[kChunkVpt];
+#pragma unroll
+    for (int k = 0; k < kChunkVpt; ++k) {
+        const int64_t v = v0 + threadIdx.x + k * kBlock;
+        if (v < nvec && v * 4 < valid) raw[k] = ld128(xr + v * 4);
+    }
+#pragma unroll
+    for (int k = 0; k < kChunkVpt; ++k) {
+        const int64_t v = v0 + threadIdx.x + k * kBlock;
+        if (v < nvec && v * 4 < valid) {
+            unpack<F32>(raw[k], s[k]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s[k][i] = v * 4 + i < valid ? s[k][i] * p.scale : -INFINITY;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s[k][i] = -INFINITY;
+        }
+    }
+}
+
+// Launch 1, grid (chunks, rows): partial[row][chunk] = (m_j as f32 bits, s_j as f64 bits).
+__global__ __launch_bounds__(kBlock) void softmax_partials(SoftmaxArgs p, int chunks, uint64_t* __restrict__ partial) {
+    __shared__ float lds_f[kBlock / 64];
+    __shared__ double lds_d[kBlock / 64];
+    const int64_t row = blockIdx.y;
+    const int chunk = blockIdx.x;
+    const int64_t valid = row_valid(p, row);
+    float s[kChunkVpt][4];
+    load_chunk(p, row, chunk, valid, s);
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kChunkVpt; ++k)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) m = fmaxf(m, s[k][i]);
+    m = block_max(m, lds_f);
+    // A chunk whose keys are all masked or -inf adds nothing against any finite M (and its exponentials relative to
+    // its own -inf maximum would be NaN), so its sum is 0.
+    double sum = 0.0;
+    if (m != -INFINITY) {
+#pragma unroll
+        for (int k = 0; k < kChunkVpt; ++k)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sum += static_cast<double>(exp_diff(s[k][i], m));
+    }
+    sum = block_sum(sum, lds_d);
+    if (threadIdx.x == 0) {
+        uint64_t* out = partial + (row * chunks + chunk) * 2;
+        out[0] = __float_as_uint(m);
+        out[1] = static_cast<uint64_t>(__double_as_longlong(sum));
+    }
+}
+
+// Launch 2, grid (chunks, rows): combines the row's partials and writes the chunk's outputs.
+__global__ __launch_bounds__(kBlock) void softmax_finish(SoftmaxArgs p, int chunks,
+                                                         const uint64_t* __restrict__ partial) {
+    __shared__ float s_M;
+    __shared__ double s_S;
+    const int64_t row = blockIdx.y;
+    const int chunk = blockIdx.x;
+    const int64_t valid = row_valid(p, row);
+    float s[kChunkVpt][4];
+    load_chunk(p, row, chunk, valid, s);
+    if (threadIdx.x < 64) {
+        const int j = threadIdx.x;
+        const uint64_t* pr = partial + row * chunks * 2;
+        const float mj = j < chunks ? __uint_as_float(static_cast<uint32_t>(pr[2 * j])) : -INFINITY;
+        const double sj = j < chunks ? __longlong_as_double(static_cast<long long>(pr[2 * j + 1])) : 0.0;
+        const float M = group_reduce<64, OpMax>(mj);
+        // M = -inf: every key masked or -inf; cpu-ref's exp(-inf - (-inf)) makes the row NaN.
+        const double t = mj != -INFINITY ? sj * exp(static_cast<double>(mj) - static_cast<double>(M))
+                                         : (M == -INFINITY && j < chunks ? static_cast<double>(NAN) : 0.0);
+        const double S = group_sum_f64<64>(t);
+        if (j == 0) {
+            s_M = M;
+            s_S = S;
+        }
+    }
+    __syncthreads();
+    const float M = s_M;
+    const double rinv = 1.0 / s_S;
+    float* yr = p.y + row * p.row_stride;
+    const int64_t v0 = chunk * (kChunk / 4);
+    const int64_t nvec = p.width / 4;
+#pragma unroll
+    for (int k = 0; k < kChunkVpt; ++k) {
+        const int64_t v = v0 + threadIdx.x + k * kBlock;
+        if (v < nvec) {
+            float o[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                // masked keys: exp(-inf - M) = 0 (NaN when the sum is)
+                const float e = s[k][i] == -INFINITY ? 0.0f : exp_diff(s[k][i], M);
+                o[i] = static_cast<float>(static_cast<double>(e) * rinv);
+            }
+            st128_nt(yr + v * 4, pack<F32>(o));
+        }
+    }
+}
+
+int64_t split_chunks(int64_t rows, int64_t width) {
+    const int64_t chunks = (width + kChunk - 1) / kChunk;
+    // Split only rows whose one-workgroup form would leave the chip mostly idle.
+    if (chunks < 2 || chunks > kMaxChunks || rows > kMaxRows || rows * 4 >= 1024 || width % 4 != 0) return 0;
+    return chunks;
+}
+
+size_t split_scratch_bytes(int64_t rows, int64_t chunks) {
+    return (static_cast<size_t>(rows * chunks) * 16 + 255) / 256 * 256;
+}
+
 template <int LPR>
 int go_vec(hipStream_t s, const SoftmaxArgs& p, int nv) {
     constexpr int BLOCK = LPR > kBlock ? LPR : kBlock;
@@ -183,8 +337,20 @@ int go_vec(hipStream_t s, const SoftmaxArgs& p, int nv) {
 
 constexpr int kMaxNv = 8;
 
-int launch_softmax(hipStream_t s, const SoftmaxArgs& p) {
+int launch_softmax(hipStream_t s, const SoftmaxArgs& p, void* scratch) {
     if (p.rows == 0) return XS_HIP_OK;
+    const int64_t chunks = split_chunks(p.rows, p.width);
+    if (scratch != nullptr && chunks > 0 && aligned16(p.x) && aligned16(p.y) && p.row_stride % 4 == 0) {
+        if (reinterpret_cast<uintptr_t>(scratch) % 16 != 0)
+            return fail(XS_HIP_EINVAL, "xs_hip_softmax_masked: scratch must be 16-byte aligned");
+        auto* partial = static_cast<uint64_t*>(scratch);
+        const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(p.rows));
+        softmax_partials<<<grid, kBlock, 0, s>>>(p, static_cast<int>(chunks), partial);
+        int rc = check_launch("xs_hip_softmax_masked");
+        if (rc != XS_HIP_OK) return rc;
+        softmax_finish<<<grid, kBlock, 0, s>>>(p, static_cast<int>(chunks), partial);
+        return check_launch("xs_hip_softmax_masked");
+    }
     // The in-register kernel needs whole 128-bit vectors; the three-pass kernel handles y aliasing x by reading the
     // row before writing it, the in-register one trivially (each lane reads its values before writing them).
     const bool vec = p.width % 4 == 0 && p.row_stride % 4 == 0 && aligned16(p.x) && aligned16(p.y);
@@ -222,18 +388,24 @@ int xs_hip_softmax(void* stream, const float* x, float* y, int64_t rows, int64_t
     if (rows == 0) return XS_HIP_OK;
     if (x == nullptr || y == nullptr) return fail(XS_HIP_EINVAL, "xs_hip_softmax: null buffer");
     const SoftmaxArgs p{x, y, rows, width, width, 1.0f, nullptr, width};
-    return launch_softmax(as_stream(stream), p);
+    return launch_softmax(as_stream(stream), p, nullptr);
+}
+
+size_t xs_hip_softmax_scratch(int64_t rows, int64_t width) {
+    if (rows <= 0 || width <= 0) return 0;
+    const int64_t chunks = split_chunks(rows, width);
+    return chunks > 0 ? split_scratch_bytes(rows, chunks) : 0;
 }
 
 int xs_hip_softmax_masked(void* stream, const float* x, float* y, int64_t rows, int64_t width, int64_t row_stride,
-                          float scale, const int64_t* valid_len, int64_t valid_len_all) {
+                          float scale, const int64_t* valid_len, int64_t valid_len_all, void* scratch) {
     if (rows < 0 || width <= 0 || rows > 0x7fffffffLL || row_stride < width)
         return fail(XS_HIP_EINVAL, "xs_hip_softmax_masked: " + std::to_string(rows) + " rows of width " +
                                        std::to_string(width) + " with row stride " + std::to_string(row_stride));
     if (rows == 0) return XS_HIP_OK;
     if (x == nullptr || y == nullptr) return fail(XS_HIP_EINVAL, "xs_hip_softmax_masked: null buffer");
     const SoftmaxArgs p{x, y, rows, width, row_stride, scale, valid_len, valid_len_all};
-    return launch_softmax(as_stream(stream), p);
+    return launch_softmax(as_stream(stream), p, scratch);
 }
 
 }  // extern "C"

@@ -12,9 +12,9 @@
 // comparator is not a strict weak order with NaN, so its result there is unspecified).
 //
 // k = 1: a row is cut into chunks of kChunk values; a block reduces one chunk (one 128-bit load per lane, DPP within
-// waves, one LDS stage across waves) and, when a row has several chunks, publishes its (value, index) to scratch and
-// bumps the row's arrival counter; the block that arrives last reduces the row's partials, writes the result and
-// resets the counter to zero. No block ever waits on another, so the launch needs no co-residency.
+// waves, one LDS stage across waves). A row of one chunk is done there; otherwise each chunk's (value, index) goes to
+// scratch and a second launch, one block per row, reduces the row's partials -- no atomics and no waiting between
+// workgroups.
 // k > 1: one block per row picks the k winners one after another, each pass finding the best element strictly after
 // the previous winner in the order above (k passes over the row, the later ones from cache).
 #include <cfloat>
@@ -26,11 +26,7 @@ namespace xs_hip {
 namespace {
 
 constexpr int kChunk = 1024;  // values per block for k = 1: one 128-bit vector per lane
-// Scratch layout for k = 1 over several chunks: arrival counters for up to kMaxRows rows at offset 0 (they must be zero
-// when a call starts, and every call leaves the ones it used zero again), then the partials, which need no initial
-// value. Fixing the counters' place makes one zero-filled scratch reusable by calls of any shape.
 constexpr int64_t kMaxRows = 65535;  // grid.y
-constexpr size_t kCounterBytes = 65536 * 4;
 
 // A (value, index) partial as one 64-bit word: the value's bits low, the index high, so it moves with one atomic.
 __device__ __forceinline__ uint64_t pack_best(float v, int32_t i) {
@@ -88,10 +84,10 @@ __device__ __forceinline__ void block_best(float& v, int32_t& i) {
     __syncthreads();
 }
 
-// grid (chunks, rows). counters [rows] u32 and partials [rows][chunks] (packed value and index) in scratch.
+// grid (chunks, rows). A row of one chunk writes its result; otherwise partials [rows][chunks] (packed value, index).
 __global__ __launch_bounds__(kBlock) void argmax_chunks(const float* __restrict__ x, float* __restrict__ values,
                                                         int32_t* __restrict__ indices, int64_t width, int chunks,
-                                                        uint64_t* __restrict__ partials, unsigned* __restrict__ counters) {
+                                                        uint64_t* __restrict__ partials) {
     const int64_t row = blockIdx.y;
     const int chunk = blockIdx.x;
     const float* xr = x + row * width;
@@ -114,7 +110,7 @@ __global__ __launch_bounds__(kBlock) void argmax_chunks(const float* __restrict_
     } else {
         for (int k = 0; k < 4; ++k) {
             const int64_t j = idx + k;
-            if (j < width && j < start + kChunk) {
+            if (j < width) {
                 const float v = xr[j];
                 if (better(v, static_cast<int32_t>(j), bv, bi)) {
                     bv = v;
@@ -124,32 +120,28 @@ __global__ __launch_bounds__(kBlock) void argmax_chunks(const float* __restrict_
         }
     }
     block_best(bv, bi);
+    if (threadIdx.x != 0) return;
     if (chunks == 1) {
-        if (threadIdx.x == 0) {
-            if (bi == INT32_MAX) {  // no non-NaN value
-                bi = 0;
-                bv = xr[0];
-            }
-            values[row] = bv;
-            indices[row] = bi;
+        if (bi == INT32_MAX) {  // no non-NaN value
+            bi = 0;
+            bv = xr[0];
         }
-        return;
+        values[row] = bv;
+        indices[row] = bi;
+    } else {
+        partials[row * chunks + chunk] = pack_best(bv, bi);
     }
-    __shared__ bool last;
-    if (threadIdx.x == 0) {
-        __hip_atomic_store(&partials[row * chunks + chunk], pack_best(bv, bi), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-        __threadfence();  // release the partial before the arrival is counted
-        const unsigned prev = __hip_atomic_fetch_add(&counters[row], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        last = prev == static_cast<unsigned>(chunks - 1);
-    }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();  // acquire: every other block's partial is visible
-    bv = -INFINITY;
-    bi = INT32_MAX;
+}
+
+// grid (rows): the best of a row's partials.
+__global__ __launch_bounds__(kBlock) void argmax_final(const float* __restrict__ x, float* __restrict__ values,
+                                                       int32_t* __restrict__ indices, int64_t width, int chunks,
+                                                       const uint64_t* __restrict__ partials) {
+    const int64_t row = blockIdx.x;
+    float bv = -INFINITY;
+    int32_t bi = INT32_MAX;
     for (int c = threadIdx.x; c < chunks; c += kBlock) {
-        const uint64_t b = __hip_atomic_load(&partials[row * chunks + c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t b = partials[row * chunks + c];
         const float v = __uint_as_float(static_cast<uint32_t>(b));
         const int32_t i = static_cast<int32_t>(static_cast<uint32_t>(b >> 32));
         if (better(v, i, bv, bi)) {
@@ -161,11 +153,10 @@ __global__ __launch_bounds__(kBlock) void argmax_chunks(const float* __restrict_
     if (threadIdx.x == 0) {
         if (bi == INT32_MAX) {
             bi = 0;
-            bv = xr[0];
+            bv = x[row * width];
         }
         values[row] = bv;
         indices[row] = bi;
-        __hip_atomic_store(&counters[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -217,7 +208,7 @@ size_t xs_hip_topk_scratch(int64_t rows, int64_t width, int64_t k) {
     if (rows <= 0 || width <= 0 || k != 1) return 0;
     const int64_t chunks = argmax_chunks_of(width);
     if (chunks <= 1) return 0;
-    return kCounterBytes + align_up(static_cast<size_t>(rows * chunks) * sizeof(uint64_t), 256);
+    return align_up(static_cast<size_t>(rows * chunks) * sizeof(uint64_t), 256);
 }
 
 int xs_hip_topk(void* stream, const float* x, float* values, int32_t* indices, int64_t rows, int64_t width, int64_t k,
@@ -235,18 +226,20 @@ int xs_hip_topk(void* stream, const float* x, float* values, int32_t* indices, i
         if (rows > kMaxRows || chunks > INT32_MAX)
             return fail(XS_HIP_EUNSUPPORTED, "xs_hip_topk: more than 65535 rows in one call");
         uint64_t* partials = nullptr;
-        unsigned* counters = nullptr;
         if (chunks > 1) {
             if (scratch == nullptr)
                 return fail(XS_HIP_EINVAL, "xs_hip_topk: argmax over rows of " + std::to_string(width) +
-                                               " needs xs_hip_topk_scratch bytes of zero-filled scratch");
-            if (reinterpret_cast<uintptr_t>(scratch) % 256 != 0)
-                return fail(XS_HIP_EINVAL, "xs_hip_topk: scratch must be 256-byte aligned");
-            counters = static_cast<unsigned*>(scratch);
-            partials = reinterpret_cast<uint64_t*>(static_cast<char*>(scratch) + kCounterBytes);
+                                               " needs xs_hip_topk_scratch bytes of scratch");
+            if (reinterpret_cast<uintptr_t>(scratch) % 8 != 0)
+                return fail(XS_HIP_EINVAL, "xs_hip_topk: scratch must be 8-byte aligned");
+            partials = static_cast<uint64_t*>(scratch);
         }
         argmax_chunks<<<dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(rows)), kBlock, 0, s>>>(
-            x, values, indices, width, static_cast<int>(chunks), partials, counters);
+            x, values, indices, width, static_cast<int>(chunks), partials);
+        int rc = check_launch("xs_hip_topk");
+        if (rc != XS_HIP_OK || chunks == 1) return rc;
+        argmax_final<<<static_cast<unsigned>(rows), kBlock, 0, s>>>(x, values, indices, width, static_cast<int>(chunks),
+                                                                     partials);
         return check_launch("xs_hip_topk");
     }
     if (rows > INT32_MAX) return fail(XS_HIP_EUNSUPPORTED, "xs_hip_topk: too many rows");

@@ -92,15 +92,18 @@ _SIGS = {
     "xs_hip_rms_norm": [_P, _INT, _P, _P, _P, _INT, _P, _I64, _I64, _F],
     "xs_hip_add_rms_norm": [_P, _P, _P, _P, _P, _P, _INT, _P, _I64, _I64, _F],
     "xs_hip_softmax": [_P, _P, _P, _I64, _I64],
-    "xs_hip_softmax_masked": [_P, _P, _P, _I64, _I64, _I64, _F, _P, _I64],
+    "xs_hip_softmax_masked": [_P, _P, _P, _I64, _I64, _I64, _F, _P, _I64, _P],
+    "xs_hip_softmax_scratch": [_I64, _I64],
     "xs_hip_topk_scratch": [_I64, _I64, _I64],
     "xs_hip_topk": [_P, _P, _P, _P, _I64, _I64, _I64, _P],
     "xs_hip_rope": [_P, _INT, _P, _INT, _P, _P, _INT, _P, _I64, _I64, _I64, _I64, _I64, _P],
+    "xs_hip_rope2": [_P, _INT, _P, _P, _I64, _P, _P, _I64, _INT, _P, _P, _INT, _I64, _I64, _I64, _I64, _P],
     "xs_hip_quantize_kv": [_P, _INT, _INT, _P, _P, _P, _I64, _I64],
     "xs_hip_dequantize_kv": [_P, _INT, _P, _P, _INT, _P, _I64, _I64],
     "xs_hip_copy": [_P, _P, _P, C.c_size_t],
 }
-_RESTYPES = {"xs_hip_topk_scratch": C.c_size_t, "xs_hip_last_error": C.c_char_p}
+_RESTYPES = {"xs_hip_topk_scratch": C.c_size_t, "xs_hip_softmax_scratch": C.c_size_t,
+             "xs_hip_last_error": C.c_char_p}
 
 _lib_handle = None
 
@@ -305,35 +308,46 @@ def softmax(x: DeviceTensor, stream=None) -> DeviceTensor:
     return y
 
 
-def softmax_masked(x: DeviceTensor, scale: float, valid_len, stream=None) -> DeviceTensor:
-    """softmax(x * scale) with keys >= valid_len masked to -inf (exactly 0 out); valid_len an int for every row or
-    a DeviceTensor of i64 per row."""
-    width = x.shape[-1]
-    rows = x.numel // width
-    y = DeviceTensor.empty(F32, x.shape)
-    if isinstance(valid_len, DeviceTensor):
-        call("xs_hip_softmax_masked", stream, C.c_void_p(x.ptr), C.c_void_p(y.ptr), rows, width, width,
-             C.c_float(scale), C.c_void_p(valid_len.ptr), 0)
-    else:
-        call("xs_hip_softmax_masked", stream, C.c_void_p(x.ptr), C.c_void_p(y.ptr), rows, width, width,
-             C.c_float(scale), None, int(valid_len))
-    return y
-
-
-class TopkScratch:
-    """Zero-filled scratch for xs_hip_topk, grown on demand (sycl_backend.cpp:286-292 keeps one per session)."""
+class Scratch:
+    """A zero-filled device scratch grown on demand, for the entry points that combine partials across workgroups
+    (the reference keeps one such buffer per session for top-k, sycl_backend.cpp:286-292)."""
 
     def __init__(self):
         self.buf: Optional[DeviceBuffer] = None
 
-    def get(self, rows: int, width: int, k: int) -> int:
-        need = lib().xs_hip_topk_scratch(rows, width, k)
+    def ptr(self, need: int) -> int:
         if need == 0:
             return 0
         if self.buf is None or self.buf.nbytes < need:
             self.buf = DeviceBuffer(need)
             call("xs_hip_memset", C.c_void_p(self.buf.ptr), 0, C.c_size_t(need), None)
+            synchronize()
         return self.buf.ptr
+
+
+_softmax_scratch = Scratch()
+
+
+def softmax_masked(x: DeviceTensor, scale: float, valid_len, scratch: Optional[Scratch] = _softmax_scratch,
+                   stream=None) -> DeviceTensor:
+    """softmax(x * scale) with keys >= valid_len masked to -inf (exactly 0 out); valid_len an int for every row or
+    a DeviceTensor of i64 per row. With scratch=None each row stays in one workgroup."""
+    width = x.shape[-1]
+    rows = x.numel // width
+    y = DeviceTensor.empty(F32, x.shape)
+    sp = 0 if scratch is None else scratch.ptr(lib().xs_hip_softmax_scratch(rows, width))
+    if isinstance(valid_len, DeviceTensor):
+        call("xs_hip_softmax_masked", stream, C.c_void_p(x.ptr), C.c_void_p(y.ptr), rows, width, width,
+             C.c_float(scale), C.c_void_p(valid_len.ptr), 0, C.c_void_p(sp))
+    else:
+        call("xs_hip_softmax_masked", stream, C.c_void_p(x.ptr), C.c_void_p(y.ptr), rows, width, width,
+             C.c_float(scale), None, int(valid_len), C.c_void_p(sp))
+    return y
+
+
+class TopkScratch(Scratch):
+    def get(self, rows: int, width: int, k: int) -> int:
+        return self.ptr(lib().xs_hip_topk_scratch(rows, width, k))
 
 
 _default_scratch = TopkScratch()
@@ -366,6 +380,21 @@ def rope(x: DeviceTensor, positions: DeviceTensor, inv_freq: DeviceTensor, rotar
          C.c_void_p(inv_freq.ptr), y.dtype, C.c_void_p(y.ptr), tokens, heads, dim, rotary_dim, sections,
          C.c_void_p(pair_axes.ptr if pair_axes is not None else 0))
     return y
+
+
+def rope_qk(q: DeviceTensor, k: DeviceTensor, positions: DeviceTensor, inv_freq: DeviceTensor, rotary_dim: int = 0,
+            y_dtype: Optional[int] = None, in_place: bool = False, stream=None) -> Tuple[DeviceTensor, DeviceTensor]:
+    """RoPE of q [T, Hq, D] and k [T, Hk, D] in one launch (xs_hip_rope2), each as rope() rotates it."""
+    tokens, hq, dim = q.shape
+    hk = k.shape[1]
+    sections = 1 if len(positions.shape) == 1 else positions.shape[1]
+    yd = q.dtype if y_dtype is None else y_dtype
+    yq = q if in_place else DeviceTensor.empty(yd, q.shape)
+    yk = k if in_place else DeviceTensor.empty(yd, k.shape)
+    call("xs_hip_rope2", stream, q.dtype, C.c_void_p(q.ptr), C.c_void_p(yq.ptr), hq, C.c_void_p(k.ptr),
+         C.c_void_p(yk.ptr), hk, positions.dtype, C.c_void_p(positions.ptr), C.c_void_p(inv_freq.ptr), yd, tokens, dim,
+         rotary_dim, sections, None)
+    return yq, yk
 
 
 def quantize_kv(x: DeviceTensor, stream=None) -> Tuple[DeviceTensor, DeviceTensor]:
