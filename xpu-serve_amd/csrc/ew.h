@@ -3,8 +3,11 @@
 // y[r, c] = f(a[r, c], b[r, c], bias[c]) for r < rows, c < cols, with a row stride per operand (a row stride of 0
 // repeats a row vector over the leading dims). f is a compile-time op (and activation), so the per-element code holds
 // nothing but the arithmetic. Each lane handles chunks of 8 consecutive elements of a row -- one or two 128-bit loads
-// per operand, one or two 128-bit stores -- and keeps U chunks in flight; the flat chunk index is split into (row,
-// column) with a multiply-high division by the chunk count of a row.
+// per operand, one or two 128-bit stores -- and keeps U chunks in flight. A workgroup takes one contiguous tile of
+// kBlock * U chunks (lane t its chunks t, t + kBlock, ...) and the grid covers the whole tensor, so the workgroups in
+// flight at any moment read one contiguous window of memory, which HBM serves faster than the scattered windows of a
+// grid-stride loop. The flat chunk index is split into (row, column) with a multiply-high division by the chunk count
+// of a row.
 //
 // Arithmetic: operands widened exactly to f32, each reference op rounded once in f32 in the reference's order; the
 // build disables FMA contraction, so a + b * c rounds twice as in cpu-ref. SiLU and sigmoid take a fast f32 form
@@ -146,8 +149,9 @@ __global__ __launch_bounds__(kBlock) void ew2d_vec(Ew2D e, uint32_t units, FastD
     const SX* b = static_cast<const SX*>(e.b);
     const SX* c = static_cast<const SX*>(e.c);
     SY* y = static_cast<SY*>(e.y);
-    const uint32_t stride = gridDim.x * kBlock;
-    for (uint32_t u0 = blockIdx.x * kBlock + threadIdx.x; u0 < units; u0 += U * stride) {
+    constexpr uint32_t stride = kBlock;
+    {
+        const uint32_t u0 = blockIdx.x * (kBlock * U) + threadIdx.x;
         float fa[U][8], fb[U][8], fc[U][8];
         int64_t row[U], col[U];
 #pragma unroll
@@ -213,8 +217,8 @@ int launch(hipStream_t s, const Ew2D& e, const char* what) {
     const int64_t cpr = e.cols / 8;
     const int64_t units = e.rows * cpr;
     if (vec && units < (int64_t{1} << 31)) {
-        constexpr int U = 4;
-        const unsigned grid = grid_for(units, kBlock * U);
+        constexpr int U = 2;
+        const unsigned grid = static_cast<unsigned>((units + kBlock * U - 1) / (kBlock * U));
         ew2d_vec<TX, TY, OP, ACT, U><<<grid, kBlock, 0, s>>>(e, static_cast<uint32_t>(units),
                                                             FastDiv32(static_cast<uint32_t>(cpr)),
                                                             static_cast<uint32_t>(cpr));

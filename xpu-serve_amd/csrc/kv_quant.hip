@@ -18,6 +18,10 @@
 // Dequantize layout: a unit is 8 codes (one 64-bit load) and their 8 outputs (one 128-bit store for f16/bf16, two
 // for f32); consecutive lanes take consecutive units, so loads and stores are contiguous across the wave, and each
 // lane keeps U units (codes and row scales) in flight.
+//
+// Both kernels give each workgroup one contiguous tile of the tensor and launch as many workgroups as there are
+// tiles: the workgroups in flight then read one contiguous window of memory, which HBM serves faster than the
+// scattered windows of a grid-stride loop.
 #include "common.h"
 
 namespace xs_hip {
@@ -49,13 +53,14 @@ __global__ __launch_bounds__(kBlock) void quantize_i8_vec(const typename T::stor
                                                           int64_t rows, int64_t width) {
     constexpr int VEC = vec_elems<T>();
     constexpr int RPW = 64 / L;  // rows per wave
+    constexpr int WAVES = kBlock / 64;
     const int lane = threadIdx.x & 63;
     const int sub = lane / L;
     const int l = lane % L;
-    const int64_t waves = static_cast<int64_t>(gridDim.x) * (kBlock / 64);
-    const int64_t wave_id = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
-    const int64_t stride = waves * RPW;
-    for (int64_t base = wave_id * RPW + sub; base < rows; base += U * stride) {
+    // The block's tile: U * WAVES * RPW contiguous rows; wave w takes rows (u * WAVES + w) * RPW + sub.
+    constexpr int64_t stride = WAVES * RPW;
+    {
+        const int64_t base = static_cast<int64_t>(blockIdx.x) * (U * WAVES * RPW) + (threadIdx.x >> 6) * RPW + sub;
         u32x4 raw[U][VPL];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -123,8 +128,9 @@ __global__ __launch_bounds__(kBlock) void dequantize_i8_vec(const uint64_t* __re
                                                             const float* __restrict__ scales,
                                                             typename Y::storage* __restrict__ out, uint32_t units,
                                                             FastDiv32 units_per_row) {
-    const uint32_t stride = gridDim.x * kBlock;
-    for (uint32_t v0 = blockIdx.x * kBlock + threadIdx.x; v0 < units; v0 += U * stride) {
+    constexpr uint32_t stride = kBlock;
+    {
+        const uint32_t v0 = blockIdx.x * (kBlock * U) + threadIdx.x;
         uint64_t raw[U];
         float scale[U];
 #pragma unroll
@@ -175,10 +181,10 @@ int launch_quantize(hipStream_t s, const void* x, int8_t* codes, float* scales, 
     const bool vec_ok = row_bytes % 16 == 0 && aligned16(x) && (reinterpret_cast<uintptr_t>(codes) % 8 == 0) &&
                         (nvr & (nvr - 1)) == 0 && nvr >= 1 && nvr <= 64;
     const auto* xs = static_cast<const S*>(x);
-    constexpr int U = 4;
+    constexpr int U = 2;
     auto go = [&](auto kernel, int lanes) {
-        const int64_t rows_per_block = (kBlock / 64) * (64 / lanes);
-        const unsigned grid = grid_for(rows, static_cast<int>(rows_per_block * U));
+        const int64_t rows_per_tile = (kBlock / 64) * (64 / lanes) * U;
+        const unsigned grid = static_cast<unsigned>((rows + rows_per_tile - 1) / rows_per_tile);
         kernel<<<grid, kBlock, 0, s>>>(xs, codes, scales, rows, width);
         return check_launch("xs_hip_quantize_kv");
     };
@@ -207,7 +213,8 @@ int launch_dequantize(hipStream_t s, const int8_t* codes, const float* scales, v
     auto* o = static_cast<S*>(out);
     if (width % 8 == 0 && reinterpret_cast<uintptr_t>(codes) % 8 == 0 && aligned16(out) && n / 8 < (int64_t{1} << 32)) {
         const uint32_t units = static_cast<uint32_t>(n / 8);
-        dequantize_i8_vec<Y, 4><<<grid_for(units, kBlock * 4), kBlock, 0, s>>>(
+        constexpr int U = 2;
+        dequantize_i8_vec<Y, U><<<(units + kBlock * U - 1) / (kBlock * U), kBlock, 0, s>>>(
             reinterpret_cast<const uint64_t*>(codes), scales, o, units, FastDiv32(static_cast<uint32_t>(width / 8)));
     } else {
         dequantize_i8_any<Y><<<grid_for(n, kBlock * 4), kBlock, 0, s>>>(codes, scales, o, n, width);

@@ -184,7 +184,7 @@ int go_vec(hipStream_t s, const NormArgs& p, int nv) {
 // kTargetWaves waves on the chip (few rows get more lanes each, so the whole chip pulls on HBM), or keeps at most two
 // vectors per lane; rows wider than 1024 lanes * kMaxNv vectors take the two-pass kernel.
 constexpr int kMaxNv = 8;
-constexpr int64_t kTargetWaves = 2048;  // 8 per CU on 256 CUs
+constexpr int64_t kTargetWaves = 4096;  // 16 per CU on 256 CUs
 
 template <typename TX, typename TY>
 int launch_norm(hipStream_t s, const NormArgs& p) {

@@ -8,12 +8,14 @@
 // (src/backend/sycl/sycl_kernels.h:114-116, sycl_kernels.cpp:1678-1717), which uses an f32 angle; this kernel keeps the
 // reference CPU path's f64 angle, so its outputs round from the same f64 values cpu-ref computes.
 //
-// Layout: a block takes a tile of TT tokens. Its threads first fill an LDS table of (cos, sin) in f64 for the tile's
-// TT x pairs entries -- one sincos per (token, pair), shared by every head of the token; one f64 pair of padding every
-// 8 entries spreads the 8 entries a wave reads at once over distinct LDS banks. Then each thread owns one unit slot
-// (head, VEC consecutive pairs) for the whole tile and walks the tile's tokens two at a time, issuing both tokens'
-// 128-bit loads of x1 and x2 before rotating; the rotation is an f64 FMA of the exactly widened inputs, rounded to f32
-// and then to y's dtype, as cpu-ref's f64 expression is.
+// Layout: a block of 256 threads takes a tile of TT tokens (about four units of work per thread). It first fills an LDS
+// table of (cos, sin) in f64 for the tile's TT x pairs entries -- one sincos per (token, pair), shared by every head of
+// the token; one f64 pair of padding every 8 entries spreads the 8 entries a wave reads at once over distinct LDS
+// banks. Then thread t walks the tile's units t, t + 256, ... -- a unit is (token, head, VEC consecutive pairs): one
+// 128-bit load of x1 and one of x2, the rotation, two stores -- so a wave's units are 64 consecutive ones and its loads
+// cover whole half-rows of consecutive heads. The rotation is an f64 FMA of the exactly widened inputs, rounded to f32
+// and then to y's dtype, as cpu-ref's f64 expression is. (Measured on MI355X: 256-thread blocks beat 320- and
+// 640-thread ones that give each thread one fixed unit, and beat splitting a head row across lanes.)
 #include <cmath>
 
 #include "common.h"
@@ -99,7 +101,7 @@ __device__ __forceinline__ void rotate(const float* x1, const float* x2, const d
 }
 
 template <typename TX, typename TY, typename I, int VEC>
-__global__ __launch_bounds__(kBlock) void rope_kernel(RopeArgs a) {
+__global__ __launch_bounds__(kBlock) void rope_kernel(RopeArgs a, FastDiv32 pv_div) {
     using SX = typename TX::storage;
     using SY = typename TY::storage;
     __shared__ double2 table[kTableSlots];
@@ -110,13 +112,15 @@ __global__ __launch_bounds__(kBlock) void rope_kernel(RopeArgs a) {
     const bool axes = a.pair_axes != nullptr;
     const int64_t width = axes ? a.rotary : a.rotary / a.sections;  // section width
     const int64_t half = width / 2;
+    const int heads = static_cast<int>(a.heads + a.heads2);
+    const int pv_per_head = static_cast<int>(pairs / VEC);
+    const int upt = heads * pv_per_head;  // rotation units per token
 
     // (cos, sin) of every (token, pair) of the tile.
     const int entries = tt_n * static_cast<int>(pairs);
     for (int e = threadIdx.x; e < entries; e += kBlock) {
-        const int tt = e / static_cast<int>(pairs);
-        const int64_t p = e - static_cast<int64_t>(tt) * pairs;
-        const int64_t t = t0 + tt;
+        const int te = e / static_cast<int>(pairs);
+        const int64_t p = e - static_cast<int64_t>(te) * pairs;
         int64_t sec, i;
         if (axes) {
             // Axes outside [0, sections) are a caller error the host cannot see in device memory; clamp so the read
@@ -128,84 +132,44 @@ __global__ __launch_bounds__(kBlock) void rope_kernel(RopeArgs a) {
             sec = p / half;
             i = p - sec * half;
         }
-        const double pos = static_cast<double>(pos_at<I>(a.pos, t * a.sections + sec));
+        const double pos = static_cast<double>(pos_at<I>(a.pos, (t0 + te) * a.sections + sec));
         const double angle = pos * static_cast<double>(a.inv_freq[i]);
-        double s, c;
-        sincos(angle, &s, &c);
-        table[table_slot(e)] = make_double2(c, s);
+        double sn, cs;
+        sincos(angle, &sn, &cs);
+        table[table_slot(e)] = make_double2(cs, sn);
     }
     __syncthreads();
 
-    const int heads = static_cast<int>(a.heads + a.heads2);
-    const int pv_per_head = static_cast<int>(pairs / VEC);
-    const int upt = heads * pv_per_head;  // rotation units per token
-    if (upt <= kBlock) {
-        // Each thread owns one (head, pair vector) slot; the block's threads cover tpp tokens per pass.
-        const int tpp = kBlock / upt;
-        const int slot = threadIdx.x % upt;
-        const int t_off = threadIdx.x / upt;
-        if (t_off < tpp) {
-            const int h = slot / pv_per_head;
-            const int p0 = (slot - h * pv_per_head) * VEC;
-            int64_t c1 = p0;
-            if (!axes) {
-                const int64_t sec = p0 / half;
-                c1 = sec * width + (p0 - sec * half);
-            }
-            for (int tt = t_off; tt < tt_n; tt += 2 * tpp) {
-                const int tt2 = tt + tpp;
-                const bool two = tt2 < tt_n;
-                const SX* x;
-                SY* y;
-                const int64_t base = head_at(a, t0 + tt, h, x, y) + c1;
-                const int64_t base2 = head_at(a, t0 + tt2, h, x, y) + c1;
-                float x1[VEC], x2[VEC], z1[VEC], z2[VEC];
-                load_n<TX, VEC>(x + base, x1);
-                load_n<TX, VEC>(x + base + half, x2);
-                if (two) {
-                    load_n<TX, VEC>(x + base2, z1);
-                    load_n<TX, VEC>(x + base2 + half, z2);
-                }
-                double2 cs[VEC];
-#pragma unroll
-                for (int k = 0; k < VEC; ++k) cs[k] = table[table_slot(tt * static_cast<int>(pairs) + p0 + k)];
-                float y1[VEC], y2[VEC];
-                rotate<VEC>(x1, x2, cs, y1, y2);
-                store_n<TY, VEC>(y + base, y1);
-                store_n<TY, VEC>(y + base + half, y2);
-                if (two) {
-#pragma unroll
-                    for (int k = 0; k < VEC; ++k) cs[k] = table[table_slot(tt2 * static_cast<int>(pairs) + p0 + k)];
-                    rotate<VEC>(z1, z2, cs, y1, y2);
-                    store_n<TY, VEC>(y + base2, y1);
-                    store_n<TY, VEC>(y + base2 + half, y2);
-                }
-            }
+    // Thread t takes units t, t + kBlock, ... of the tile; (token, slot) of the next unit follows from the last by
+    // adding kBlock to the slot and carrying whole tokens, so no unit needs a division.
+    int tt = threadIdx.x / upt;
+    int slot = threadIdx.x - tt * upt;
+    const int carry_t = kBlock / upt, carry_s = kBlock - carry_t * upt;
+    for (; tt < tt_n;) {
+        const int h = static_cast<int>(pv_div.div(static_cast<uint32_t>(slot)));
+        const int p0 = (slot - h * pv_per_head) * VEC;
+        int64_t c1 = p0;
+        if (!axes) {
+            const int64_t sec = p0 / half;
+            c1 = sec * width + (p0 - sec * half);
         }
-    } else {
-        const int rot_units = tt_n * upt;
-        for (int u = threadIdx.x; u < rot_units; u += kBlock) {
-            const int tt = u / upt;
-            const int rem = u - tt * upt;
-            const int h = rem / pv_per_head;
-            const int p0 = (rem - h * pv_per_head) * VEC;
-            int64_t c1 = p0;
-            if (!axes) {
-                const int64_t sec = p0 / half;
-                c1 = sec * width + (p0 - sec * half);
-            }
-            const SX* x;
-            SY* y;
-            const int64_t base = head_at(a, t0 + tt, h, x, y) + c1;
-            float x1[VEC], x2[VEC], y1[VEC], y2[VEC];
-            load_n<TX, VEC>(x + base, x1);
-            load_n<TX, VEC>(x + base + half, x2);
-            double2 cs[VEC];
+        const SX* x;
+        SY* y;
+        const int64_t base = head_at(a, t0 + tt, h, x, y) + c1;
+        float x1[VEC], x2[VEC], y1[VEC], y2[VEC];
+        load_n<TX, VEC>(x + base, x1);
+        load_n<TX, VEC>(x + base + half, x2);
+        double2 cs[VEC];
 #pragma unroll
-            for (int k = 0; k < VEC; ++k) cs[k] = table[table_slot(tt * static_cast<int>(pairs) + p0 + k)];
-            rotate<VEC>(x1, x2, cs, y1, y2);
-            store_n<TY, VEC>(y + base, y1);
-            store_n<TY, VEC>(y + base + half, y2);
+        for (int k = 0; k < VEC; ++k) cs[k] = table[table_slot(tt * static_cast<int>(pairs) + p0 + k)];
+        rotate<VEC>(x1, x2, cs, y1, y2);
+        store_n<TY, VEC>(y + base, y1);
+        store_n<TY, VEC>(y + base + half, y2);
+        tt += carry_t;
+        slot += carry_s;
+        if (slot >= upt) {
+            slot -= upt;
+            ++tt;
         }
     }
 
@@ -215,12 +179,12 @@ __global__ __launch_bounds__(kBlock) void rope_kernel(RopeArgs a) {
         const int64_t units = static_cast<int64_t>(tt_n) * heads * rest;
         for (int64_t u = threadIdx.x; u < units; u += kBlock) {
             const int64_t th = u / rest;
-            const int64_t tt = th / heads;
-            const int h = static_cast<int>(th - tt * heads);
-            const SX* x;
-            SY* y;
-            const int64_t at = head_at(a, t0 + tt, h, x, y) + a.rotary + (u - th * rest);
-            if (static_cast<const void*>(x) != static_cast<const void*>(y)) y[at] = TY::store(TX::load(x[at]));
+            const int64_t tu = th / heads;
+            const int hu = static_cast<int>(th - tu * heads);
+            const SX* xp;
+            SY* yp;
+            const int64_t at = head_at(a, t0 + tu, hu, xp, yp) + a.rotary + (u - th * rest);
+            if (static_cast<const void*>(xp) != static_cast<const void*>(yp)) yp[at] = TY::store(TX::load(xp[at]));
         }
     }
 }
@@ -233,17 +197,18 @@ int launch_rope(hipStream_t s, RopeArgs a) {
     const int64_t half = axes ? pairs : (a.rotary / a.sections) / 2;
     const bool vec = half % VEC == 0 && a.dim % VEC == 0 && aligned16(a.x) && aligned16(a.y) &&
                      (a.heads2 == 0 || (aligned16(a.x2) && aligned16(a.y2)));
-    // Tokens per block: four rotation units per thread, within the LDS table.
-    const int64_t units_per_token = (a.heads + a.heads2) * (pairs / (vec ? VEC : 1));
-    int64_t tt = units_per_token > 0 ? (4 * kBlock + units_per_token - 1) / units_per_token : 1;
-    if (tt < 1) tt = 1;
+    const int64_t pv = pairs / (vec ? VEC : 1);
+    const int64_t upt = (a.heads + a.heads2) * pv;  // rotation units per token
+    // Tile: about four units per thread (measured best on MI355X against two and eight), within the LDS table.
+    int64_t tt = (4 * kBlock + upt - 1) / upt;
     const int64_t max_tt = pairs > 0 ? kMaxTableEntries / pairs : 64;
     if (tt > max_tt) tt = max_tt;
-    if (tt > 64) tt = 64;
+    if (tt < 1) tt = 1;
     a.tile_tokens = static_cast<int>(tt);
     const unsigned grid = static_cast<unsigned>((a.tokens + tt - 1) / tt);
-    if (vec) rope_kernel<TX, TY, I, VEC><<<grid, kBlock, 0, s>>>(a);
-    else rope_kernel<TX, TY, I, 1><<<grid, kBlock, 0, s>>>(a);
+    const FastDiv32 pv_div(static_cast<uint32_t>(pv));
+    if (vec) rope_kernel<TX, TY, I, VEC><<<grid, kBlock, 0, s>>>(a, pv_div);
+    else rope_kernel<TX, TY, I, 1><<<grid, kBlock, 0, s>>>(a, pv_div);
     return check_launch("xs_hip_rope");
 }
 

@@ -58,19 +58,10 @@ int device_cus() {
 
 namespace {
 
-// y = x in 16-byte vectors, four in flight per lane per iteration.
+// y = x in 16-byte vectors, one per lane: a tile of kBlock vectors per workgroup, as many workgroups as tiles.
 __global__ __launch_bounds__(kBlock) void copy_kernel(const u32x4* __restrict__ x, u32x4* __restrict__ y, int64_t n) {
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
-    int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    for (; i + 3 * stride < n; i += 4 * stride) {
-        const u32x4 a = ld128_nt(x + i), b = ld128_nt(x + i + stride), c = ld128_nt(x + i + 2 * stride),
-                    d = ld128_nt(x + i + 3 * stride);
-        st128_nt(y + i, a);
-        st128_nt(y + i + stride, b);
-        st128_nt(y + i + 2 * stride, c);
-        st128_nt(y + i + 3 * stride, d);
-    }
-    for (; i < n; i += stride) st128_nt(y + i, ld128_nt(x + i));
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (i < n) st128_nt(y + i, ld128_nt(x + i));
 }
 
 }  // namespace
@@ -262,8 +253,9 @@ int xs_hip_copy(void* stream, const void* x, void* y, size_t bytes) {
         return fail(XS_HIP_EINVAL, "xs_hip_copy: needs non-null 16-byte aligned buffers and a multiple of 16 bytes, got " +
                                        std::to_string(bytes));
     const int64_t n = static_cast<int64_t>(bytes / 16);
-    copy_kernel<<<grid_for(n, kBlock * 4), kBlock, 0, as_stream(stream)>>>(static_cast<const u32x4*>(x),
-                                                                           static_cast<u32x4*>(y), n);
+    if ((n + kBlock - 1) / kBlock > 0x7fffffffLL) return fail(XS_HIP_EUNSUPPORTED, "xs_hip_copy: too many bytes");
+    copy_kernel<<<static_cast<unsigned>((n + kBlock - 1) / kBlock), kBlock, 0, as_stream(stream)>>>(
+        static_cast<const u32x4*>(x), static_cast<u32x4*>(y), n);
     return check_launch("xs_hip_copy");
 }
 

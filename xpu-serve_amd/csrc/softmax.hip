@@ -171,8 +171,8 @@ __global__ __launch_bounds__(kBlock) void softmax_any(SoftmaxArgs p) {
     }
 }
 
-constexpr int kChunkVpt = 4;                      // 128-bit vectors per lane in a chunk
-constexpr int64_t kChunk = kBlock * kChunkVpt * 4;  // keys per chunk: 4096
+constexpr int kChunkVpt = 1;                      // 128-bit vectors per lane in a chunk
+constexpr int64_t kChunk = kBlock * kChunkVpt * 4;  // keys per chunk: 1024
 constexpr int64_t kMaxRows = 65535;
 constexpr int kMaxChunks = 64;                      // the second launch combines a row's partials in one wave
 
