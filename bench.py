@@ -380,6 +380,18 @@ def cpu_baseline(seconds):
             "host_cpu": model, "nproc": os.cpu_count()}
 
 
+def measured_traffic():
+    """HBM bytes per launch of each workload kernel, read from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
+    (already scaled by the copy-kernel calibration recorded there). None where the summary is absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic_pmc_all_ops.md")
+    try:
+        text = open(path).read()
+        block = text.split("```json", 1)[1].split("```", 1)[0]
+        return json.loads(block)["traffic_bytes_per_launch"]
+    except (OSError, IndexError, ValueError, KeyError):
+        return {}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -408,7 +420,9 @@ def main():
         log(f"  {op.name}: {results[op.name]['us_per_call']} us/call, {results[op.name]['gb_s']} GB/s")
     X.call("xs_hip_stream_destroy", stream)
 
-    head = results.get("swiglu_bias") or next(iter(results.values()))
+    head_name = "swiglu_bias" if "swiglu_bias" in results else next(iter(results))
+    head = results[head_name]
+    traffic = measured_traffic().get(head_name)
     line = {
         "metric": METRIC,
         "value": head["gb_s"],
@@ -426,7 +440,8 @@ def main():
                                "gate/up/out bf16 [2048, 9728], bias bf16 [9728]",
                    "entry_point": "xs_hip_act_bias_mul_2d", "algorithmic_bytes_per_call": W.ALGO_BYTES["swiglu_bias"]},
         "roofline": {"bound": "hbm", "achieved": head["gb_s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": head["frac_of_peak"], "traffic": None,
+                     "frac": head["frac_of_peak"], "traffic": traffic,
+                     "traffic_source": "profiles/hbm_traffic_pmc_all_ops.md" if traffic else None,
                      "kernel": head["kernel"], "avg_launch_us": head["us_per_call"] / head["launches"]},
         "device": dev_name,
         "ops": results,

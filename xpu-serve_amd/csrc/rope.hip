@@ -116,6 +116,30 @@ __global__ __launch_bounds__(kBlock) void rope_kernel(RopeArgs a, FastDiv32 pv_d
     const int pv_per_head = static_cast<int>(pairs / VEC);
     const int upt = heads * pv_per_head;  // rotation units per token
 
+    // The thread's first unit is loaded before the table is built, so its HBM latency overlaps the sincos work.
+    int tt = threadIdx.x / upt;
+    int slot = threadIdx.x - tt * upt;
+    float x1[VEC], x2[VEC];
+    const SX* x = nullptr;
+    SY* y = nullptr;
+    int64_t base = 0;
+    int p0 = 0;
+    auto locate = [&]() {
+        const int h = static_cast<int>(pv_div.div(static_cast<uint32_t>(slot)));
+        p0 = (slot - h * pv_per_head) * VEC;
+        int64_t c1 = p0;
+        if (!axes) {
+            const int64_t sec = p0 / half;
+            c1 = sec * width + (p0 - sec * half);
+        }
+        base = head_at(a, t0 + tt, h, x, y) + c1;
+    };
+    if (tt < tt_n) {
+        locate();
+        load_n<TX, VEC>(x + base, x1);
+        load_n<TX, VEC>(x + base + half, x2);
+    }
+
     // (cos, sin) of every (token, pair) of the tile.
     const int entries = tt_n * static_cast<int>(pairs);
     for (int e = threadIdx.x; e < entries; e += kBlock) {
@@ -142,23 +166,16 @@ __global__ __launch_bounds__(kBlock) void rope_kernel(RopeArgs a, FastDiv32 pv_d
 
     // Thread t takes units t, t + kBlock, ... of the tile; (token, slot) of the next unit follows from the last by
     // adding kBlock to the slot and carrying whole tokens, so no unit needs a division.
-    int tt = threadIdx.x / upt;
-    int slot = threadIdx.x - tt * upt;
     const int carry_t = kBlock / upt, carry_s = kBlock - carry_t * upt;
+    bool first = true;
     for (; tt < tt_n;) {
-        const int h = static_cast<int>(pv_div.div(static_cast<uint32_t>(slot)));
-        const int p0 = (slot - h * pv_per_head) * VEC;
-        int64_t c1 = p0;
-        if (!axes) {
-            const int64_t sec = p0 / half;
-            c1 = sec * width + (p0 - sec * half);
+        if (!first) {
+            locate();
+            load_n<TX, VEC>(x + base, x1);
+            load_n<TX, VEC>(x + base + half, x2);
         }
-        const SX* x;
-        SY* y;
-        const int64_t base = head_at(a, t0 + tt, h, x, y) + c1;
-        float x1[VEC], x2[VEC], y1[VEC], y2[VEC];
-        load_n<TX, VEC>(x + base, x1);
-        load_n<TX, VEC>(x + base + half, x2);
+        first = false;
+        float y1[VEC], y2[VEC];
         double2 cs[VEC];
 #pragma unroll
         for (int k = 0; k < VEC; ++k) cs[k] = table[table_slot(tt * static_cast<int>(pairs) + p0 + k)];
