@@ -127,7 +127,9 @@ int xs_hip_device_info(int device, char* name, size_t name_len, uint64_t* memory
     const int rc = check_hip(hipGetDeviceProperties(&p, device), "hipGetDeviceProperties");
     if (rc != XS_HIP_OK) return rc;
     if (name != nullptr && name_len > 0) {
-        std::snprintf(name, name_len, "%s (%s)", p.name, p.gcnArchName);
+        // The marketing name can be empty (seen on MI355X boxes); the arch, CU count and memory always identify it.
+        std::snprintf(name, name_len, "%s%s%s, %d CUs, %.0f GiB", p.name, p.name[0] != '\0' ? " " : "", p.gcnArchName,
+                      p.multiProcessorCount, static_cast<double>(p.totalGlobalMem) / (1u << 30));
     }
     if (memory_bytes != nullptr) *memory_bytes = p.totalGlobalMem;
     if (compute_units != nullptr) *compute_units = p.multiProcessorCount;
