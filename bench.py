@@ -304,8 +304,8 @@ def op_kv_dequantize(inputs):
               "dequantize_i8_vec")
 
 
-def op_copy():
-    n = 256 << 20  # bytes per call: the kernel the hardware byte counters are calibrated against
+def op_copy(n=256 << 20):
+    """Bytes per call n (default 256 MiB): the kernel the hardware byte counters are calibrated against."""
     x0 = X.DeviceBuffer(n)
     X.call("xs_hip_memset", C.c_void_p(x0.ptr), 1, C.c_size_t(n), None)
 

@@ -551,3 +551,45 @@ def test_rope_scalar_path(ora):
     f = ora.rope_inv_freq(10000.0, 20, 10, 10)
     step("rope [9, 3, 20] scalar path")
     assert_f32_close(X.rope(dev(x), dev(pos), dev(f)).numpy(), ora.rope(x, pos, f), what="scalar rope")
+
+
+@pytest.mark.parametrize("xdt,shape", [(F32, (19, 4, 128)), (F16, (19, 3, 256)), (F32, (11, 2, 32)),
+                                       (BF16, (10, 7, 64)), (F32, (3, 65, 128))])
+def test_rope_row_kernel_shapes(ora, xdt, shape):
+    """Rows of 8, 16 and 32 vectors (the row-contiguous kernel's partner exchange by DPP and by shuffle), token
+    counts that leave a partial tile, and a token too wide for one tile (65 heads of 32 vectors: the per-pair kernel)."""
+    rng = np.random.default_rng(20)
+    x = ora.narrow(rng.standard_normal(shape).astype(np.float32), xdt)
+    dim = shape[2]
+    pos = rng.integers(0, 40000, shape[0]).astype(np.int32)
+    f = ora.rope_inv_freq(1e6, dim, dim // 2, dim // 2)
+    step(f"rope row kernel {shape} {DT[xdt]}")
+    y = X.rope(dev(x, xdt), dev(pos), dev(f)).numpy()
+    check_out(y, ora.rope(ora.widen(x, xdt), pos, f), xdt, ora, f"rope {shape}")
+
+
+@pytest.mark.parametrize("xdt,dim", [(F16, 64), (F32, 64), (F16, 128)])
+def test_rope_row_kernel_pair_axes(ora, xdt, dim):
+    """Pair axes (each pair rotated by one column of [T, 3] positions) through the row-contiguous kernel."""
+    rng = np.random.default_rng(21)
+    x = ora.narrow(rng.standard_normal((13, 4, dim)).astype(np.float32), xdt)
+    pos = rng.integers(0, 5000, (13, 3)).astype(np.int64)
+    axes = rng.integers(0, 3, dim // 2).astype(np.int32)
+    f = ora.rope_inv_freq(10000.0, dim, dim // 2, dim // 2)
+    step(f"rope row kernel pair axes [13, 4, {dim}] {DT[xdt]}")
+    y = X.rope(dev(x, xdt), dev(pos), dev(f), 0, dev(axes)).numpy()
+    check_out(y, ora.rope(ora.widen(x, xdt), pos, f, 0, axes), xdt, ora, "rope pair axes")
+
+
+def test_rope_qk_fused_odd_shapes(ora):
+    """Q and K of different head counts over a token count that is no multiple of the tile, f32 and bf16."""
+    rng = np.random.default_rng(22)
+    for xdt in (F32, BF16):
+        xq = ora.narrow(rng.standard_normal((37, 6, 64)).astype(np.float32), xdt)
+        xk = ora.narrow(rng.standard_normal((37, 2, 64)).astype(np.float32), xdt)
+        pos = (np.arange(37, dtype=np.int64) * 97) % 3001
+        f = ora.rope_inv_freq(1e6, 64, 32, 32)
+        step(f"rope2 [37, 6+2, 64] {DT[xdt]}")
+        yq, yk = X.rope_qk(dev(xq, xdt), dev(xk, xdt), dev(pos), dev(f))
+        check_out(yq.numpy(), ora.rope(ora.widen(xq, xdt), pos, f), xdt, ora, "rope2 q")
+        check_out(yk.numpy(), ora.rope(ora.widen(xk, xdt), pos, f), xdt, ora, "rope2 k")

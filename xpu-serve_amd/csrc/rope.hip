@@ -8,14 +8,17 @@
 // (src/backend/sycl/sycl_kernels.h:114-116, sycl_kernels.cpp:1678-1717), which uses an f32 angle; this kernel keeps the
 // reference CPU path's f64 angle, so its outputs round from the same f64 values cpu-ref computes.
 //
-// Layout: a block of 256 threads takes a tile of TT tokens (about four units of work per thread). It first fills an LDS
-// table of (cos, sin) in f64 for the tile's TT x pairs entries -- one sincos per (token, pair), shared by every head of
-// the token; one f64 pair of padding every 8 entries spreads the 8 entries a wave reads at once over distinct LDS
-// banks. Then thread t walks the tile's units t, t + 256, ... -- a unit is (token, head, VEC consecutive pairs): one
-// 128-bit load of x1 and one of x2, the rotation, two stores -- so a wave's units are 64 consecutive ones and its loads
-// cover whole half-rows of consecutive heads. The rotation is an f64 FMA of the exactly widened inputs, rounded to f32
-// and then to y's dtype, as cpu-ref's f64 expression is. (Measured on MI355X: 256-thread blocks beat 320- and
-// 640-thread ones that give each thread one fixed unit, and beat splitting a head row across lanes.)
+// Two kernels. The row-contiguous kernel (rope_rows_kernel, below) takes the common shapes -- rotary == dim, one
+// section or pair axes, rows of 8, 16 or 32 128-bit vectors: a block's loads and stores are those of a plain copy over
+// whole tokens of Q and K, and partner lanes swap half-rows through DPP. The per-pair kernel (rope_kernel) takes every
+// other shape (sections, partial rotary, odd widths): a block of 256 threads takes a tile of TT tokens (about four
+// units of work per thread). It first fills an LDS table of (cos, sin) in f64 for the tile's TT x pairs entries -- one
+// sincos per (token, pair), shared by every head of the token; one f64 pair of padding every 8 entries spreads the 8
+// entries a wave reads at once over distinct LDS banks. Then thread t walks the tile's units t, t + 256, ... -- a unit
+// is (token, head, VEC consecutive pairs): one 128-bit load of x1 and one of x2, the rotation, two stores. The rotation
+// is an f64 FMA of the exactly widened inputs, rounded to f32 and then to y's dtype, as cpu-ref's f64 expression is.
+// Measured on MI355X at the Q+K shape of 8192 tokens x (32 + 8) heads x 128, f16: the per-pair kernel 33.3 us, the
+// row-contiguous one 29.6 us, a plain copy of the same bytes 27.5 us.
 #include <cmath>
 
 #include "common.h"
@@ -206,8 +209,254 @@ __global__ __launch_bounds__(kBlock) void rope_kernel(RopeArgs a, FastDiv32 pv_d
     }
 }
 
+// ---- Row-contiguous kernel (rotary == dim, one section or pair axes, a row of R = dim / VEC 128-bit vectors with R
+// 8, 16 or 32) --------------------------------------------------------------------------------------------
+//
+// A block takes TT whole tokens: the rows of those tokens in x (heads) and then in x2 (heads2), which are two contiguous
+// runs of memory. Thread t reads vectors t, t + 256, ... of that run with one 128-bit load each -- the access pattern of
+// a plain copy, every wave instruction covering 1 KiB of consecutive bytes. Since 256 is a multiple of R, a thread's
+// vector sits at the same place v = t % R in every row it visits: lanes with v < R/2 hold x1 (the first half of the
+// row), and the partner lane t ^ (R/2) holds the x2 of the same pairs. The partners split the work: the "lo" lane
+// rotates the first VEC/2 pairs of the vector and the "hi" lane the last VEC/2, each after receiving the other's two
+// dwords of input, and they swap two dwords of results back so each stores its own vector. So each lane reads VEC/2
+// (cos, sin) entries from the LDS table per vector, and the rotation and roundings are the same f64 expression as the
+// kernel above.
+template <int M>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+    if constexpr (M == 8) {
+        // row_ror:8 within each 16-lane row is lane ^ 8.
+        return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), 0x128, 0xF,
+                                                                 0xF, false));
+    } else if constexpr (M == 1) {
+        return static_cast<uint32_t>(dpp_i<dpp::kQuadXor1>(static_cast<int>(v)));
+    } else if constexpr (M == 2) {
+        return static_cast<uint32_t>(dpp_i<dpp::kQuadXor2>(static_cast<int>(v)));
+    } else {
+        return static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), M, 64));
+    }
+}
+
+// Lanes selected by BankMask (4 lanes a bank, 4 banks a 16-lane row) take `src` of lane ^ 8; the others keep `own`.
+template <int BankMask>
+__device__ __forceinline__ uint32_t dpp_merge(uint32_t own, uint32_t src) {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(static_cast<int>(own), static_cast<int>(src), 0x128, 0xF, BankMask, false));
+}
+
+struct RowArgs {
+    const void* x;
+    void* y;
+    const void* x2;
+    void* y2;
+    const void* pos;
+    const float* inv_freq;
+    const int32_t* pair_axes;
+    int64_t tokens, sections;
+    int heads, heads2, pairs;  // pairs = dim / 2
+    int tile_tokens;
+    FastDiv32 row_vecs_a, row_vecs_b;  // dividers by heads * R and heads2 * R (vectors per token of each tensor)
+};
+
+template <typename TX, typename TY, typename I, int R, int NV>
+__global__ __launch_bounds__(kBlock) void rope_rows_kernel(RowArgs a) {
+    using SX = typename TX::storage;
+    using SY = typename TY::storage;
+    constexpr int VEC = vec_elems<TX>();
+    constexpr int H = VEC / 2;                      // pairs each partner rotates
+    constexpr int YW = H * sizeof(SY) / 4;          // dwords of H outputs
+    constexpr int YB = VEC * sizeof(SY);            // bytes of one output vector: 8, 16 or 32
+    static_assert(R >= 2 && R <= 64 && (R & (R - 1)) == 0, "row of a power-of-two count of vectors");
+    __shared__ double2 table[kTableSlots];
+
+    const int t = threadIdx.x;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * a.tile_tokens;
+    const int tt_n = static_cast<int>(a.tokens - t0 < a.tile_tokens ? a.tokens - t0 : a.tile_tokens);
+    const int na = tt_n * a.heads * R;             // vectors of the tile in x
+    const int n = na + tt_n * a.heads2 * R;         // and in x2
+    const int v = t & (R - 1);
+    const bool hi = v >= R / 2;
+    const int pbase = (v & (R / 2 - 1)) * VEC + (hi ? H : 0);  // first pair this lane rotates
+
+    const SX* xa = static_cast<const SX*>(a.x) + t0 * a.heads * R * VEC;
+    const SX* xb = static_cast<const SX*>(a.x2) + t0 * a.heads2 * R * VEC;
+    // Every load is issued, those past the tile re-reading its last vector, so no branch separates them.
+    u32x4 raw[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int j = min(t + k * kBlock, n - 1);
+        raw[k] = ld128_nt(j < na ? xa + static_cast<int64_t>(j) * VEC : xb + static_cast<int64_t>(j - na) * VEC);
+    }
+
+    // (cos, sin) of every (token, pair) of the tile, as the kernel above builds it.
+    const int entries = tt_n * a.pairs;
+    for (int e = t; e < entries; e += kBlock) {
+        const int te = e / a.pairs;
+        const int p = e - te * a.pairs;
+        int64_t sec = 0;
+        if (a.pair_axes != nullptr) {
+            sec = a.pair_axes[p];
+            sec = sec < 0 ? 0 : (sec >= a.sections ? a.sections - 1 : sec);
+        }
+        const double pos = static_cast<double>(pos_at<I>(a.pos, (t0 + te) * a.sections + sec));
+        const double angle = pos * static_cast<double>(a.inv_freq[p]);
+        double sn, cs;
+        sincos(angle, &sn, &cs);
+        table[table_slot(e)] = make_double2(cs, sn);
+    }
+    __syncthreads();
+
+    SY* ya = static_cast<SY*>(a.y) + t0 * a.heads * R * VEC;
+    SY* yb = static_cast<SY*>(a.y2) + t0 * a.heads2 * R * VEC;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int j = t + k * kBlock;
+        if (j >= n) break;  // rows are whole, so a lane and its partner leave together
+        const int tl = static_cast<int>(j < na ? a.row_vecs_a.div(static_cast<uint32_t>(j))
+                                               : a.row_vecs_b.div(static_cast<uint32_t>(j - na)));
+        // lo keeps x1 of pairs [0, H) and receives x2 of them; hi keeps x2 of [H, VEC) and receives x1 of them.
+        u32x4 own1, own2;  // x1 and x2 of this lane's H pairs, in the first two dwords
+        if constexpr (R == 16) {
+            // The partner is lane ^ 8 in the lane's 16-lane row: row_ror:8, written only into the lanes that take
+            // the partner's word (bank_mask 0xC: lanes 8..15 of each row, the hi lanes; 0x3: the lo lanes).
+            own1[0] = dpp_merge<0xC>(raw[k][0], raw[k][2]);
+            own1[1] = dpp_merge<0xC>(raw[k][1], raw[k][3]);
+            own2[0] = dpp_merge<0x3>(raw[k][2], raw[k][0]);
+            own2[1] = dpp_merge<0x3>(raw[k][3], raw[k][1]);
+        } else {
+            const uint32_t s0 = xor_lane<R / 2>(hi ? raw[k][0] : raw[k][2]);
+            const uint32_t s1 = xor_lane<R / 2>(hi ? raw[k][1] : raw[k][3]);
+            own1[0] = hi ? s0 : raw[k][0];
+            own1[1] = hi ? s1 : raw[k][1];
+            own2[0] = hi ? raw[k][2] : s0;
+            own2[1] = hi ? raw[k][3] : s1;
+        }
+        own1[2] = own1[3] = own2[2] = own2[3] = 0;
+        float x1[VEC], x2[VEC];
+        unpack<TX>(own1, x1);
+        unpack<TX>(own2, x2);
+        float y1[H], y2[H];
+        // The H entries share one group of 8 (pairs and pbase are multiples of H, H <= 4), so their slots are
+        // consecutive.
+        const double2* cs_row = table + table_slot(tl * a.pairs + pbase);
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            const double2 cs = cs_row[i];
+            const double d1 = x1[i], d2 = x2[i];
+            y1[i] = static_cast<float>(fma(d1, cs.x, -(d2 * cs.y)));
+            y2[i] = static_cast<float>(fma(d2, cs.x, d1 * cs.y));
+        }
+        // Narrow this lane's H results of each half; lo stores y1 of all VEC pairs, hi y2.
+        uint32_t p1[YW], p2[YW];
+        if constexpr (sizeof(SY) == 4) {
+#pragma unroll
+            for (int i = 0; i < H; ++i) {
+                p1[i] = __float_as_uint(y1[i]);
+                p2[i] = __float_as_uint(y2[i]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < YW; ++i) {
+                p1[i] = pack2<TY>(y1[2 * i], y1[2 * i + 1]);
+                p2[i] = pack2<TY>(y2[2 * i], y2[2 * i + 1]);
+            }
+        }
+        uint32_t out[2 * YW];
+#pragma unroll
+        for (int i = 0; i < YW; ++i) {
+            if constexpr (R == 16) {
+                out[i] = dpp_merge<0xC>(p1[i], p2[i]);       // hi takes lo's y2
+                out[YW + i] = dpp_merge<0x3>(p2[i], p1[i]);  // lo takes hi's y1
+            } else {
+                const uint32_t got = xor_lane<R / 2>(hi ? p1[i] : p2[i]);  // lo sends y2, hi sends y1
+                out[i] = hi ? got : p1[i];
+                out[YW + i] = hi ? p2[i] : got;
+            }
+        }
+        SY* dst = (j < na ? ya + static_cast<int64_t>(j) * VEC : yb + static_cast<int64_t>(j - na) * VEC);
+        if constexpr (YB == 8) {
+            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+            u32x2 w;
+            w[0] = out[0];
+            w[1] = out[1];
+            __builtin_nontemporal_store(w, reinterpret_cast<u32x2*>(dst));
+        } else {
+#pragma unroll
+            for (int q = 0; q < YB / 16; ++q) {
+                u32x4 w;
+                w[0] = out[4 * q];
+                w[1] = out[4 * q + 1];
+                w[2] = out[4 * q + 2];
+                w[3] = out[4 * q + 3];
+                st128_nt(dst + q * (16 / sizeof(SY)), w);
+            }
+        }
+        // Keeps the scheduler from hoisting every vector's table reads ahead of the first store, which would hold
+        // NV vectors' worth of f64 (cos, sin) in registers at once.
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Vectors per thread the row kernel is instantiated for, and the tile it aims at (vectors per block).
+constexpr int kRowMaxNV = 8;
+constexpr int kRowTargetVectors = 6 * kBlock;
+
+template <typename TX, typename TY, typename I, int R>
+int launch_rows_nv(hipStream_t s, const RowArgs& a, int nv, unsigned grid) {
+    // Instantiated for an even count of vectors per thread (the last one idles when the tile needs an odd count).
+    switch ((nv + 1) / 2) {
+        case 1: rope_rows_kernel<TX, TY, I, R, 2><<<grid, kBlock, 0, s>>>(a); break;
+        case 2: rope_rows_kernel<TX, TY, I, R, 4><<<grid, kBlock, 0, s>>>(a); break;
+        case 3: rope_rows_kernel<TX, TY, I, R, 6><<<grid, kBlock, 0, s>>>(a); break;
+        default: rope_rows_kernel<TX, TY, I, R, 8><<<grid, kBlock, 0, s>>>(a); break;
+    }
+    return check_launch("xs_hip_rope");
+}
+
+// Launches the row kernel when the shape suits it; returns -1 (nothing launched) otherwise.
+template <typename TX, typename TY, typename I>
+int try_launch_rows(hipStream_t s, const RopeArgs& a) {
+    constexpr int VEC = vec_elems<TX>();
+    if (a.rotary != a.dim || (a.sections != 1 && a.pair_axes == nullptr) || a.dim % VEC != 0) return -1;
+    const int64_t r = a.dim / VEC;
+    if (r != 8 && r != 16 && r != 32) return -1;  // head dims 64 / 128 / 256 at 16 bits, 32 / 64 / 128 at 32 bits
+    if (!aligned16(a.x) || !aligned16(a.y) || (a.heads2 > 0 && (!aligned16(a.x2) || !aligned16(a.y2)))) return -1;
+    const int64_t per_token = (a.heads + a.heads2) * r;  // vectors
+    if (per_token > static_cast<int64_t>(kRowMaxNV) * kBlock) return -1;
+    int64_t tt = kRowTargetVectors / per_token;
+    if (tt < 1) tt = 1;
+    const int64_t pairs = a.dim / 2;
+    if (tt * pairs > kMaxTableEntries) tt = kMaxTableEntries / pairs;
+    if (tt < 1) return -1;
+    if (tt > a.tokens) tt = a.tokens;
+    const int nv = static_cast<int>((tt * per_token + kBlock - 1) / kBlock);
+    RowArgs ra;
+    ra.x = a.x;
+    ra.y = a.y;
+    ra.x2 = a.heads2 > 0 ? a.x2 : a.x;
+    ra.y2 = a.heads2 > 0 ? a.y2 : a.y;
+    ra.pos = a.pos;
+    ra.inv_freq = a.inv_freq;
+    ra.pair_axes = a.pair_axes;
+    ra.tokens = a.tokens;
+    ra.sections = a.sections;
+    ra.heads = static_cast<int>(a.heads);
+    ra.heads2 = static_cast<int>(a.heads2);
+    ra.pairs = static_cast<int>(pairs);
+    ra.tile_tokens = static_cast<int>(tt);
+    ra.row_vecs_a = FastDiv32(static_cast<uint32_t>(a.heads * r));
+    ra.row_vecs_b = FastDiv32(static_cast<uint32_t>(a.heads2 > 0 ? a.heads2 * r : 1));
+    const unsigned grid = static_cast<unsigned>((a.tokens + tt - 1) / tt);
+    switch (r) {
+        case 8: return launch_rows_nv<TX, TY, I, 8>(s, ra, nv, grid);
+        case 16: return launch_rows_nv<TX, TY, I, 16>(s, ra, nv, grid);
+        default: return launch_rows_nv<TX, TY, I, 32>(s, ra, nv, grid);
+    }
+}
+
 template <typename TX, typename TY, typename I>
 int launch_rope(hipStream_t s, RopeArgs a) {
+    const int rows_rc = try_launch_rows<TX, TY, I>(s, a);
+    if (rows_rc >= 0) return rows_rc;
     constexpr int VEC = vec_elems<TX>();
     const int64_t pairs = a.rotary / 2;
     const bool axes = a.pair_axes != nullptr;
