@@ -143,6 +143,12 @@ int xs_hip_add_mul(void* stream, const float* a, const float* b, const float* c,
 int xs_hip_add3(void* stream, const float* a, const float* b, const float* c, xs_dtype y_dtype, void* y, int64_t n,
                 int64_t period);
 
+/* y = op(x), n elements, x and y F32, F16 or BF16: Scale (y = x * a), Tanh, GeluTanh, Softcap (y = a tanh(x / a)),
+ * Sigmoid, Silu, Softplus (identity above 20), Clamp (min(max(x, a), b), NaN kept), Gelu. Replaces sycl_be::unary
+ * (sycl_kernels.h:21-25), whose x is f32; semantics cpu_ref::scale ... clamp (ops.cpp:209-258): f32 for Scale and
+ * Clamp, f64 for the transcendental ops, rounded once. */
+int xs_hip_unary(void* stream, xs_unary_op op, xs_dtype x_dtype, const void* x, xs_dtype y_dtype, void* y, int64_t n,
+                 float a, float b);
 /* y = act(x) * b, same shapes, x/b in x_dtype (F32, F16, BF16), y in y_dtype; act is SILU, GELU_TANH, SIGMOID or
  * GELU. Replaces sycl_be::act_mul (sycl_kernels.h:28-29), the fused Mul(Silu(gate), up) of gated_mlp
  * (src/models/common/blocks.cpp:23-27); semantics cpu_ref::silu etc. then cpu_ref::mul (ops.cpp:201-247). */
@@ -174,6 +180,18 @@ int xs_hip_rms_norm(void* stream, xs_dtype x_dtype, const void* x, const float* 
  * h = add(h, f(rms_norm(h))) (src/models/qwen3/qwen3_decoder.cpp:101-102) evaluated by cpu-ref as Add then RmsNorm. */
 int xs_hip_add_rms_norm(void* stream, const float* x, const float* residual, const float* w, const float* bias,
                         float* h_out, xs_dtype y_dtype, void* y, int64_t rows, int64_t width, float eps);
+/* Rows of `width`: y = (h - mean(h)) / sqrt(var(h) + eps) [* w] [+ b], h = x + shift (shift f32 [width], added in f32,
+ * or NULL: h = x); w and b f32 [width] or NULL. Mean and variance in f64, output formed in f64 and rounded once. x
+ * F32, F16 or BF16; y F32, F16 or BF16. Replaces sycl_be::layer_norm (sycl_kernels.h:91-94); semantics
+ * cpu_ref::layer_norm (ops.cpp:595-614), after cpu_ref::add for the shift. */
+int xs_hip_layer_norm(void* stream, xs_dtype x_dtype, const void* x, const float* shift, const float* w, const float* b,
+                      xs_dtype y_dtype, void* y, int64_t rows, int64_t width, float eps);
+/* Rows of `width`, f32: y = x * min(1, threshold / (|x| + eps)), |x| the row's L2 norm in f64. Replaces
+ * sycl_be::l2_clip (sycl_kernels.h:141-142); semantics cpu_ref::l2_clip (ops.cpp:401-412). */
+int xs_hip_l2_clip(void* stream, const float* x, float* y, int64_t rows, int64_t width, float threshold, float eps);
+/* y [outer, inner] = the sum over the middle axis of x [outer, dim, inner], f32, accumulated in f64. Replaces
+ * sycl_be::reduce_sum (sycl_kernels.h:80-81); semantics cpu_ref::reduce_sum (ops.cpp:686-705). */
+int xs_hip_reduce_sum(void* stream, const float* x, float* y, int64_t outer, int64_t dim, int64_t inner);
 /* Row softmax, f32, rows of `width`. Replaces sycl_be::softmax (sycl_kernels.h:58); semantics cpu_ref::softmax
  * (ops.cpp:644-661): max, sum of exp, exp / sum. */
 int xs_hip_softmax(void* stream, const float* x, float* y, int64_t rows, int64_t width);

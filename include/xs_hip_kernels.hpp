@@ -105,6 +105,15 @@ inline xs_broadcast to_abi(const Broadcast& s) {
 
 // ---- Elementwise and broadcast -------------------------------------------------------------------------------------
 
+// y = op(x); `a` is the scale factor, softcap or lower bound, `b` the upper bound (sycl_kernels.h:21-25). The
+// reference's x is f32; here X may also be half or bf16.
+template <typename Y, typename X = float>
+void unary(Stream q, UnaryOp op, const X* x, Y* y, int64_t n, float a, float b) {
+    detail::check(xs_hip_unary(q, static_cast<xs_unary_op>(op), detail::dtype_of<X>(), x, detail::dtype_of<Y>(), y, n,
+                               a, b),
+                  "unary");
+}
+
 // y = act(x) * b, same shapes; act is Silu, GeluTanh, Sigmoid or Gelu (sycl_kernels.h:27-29). X, Y: float, half, bf16.
 template <typename X, typename Y>
 void act_mul(Stream q, UnaryOp act, const X* x, const X* b, Y* y, int64_t n) {
@@ -193,6 +202,24 @@ void add_rms_norm(Stream q, const float* x, const float* residual, const float* 
                   Y* y, int64_t rows, int64_t width, float eps) {
     detail::check(xs_hip_add_rms_norm(q, x, residual, w, bias, h_out, detail::dtype_of<Y>(), y, rows, width, eps),
                   "add_rms_norm");
+}
+
+// Rows of `width`: (x [+ shift] - mean) / sqrt(var + eps) [* w] [+ b] (sycl_kernels.h:91-94).
+template <typename Y>
+void layer_norm(Stream q, const float* x, const float* shift, const float* w, const float* b, Y* y, int64_t rows,
+                int64_t width, float eps) {
+    detail::check(xs_hip_layer_norm(q, XS_F32, x, shift, w, b, detail::dtype_of<Y>(), y, rows, width, eps),
+                  "layer_norm");
+}
+
+// y = x * min(1, threshold / (|x| + eps)) per row (sycl_kernels.h:141-142).
+inline void l2_clip(Stream q, const float* x, float* y, int64_t rows, int64_t width, float threshold, float eps) {
+    detail::check(xs_hip_l2_clip(q, x, y, rows, width, threshold, eps), "l2_clip");
+}
+
+// y [outer, inner] = the sum over the middle axis of x [outer, dim, inner] (sycl_kernels.h:80-81).
+inline void reduce_sum(Stream q, const float* x, float* y, int64_t outer, int64_t dim, int64_t inner) {
+    detail::check(xs_hip_reduce_sum(q, x, y, outer, dim, inner), "reduce_sum");
 }
 
 // Rows of `width` (sycl_kernels.h:57-58).

@@ -16,7 +16,11 @@
 //                              bf16 KAT 39.191836 -> 39.25; goldens from the compiled reference (oracle/_ref)
 //   ora_binary                 brute force multi-index broadcast on the reference's shape cases; goldens
 //   ora_unary                  closed forms at special points and an f64 evaluation; goldens
+//   ora_unary_op               closed forms (tanh/softcap/softplus identities, clamp bounds, NaN), goldens
 //   ora_rms_norm               f64 evaluation + invariants (unit rms of the output); goldens
+//   ora_layer_norm             invariants (zero mean, unit variance of the unweighted output), goldens
+//   ora_l2_clip                invariants (output norm = min(|x|, threshold) to rounding), goldens
+//   ora_reduce_sum             exact sums of small integers, numpy f64 sum, goldens
 //   ora_softmax                f64 evaluation, sum to 1, masked = 0, shift invariance; goldens
 //   ora_topk                   the reference's tie KATs (tests/unit/backend/moe_ops_cases.h:76-122); sort brute force
 //   ora_rope                   norm preservation per pair, position 0 identity, inv_freq 0 identity, the planted
@@ -210,6 +214,28 @@ void ora_unary(int act, const float* x, float* y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) y[i] = static_cast<float>(act_f64(act, static_cast<double>(x[i])));
 }
 
+// The whole unary family by UnaryOp value (sycl_kernels.h:21) with the op's parameters: cpu_ref::scale, tanh,
+// gelu_tanh, softcap, sigmoid, silu, softplus, clamp, gelu (ops.cpp:209-258).
+void ora_unary_op(int op, const float* x, float* y, int64_t n, float a, float b) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float v = x[i];
+        switch (op) {
+            case 0: y[i] = v * a; break;                                                       // Scale, ops.cpp:209-211
+            case 1: y[i] = static_cast<float>(std::tanh(static_cast<double>(v))); break;      // Tanh, :213-215
+            case 3:                                                                            // Softcap, :232-236
+                y[i] = static_cast<float>(static_cast<double>(a) * std::tanh(static_cast<double>(v) / a));
+                break;
+            case 6: {                                                                          // Softplus, :249-254
+                const double d = v;
+                y[i] = static_cast<float>(d > 20.0 ? d : std::log1p(std::exp(d)));
+                break;
+            }
+            case 7: y[i] = std::min(std::max(v, a), b); break;                                // Clamp, :256-258
+            default: y[i] = static_cast<float>(act_f64(op, static_cast<double>(v))); break;  // 2, 4, 5, 8
+        }
+    }
+}
+
 // The gated-MLP activation as cpu-ref evaluates Mul(Act(Add(x, bias)), b) node by node on 2-D row-strided f32
 // operands (blocks.cpp:23-27; ops.cpp:201-247): g = fl32(x + bias[c]) (no add without bias), a = fl32(act_f64(g)),
 // y = fl32(a * b). Strides in elements; y is [rows, cols] contiguous.
@@ -250,6 +276,58 @@ void ora_add_rms_norm(const float* x, const float* residual, const float* weight
     ora_rms_norm(h, weight, eps, y, rows, width);
     if (bias != nullptr)
         for (int64_t i = 0; i < n; ++i) y[i] = y[i] + bias[i % width];
+}
+
+// cpu_ref::layer_norm (ops.cpp:595-614) of h = x + shift (a cpu_ref::add of a row first, f32; shift may be null);
+// weight and bias may be null (1 and 0: the same f64 value as the reference's expression with w = 1, b = 0).
+void ora_layer_norm(const float* x, const float* shift, const float* weight, const float* bias, float eps, float* y,
+                    int64_t rows, int64_t width) {
+    std::vector<float> h(static_cast<size_t>(width));
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * width;
+        for (int64_t i = 0; i < width; ++i) h[i] = shift != nullptr ? xr[i] + shift[i] : xr[i];
+        double mean = 0;
+        for (int64_t i = 0; i < width; ++i) mean += h[i];
+        mean /= static_cast<double>(width);
+        double var = 0;
+        for (int64_t i = 0; i < width; ++i) var += (h[i] - mean) * (h[i] - mean);
+        const double inv = 1.0 / std::sqrt(var / static_cast<double>(width) + eps);
+        for (int64_t i = 0; i < width; ++i) {
+            const double w = weight != nullptr ? weight[i] : 1.0;
+            const double b = bias != nullptr ? bias[i] : 0.0;
+            y[r * width + i] = static_cast<float>((h[i] - mean) * inv * w + b);
+        }
+    }
+}
+
+// cpu_ref::l2_clip (ops.cpp:401-412), with cpu-ref's four-way f64 dot (ops.cpp:96-108).
+void ora_l2_clip(const float* x, float* y, int64_t rows, int64_t width, float threshold, float eps) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* in = x + r * width;
+        double s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+        int64_t i = 0;
+        for (; i + 4 <= width; i += 4) {
+            s0 += static_cast<double>(in[i]) * in[i];
+            s1 += static_cast<double>(in[i + 1]) * in[i + 1];
+            s2 += static_cast<double>(in[i + 2]) * in[i + 2];
+            s3 += static_cast<double>(in[i + 3]) * in[i + 3];
+        }
+        for (; i < width; ++i) s0 += static_cast<double>(in[i]) * in[i];
+        const double dot = (s0 + s1) + (s2 + s3);
+        const double factor = std::min(1.0, threshold / (std::sqrt(dot) + eps));
+        for (int64_t k = 0; k < width; ++k) y[r * width + k] = static_cast<float>(in[k] * factor);
+    }
+}
+
+// cpu_ref::reduce_sum (ops.cpp:686-705): x [outer, dim, inner] -> y [outer, inner], f64 accumulation.
+void ora_reduce_sum(const float* x, float* y, int64_t outer, int64_t dim, int64_t inner) {
+    for (int64_t o = 0; o < outer; ++o) {
+        for (int64_t i = 0; i < inner; ++i) {
+            double sum = 0;
+            for (int64_t d = 0; d < dim; ++d) sum += x[(o * dim + d) * inner + i];
+            y[o * inner + i] = static_cast<float>(sum);
+        }
+    }
 }
 
 // cpu_ref::softmax (ops.cpp:644-661).

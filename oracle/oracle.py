@@ -88,6 +88,10 @@ class Oracle(_Base):
         L.ora_scale.argtypes = [_fp, C.c_float, _fp, _L]
         L.ora_unary.argtypes = [C.c_int, _fp, _fp, _L]
         L.ora_act_bias_mul.argtypes = [C.c_int, _fp, _L, _fp, _L, _P, _fp, _L, _L]
+        L.ora_unary_op.argtypes = [C.c_int, _fp, _fp, _L, C.c_float, C.c_float]
+        L.ora_layer_norm.argtypes = [_fp, _P, _P, _P, C.c_float, _fp, _L, _L]
+        L.ora_l2_clip.argtypes = [_fp, _fp, _L, _L, C.c_float, C.c_float]
+        L.ora_reduce_sum.argtypes = [_fp, _fp, _L, _L, _L]
         L.ora_rms_norm.argtypes = [_fp, _P, C.c_float, _fp, _L, _L]
         L.ora_add_rms_norm.argtypes = [_fp, _fp, _P, _P, C.c_float, _fp, _fp, _L, _L]
         L.ora_softmax.argtypes = [_fp, _fp, _L, _L]
@@ -150,6 +154,37 @@ class Oracle(_Base):
         bias_c = None if bias is None else np.ascontiguousarray(bias, np.float32)
         y = np.empty((rows, cols), np.float32)
         self.lib.ora_act_bias_mul(act, x, cols, b, cols, _ptr(bias_c), y, rows, cols)
+        return y
+
+    def unary_op(self, op: int, x: np.ndarray, a: float = 0.0, b: float = 0.0) -> np.ndarray:
+        """The unary family by UnaryOp value with its parameters (scale / softcap / clamp bounds)."""
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty_like(x)
+        self.lib.ora_unary_op(op, x, y, x.size, a, b)
+        return y
+
+    def layer_norm(self, x, weight, bias, eps, shift=None):
+        x = np.ascontiguousarray(x, np.float32)
+        width = x.shape[-1]
+        args = [None if t is None else np.ascontiguousarray(t, np.float32) for t in (shift, weight, bias)]
+        y = np.empty_like(x)
+        self.lib.ora_layer_norm(x, *[_ptr(t) for t in args], eps, y, x.size // width, width)
+        return y
+
+    def l2_clip(self, x, threshold, eps):
+        x = np.ascontiguousarray(x, np.float32)
+        width = x.shape[-1]
+        y = np.empty_like(x)
+        self.lib.ora_l2_clip(x, y, x.size // width, width, threshold, eps)
+        return y
+
+    def reduce_sum(self, x, axis):
+        x = np.ascontiguousarray(x, np.float32)
+        outer = int(np.prod(x.shape[:axis], dtype=np.int64))
+        dim = x.shape[axis]
+        inner = int(np.prod(x.shape[axis + 1:], dtype=np.int64))
+        y = np.empty(x.shape[:axis] + x.shape[axis + 1:], np.float32)
+        self.lib.ora_reduce_sum(x, y, outer, dim, inner)
         return y
 
     def rms_norm(self, x, weight, eps):
@@ -258,6 +293,10 @@ class Reference(_Base):
         L.xsref_topk.argtypes = [_fp, _L, _L, _L, _fp, _i32]
         L.xsref_rope.argtypes = [C.c_int, _P, _L, _L, _L, _P, C.c_int, _L, _fp, _L, _L, _P, _fp]
         L.xsref_rope_inv_freq.argtypes = [C.c_double, _L, _L, _L, _fp]
+        L.xsref_unary.argtypes = [C.c_int, _fp, _L, C.c_float, C.c_float, _fp]
+        L.xsref_layer_norm.argtypes = [_fp, _P, _fp, _fp, C.c_float, _L, _L, _fp]
+        L.xsref_l2_clip.argtypes = [_fp, _L, _L, C.c_float, C.c_float, _fp]
+        L.xsref_reduce_sum.argtypes = [_fp, _L, _L, _L, _fp]
         L.xsref_quantize_kv_row_i8.argtypes = [_fp, _L, _i8]
         L.xsref_quantize_kv_row_i8.restype = C.c_float
         L.xsref_round_trip_kv_i8.argtypes = [_fp, _L, _L]
@@ -316,6 +355,38 @@ class Reference(_Base):
         else:
             v = np.ascontiguousarray(valid_len, np.int64)
             self._check(self.lib.xsref_softmax_masked(x, rows, width, scale, _ptr(v), 0, 1, out))
+        return out
+
+    def unary_op(self, op, x, a=0.0, b=0.0):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty_like(x)
+        self._check(self.lib.xsref_unary(op, x.reshape(-1), x.size, a, b, out.reshape(-1)))
+        return out
+
+    def layer_norm(self, x, weight, bias, eps, shift=None):
+        x = np.ascontiguousarray(x, np.float32)
+        width = x.shape[-1]
+        sh = None if shift is None else np.ascontiguousarray(shift, np.float32)
+        out = np.empty_like(x)
+        self._check(self.lib.xsref_layer_norm(x, _ptr(sh), np.ascontiguousarray(weight, np.float32),
+                                              np.ascontiguousarray(bias, np.float32), eps, x.size // width, width,
+                                              out))
+        return out
+
+    def l2_clip(self, x, threshold, eps):
+        x = np.ascontiguousarray(x, np.float32)
+        width = x.shape[-1]
+        out = np.empty_like(x)
+        self._check(self.lib.xsref_l2_clip(x, x.size // width, width, threshold, eps, out))
+        return out
+
+    def reduce_sum(self, x, axis):
+        x = np.ascontiguousarray(x, np.float32)
+        outer = int(np.prod(x.shape[:axis], dtype=np.int64))
+        dim = x.shape[axis]
+        inner = int(np.prod(x.shape[axis + 1:], dtype=np.int64))
+        out = np.empty(x.shape[:axis] + x.shape[axis + 1:], np.float32)
+        self._check(self.lib.xsref_reduce_sum(x, outer, dim, inner, out))
         return out
 
     def rms_norm(self, x, weight, eps, x_dtype=F32):

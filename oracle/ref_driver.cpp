@@ -225,6 +225,64 @@ int xsref_rope(int x_dtype, const void* x, int64_t tokens, int64_t heads, int64_
     });
 }
 
+// y = op(x) for the unary family by UnaryOp value (0 Scale, 1 Tanh, 2 GeluTanh, 3 Softcap, 4 Sigmoid, 5 Silu,
+// 6 Softplus, 7 Clamp, 8 Gelu), a / b the op's parameters; f32 [n].
+int xsref_unary(int op, const float* x, int64_t n, float a, float b, float* out) {
+    return guarded([&] {
+        Graph g;
+        const Value v = g.input("x", DType::F32, {n});
+        Value y;
+        switch (op) {
+            case 0: y = g.scale(v, a); break;
+            case 1: y = g.tanh(v); break;
+            case 2: y = g.gelu_tanh(v); break;
+            case 3: y = g.softcap(v, a); break;
+            case 4: y = g.sigmoid(v); break;
+            case 5: y = g.silu(v); break;
+            case 6: y = g.softplus(v); break;
+            case 7: y = g.clamp(v, a, b); break;
+            case 8: y = g.gelu(v); break;
+            default: fail("unknown unary op ", op);
+        }
+        g.output("out", y);
+        copy_f32(run_graph(g, {{"x", borrow(DType::F32, {n}, x)}}).at("out"), out);
+    });
+}
+
+// LayerNorm(Add(x, shift) or x, w, b) over rows of `width`, f32; shift may be null, w and b may not.
+int xsref_layer_norm(const float* x, const float* shift, const float* w, const float* b, float eps, int64_t rows,
+                     int64_t width, float* out) {
+    return guarded([&] {
+        Graph g;
+        Value h = g.input("x", DType::F32, {rows, width});
+        auto row = [&](const float* p) {
+            HostTensor t(DType::F32, {width});
+            std::memcpy(t.raw(), p, static_cast<size_t>(width) * 4);
+            return g.constant(t);
+        };
+        if (shift != nullptr) h = g.add(h, row(shift));
+        g.output("out", g.layer_norm(h, row(w), row(b), eps));
+        copy_f32(run_graph(g, {{"x", borrow(DType::F32, {rows, width}, x)}}).at("out"), out);
+    });
+}
+
+int xsref_l2_clip(const float* x, int64_t rows, int64_t width, float threshold, float eps, float* out) {
+    return guarded([&] {
+        Graph g;
+        g.output("out", g.l2_clip(g.input("x", DType::F32, {rows, width}), threshold, eps));
+        copy_f32(run_graph(g, {{"x", borrow(DType::F32, {rows, width}, x)}}).at("out"), out);
+    });
+}
+
+// ReduceSum over axis 1 of x [outer, dim, inner].
+int xsref_reduce_sum(const float* x, int64_t outer, int64_t dim, int64_t inner, float* out) {
+    return guarded([&] {
+        Graph g;
+        g.output("out", g.reduce_sum(g.input("x", DType::F32, {outer, dim, inner}), 1));
+        copy_f32(run_graph(g, {{"x", borrow(DType::F32, {outer, dim, inner}, x)}}).at("out"), out);
+    });
+}
+
 int xsref_rope_inv_freq(double theta, int64_t dim, int64_t pairs, int64_t length, float* out) {
     return guarded([&] { copy_f32(blocks::rope_inv_freq(theta, dim, pairs, length), out); });
 }

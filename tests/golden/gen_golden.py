@@ -42,6 +42,13 @@ def f16(x):
 
 def save(name, d):
     path = os.path.join(HERE, name + ".npz")
+    if os.path.exists(path):
+        # an unchanged fixture keeps its file (the zip container would differ byte-wise on every write)
+        with np.load(path, allow_pickle=False) as old:
+            if set(old.files) == set(d) and all(np.array_equal(old[k], np.asarray(v), equal_nan=True)
+                                                and old[k].dtype == np.asarray(v).dtype for k, v in d.items()):
+                print(f"{path}: unchanged")
+                return
     np.savez_compressed(path, **d)
     print(f"{path}: {len(d)} arrays, {os.path.getsize(path)} bytes")
 
@@ -218,3 +225,35 @@ v16 = f16(rng.standard_normal((16, 2, 128)) * 3.0)
 d["k16"], d["v16"] = k16, v16
 d["k16_rt"], d["v16_rt"] = ref.kv_cache_i8(k16, v16, F16)
 save("kv_i8", d)
+
+
+# ---- the unary family (ops.cpp:209-258): special values, the softplus threshold, clamp bounds and NaN ----
+specials = [0.0, -0.0, 1e-30, -1e-30, 19.999, 20.0, 20.001, -20.0, 88.0, -88.0, 100.0, -100.0, 1e6, -1e6,
+            float("inf"), -float("inf"), float("nan"), 0.5, -0.5, 3.0, -3.0]
+ux = np.concatenate([np.array(specials, np.float32), uniform(600, 12.0), uniform(100, 1e-3)])
+unary = {"x": ux}
+for op, a, b, tag in [(0, 0.088388346, 0.0, "scale"), (1, 0.0, 0.0, "tanh"), (2, 0.0, 0.0, "gelu_tanh"),
+                      (3, 30.0, 0.0, "softcap"), (4, 0.0, 0.0, "sigmoid"), (5, 0.0, 0.0, "silu"),
+                      (6, 0.0, 0.0, "softplus"), (7, -1.5, 2.25, "clamp"), (7, -float("inf"), 0.0, "clamp_lo_inf"),
+                      (8, 0.0, 0.0, "gelu")]:
+    unary[tag] = ref.unary_op(op, ux, a, b)
+    unary[tag + "_args"] = np.array([op, a, b], np.float64)
+save("unary", unary)
+
+# ---- layer_norm (ops.cpp:595-614) with and without the shift row; l2_clip (ops.cpp:401-412) with rows below and above
+# the threshold; reduce_sum (ops.cpp:686-705) over each axis of a 3-D tensor ----
+lx = uniform((9, 384), 3.0)
+lx[2] += 100.0  # a large mean
+lx[5] = 0.25    # a constant row: zero variance
+lw = (1.0 + uniform(384, 0.2)).astype(np.float32)
+lb = uniform(384, 0.5)
+lsh = uniform(384, 1.0)
+cx = uniform((12, 96), 1.0)
+cx[3] *= 100.0
+cx[7] = 0.0
+rx = uniform((5, 37, 24), 10.0)
+save("norms2", {"ln_x": lx, "ln_w": lw, "ln_b": lb, "ln_shift": lsh,
+                "ln_out": ref.layer_norm(lx, lw, lb, 1e-5), "ln_shift_out": ref.layer_norm(lx, lw, lb, 1e-5, lsh),
+                "l2_x": cx, "l2_out": ref.l2_clip(cx, 4.0, 1e-6),
+                "rs_x": rx, "rs_axis0": ref.reduce_sum(rx, 0), "rs_axis1": ref.reduce_sum(rx, 1),
+                "rs_axis2": ref.reduce_sum(rx, 2)})

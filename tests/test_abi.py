@@ -86,6 +86,12 @@ def test_refusals_name_the_problem():
     assert "row strides" in err()
     assert L().xs_hip_softmax_masked(None, None, None, 2, 8, 4, 1.0, None, 8, None) == 1
     assert L().xs_hip_copy(None, None, None, 17) == 1
+    assert L().xs_hip_unary(None, 9, xs_hip.F32, 1, xs_hip.F32, 1, 4, 0.0, 0.0) == 1
+    assert "unknown op 9" in err()
+    assert L().xs_hip_unary(None, xs_hip.SOFTCAP, xs_hip.F32, 1, xs_hip.F32, 1, 4, 0.0, 0.0) == 1
+    assert "softcap" in err()
+    assert L().xs_hip_layer_norm(None, xs_hip.F32, None, None, None, None, xs_hip.F32, None, 2, 0, 1e-5) == 1
+    assert L().xs_hip_reduce_sum(None, None, None, -1, 4, 1) == 1
 
 
 def test_empty_work_is_a_no_op():
@@ -94,6 +100,8 @@ def test_empty_work_is_a_no_op():
     assert L().xs_hip_act_mul(None, xs_hip.SILU, xs_hip.F32, None, None, xs_hip.F32, None, 0) == 0
     assert L().xs_hip_softmax(None, None, None, 0, 8) == 0
     assert L().xs_hip_topk(None, None, None, None, 0, 8, 1, None) == 0
+    assert L().xs_hip_unary(None, xs_hip.TANH, xs_hip.F32, None, xs_hip.F32, None, 0, 0.0, 0.0) == 0
+    assert L().xs_hip_reduce_sum(None, None, None, 0, 4, 1) == 0
 
 
 def test_softmax_scratch_sizes():

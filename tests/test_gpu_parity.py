@@ -593,3 +593,79 @@ def test_rope_qk_fused_odd_shapes(ora):
         yq, yk = X.rope_qk(dev(xq, xdt), dev(xk, xdt), dev(pos), dev(f))
         check_out(yq.numpy(), ora.rope(ora.widen(xq, xdt), pos, f), xdt, ora, "rope2 q")
         check_out(yk.numpy(), ora.rope(ora.widen(xk, xdt), pos, f), xdt, ora, "rope2 k")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# The unary family, layer_norm, l2_clip, reduce_sum
+
+UNARY_TAGS = ["scale", "tanh", "gelu_tanh", "softcap", "sigmoid", "silu", "softplus", "clamp", "clamp_lo_inf", "gelu"]
+
+
+def test_unary_family_goldens(ora):
+    g = golden("unary")
+    x = g["x"]
+    for tag in UNARY_TAGS:
+        op, a, b = (float(v) for v in g[tag + "_args"])
+        step(f"unary {tag} goldens f32 [{x.size}]")
+        y = X.unary(int(op), dev(x), a, b).numpy()
+        if tag in ("scale", "clamp", "clamp_lo_inf"):
+            assert_exact(y, g[tag], tag)
+        else:
+            atol = gelu_noise(x, np.ones_like(x)) if tag.startswith("gelu") else 0.0
+            assert_f32_close(y, g[tag], what=tag, atol=atol)
+
+
+@pytest.mark.parametrize("xdt,ydt", [(F32, F32), (BF16, BF16), (F16, F32), (F32, F16)])
+def test_unary_family_dtypes_and_tails(ora, xdt, ydt):
+    """Every op at an odd length (the vector kernel on whole chunks, the scalar one on the tail) and dtype pair."""
+    rng = np.random.default_rng(40)
+    n = 100_003
+    x = ora.narrow((rng.standard_normal(n) * 6).astype(np.float32), xdt)
+    xf = ora.widen(x, xdt)
+    xd = dev(x, xdt)
+    for op, a, b in [(X.SCALE, 0.125, 0), (X.TANH, 0, 0), (X.GELU_TANH, 0, 0), (X.SOFTCAP, 15.0, 0),
+                     (X.SIGMOID, 0, 0), (X.SILU, 0, 0), (X.SOFTPLUS, 0, 0), (X.CLAMP, -2.0, 1.5), (X.GELU, 0, 0)]:
+        step(f"unary op {op} [{n}] {DT[xdt]} -> {DT[ydt]}")
+        y = X.unary(op, xd, a, b, y_dtype=ydt).numpy()
+        want = ora.unary_op(op, xf, a, b)
+        atol = gelu_noise(xf, np.ones_like(xf)) if op in (X.GELU_TANH, X.GELU) else 0.0
+        check_out(y, want, ydt, ora, f"unary {op}", atol=atol)
+
+
+def test_layer_norm_goldens_and_shapes(ora):
+    g = golden("norms2")
+    step("layer_norm goldens [9, 384]")
+    y = X.layer_norm(dev(g["ln_x"]), dev(g["ln_w"]), dev(g["ln_b"]), 1e-5).numpy()
+    assert_f32_close(y, g["ln_out"], what="layer_norm")
+    y = X.layer_norm(dev(g["ln_x"]), dev(g["ln_w"]), dev(g["ln_b"]), 1e-5, shift=dev(g["ln_shift"])).numpy()
+    assert_f32_close(y, g["ln_shift_out"], what="layer_norm shift")
+    rng = np.random.default_rng(41)
+    for rows, width, xdt, ydt, weighted in [(64, 2560, F32, F32, True), (7, 1000, BF16, BF16, True),
+                                            (33, 4096, F16, F16, False), (3, 70000, F32, F32, True),
+                                            (5, 333, F32, F32, True)]:
+        x = ora.narrow((rng.standard_normal((rows, width)) * 2 + 1).astype(np.float32), xdt)
+        w = rng.standard_normal(width).astype(np.float32) if weighted else None
+        b = rng.standard_normal(width).astype(np.float32) if weighted else None
+        step(f"layer_norm [{rows}, {width}] {DT[xdt]} -> {DT[ydt]}")
+        y = X.layer_norm(dev(x, xdt), dev(w) if weighted else None, dev(b) if weighted else None, 1e-5,
+                         y_dtype=ydt).numpy()
+        check_out(y, ora.layer_norm(ora.widen(x, xdt), w, b, 1e-5), ydt, ora, f"layer_norm {rows}x{width}")
+
+
+def test_l2_clip_and_reduce_sum(ora):
+    g = golden("norms2")
+    step("l2_clip goldens [12, 96]")
+    assert_f32_close(X.l2_clip(dev(g["l2_x"]), 4.0, 1e-6).numpy(), g["l2_out"], what="l2_clip")
+    rng = np.random.default_rng(42)
+    x = rng.standard_normal((300, 2048)).astype(np.float32)
+    x[::2] *= 0.001
+    step("l2_clip [300, 2048]")
+    assert_f32_close(X.l2_clip(dev(x), 1.0, 1e-6).numpy(), ora.l2_clip(x, 1.0, 1e-6), what="l2_clip big")
+    for a in range(3):
+        step(f"reduce_sum goldens axis {a}")
+        assert_f32_close(X.reduce_sum(dev(g["rs_x"]), a).numpy(), g[f"rs_axis{a}"], what=f"reduce_sum {a}")
+    for shape, a in [((1000, 4096), 1), ((64, 3000, 7), 1), ((5, 200, 300), 0), ((2, 17), 1), ((1, 1, 5), 1),
+                     ((3, 0, 4), 1)]:
+        t = (rng.standard_normal(shape) * 100).astype(np.float32)
+        step(f"reduce_sum {shape} axis {a}")
+        assert_f32_close(X.reduce_sum(dev(t), a).numpy(), ora.reduce_sum(t, a), what=f"reduce_sum {shape}")

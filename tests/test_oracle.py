@@ -387,3 +387,96 @@ def test_oracle_matches_compiled_reference(ora):
     rc, rs = ref.quantize_kv(kv)
     assert_exact(c, rc)
     assert_exact(s, rs)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# The unary family, layer_norm, l2_clip, reduce_sum
+
+UNARY_TAGS = ["scale", "tanh", "gelu_tanh", "softcap", "sigmoid", "silu", "softplus", "clamp", "clamp_lo_inf", "gelu"]
+
+
+def test_unary_family_goldens(ora):
+    g = golden("unary")
+    for tag in UNARY_TAGS:
+        op, a, b = g[tag + "_args"]
+        got = ora.unary_op(int(op), g["x"], float(a), float(b))
+        assert np.array_equal(got, g[tag], equal_nan=True), tag
+
+
+def test_unary_family_closed_forms(ora):
+    x = np.array([0.0, -0.0, 1e-30, 25.0, 21.0, -3.0, np.nan, np.inf, -np.inf], np.float32)
+    assert np.array_equal(ora.unary_op(0, x, 0.5), x * np.float32(0.5), equal_nan=True)           # scale: one f32 mul
+    t = ora.unary_op(1, x)
+    assert t[0] == 0.0 and t[7] == 1.0 and t[8] == -1.0 and np.isnan(t[6])                     # tanh
+    sp = ora.unary_op(6, x)
+    assert sp[3] == 25.0 and sp[4] == 21.0                                                        # softplus: x above 20
+    assert sp[0] == np.float32(math.log(2.0)) and sp[5] == np.float32(math.log1p(math.exp(-3.0)))
+    sc = ora.unary_op(3, x, 30.0)
+    assert sc[2] == np.float32(1e-30) and sc[7] == 30.0                                           # softcap: ~x near 0
+    assert sc[5] == np.float32(30.0 * math.tanh(-0.1))
+    cl = ora.unary_op(7, x, -1.0, 2.0)
+    assert list(cl[[0, 3, 5, 7, 8]]) == [0.0, 2.0, -1.0, 2.0, -1.0] and np.isnan(cl[6])          # clamp keeps NaN
+    si = ora.unary_op(5, x)
+    assert si[3] == np.float32(25.0 / (1.0 + math.exp(-25.0))) and si[0] == 0.0
+
+
+def test_layer_norm_invariants(ora):
+    rng = np.random.default_rng(31)
+    x = (rng.standard_normal((6, 512)) * 4 + 7).astype(np.float32)
+    y = ora.layer_norm(x, None, None, 1e-12).astype(np.float64)
+    assert np.allclose(y.mean(axis=1), 0.0, atol=1e-6)
+    assert np.allclose(y.var(axis=1), 1.0, rtol=1e-5)
+    w = rng.standard_normal(512).astype(np.float32)
+    b = rng.standard_normal(512).astype(np.float32)
+    yw = ora.layer_norm(x, w, b, 1e-12)
+    assert_f32_close(yw, (y * w + b).astype(np.float32), atol=1e-5)
+    const = np.full((1, 64), 3.5, np.float32)
+    assert (ora.layer_norm(const, None, None, 1e-5) == 0.0).all()
+    sh = rng.standard_normal(512).astype(np.float32)
+    assert_exact(ora.layer_norm(x, w, b, 1e-5, sh), ora.layer_norm(x + sh, w, b, 1e-5))
+
+
+def test_norms2_goldens(ora):
+    g = golden("norms2")
+    assert_exact(ora.layer_norm(g["ln_x"], g["ln_w"], g["ln_b"], 1e-5), g["ln_out"])
+    assert_exact(ora.layer_norm(g["ln_x"], g["ln_w"], g["ln_b"], 1e-5, g["ln_shift"]), g["ln_shift_out"])
+    assert_exact(ora.l2_clip(g["l2_x"], 4.0, 1e-6), g["l2_out"])
+    for a in range(3):
+        assert_exact(ora.reduce_sum(g["rs_x"], a), g[f"rs_axis{a}"])
+
+
+def test_l2_clip_invariants(ora):
+    rng = np.random.default_rng(32)
+    x = rng.standard_normal((8, 300)).astype(np.float32)
+    x[:4] *= 0.01  # norms below the threshold: unchanged
+    y = ora.l2_clip(x, 2.0, 0.0)
+    assert_exact(y[:4], x[:4])
+    n = np.linalg.norm(y[4:].astype(np.float64), axis=1)
+    assert np.allclose(n, 2.0, rtol=1e-6)
+    assert (ora.l2_clip(np.zeros((1, 16), np.float32), 1.0, 1e-6) == 0.0).all()
+
+
+def test_reduce_sum_exact_and_f64(ora):
+    ints = np.arange(2 * 1000 * 3, dtype=np.float32).reshape(2, 1000, 3) % 17
+    for a in range(3):
+        assert_exact(ora.reduce_sum(ints, a), ints.astype(np.float64).sum(axis=a).astype(np.float32))
+    rng = np.random.default_rng(33)
+    x = rng.standard_normal((3, 4000, 5)).astype(np.float32) * 1e3
+    want = x.astype(np.float64).sum(axis=1)
+    assert np.allclose(ora.reduce_sum(x, 1), want, rtol=1e-6, atol=1e-3)
+
+
+@pytest.mark.skipif(reference() is None, reason="oracle/_ref not built (no reference tree on this host)")
+def test_oracle_matches_compiled_reference_unary_and_norms(ora):
+    ref = reference()
+    rng = np.random.default_rng(34)
+    x = (rng.standard_normal(5000) * 10).astype(np.float32)
+    for op, a, b in [(0, 1.7, 0), (1, 0, 0), (3, 15.0, 0), (6, 0, 0), (7, -2.0, 3.0), (2, 0, 0), (8, 0, 0)]:
+        assert np.array_equal(ora.unary_op(op, x, a, b), ref.unary_op(op, x, a, b), equal_nan=True), op
+    m = (rng.standard_normal((17, 1000)) * 2).astype(np.float32)
+    w, b = rng.standard_normal(1000).astype(np.float32), rng.standard_normal(1000).astype(np.float32)
+    assert_exact(ora.layer_norm(m, w, b, 1e-6, w), ref.layer_norm(m, w, b, 1e-6, w))
+    assert_exact(ora.l2_clip(m, 30.0, 1e-6), ref.l2_clip(m, 30.0, 1e-6))
+    t = rng.standard_normal((4, 33, 65)).astype(np.float32)
+    for a in range(3):
+        assert_exact(ora.reduce_sum(t, a), ref.reduce_sum(t, a))

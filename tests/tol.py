@@ -12,7 +12,8 @@ def assert_f32_close(got, want, rtol=RTOL_F32, what="", atol=0.0):
     assert got.shape == want.shape, f"{what}: shape {got.shape} != {want.shape}"
     both_nan = np.isnan(got) & np.isnan(want)
     same = (got == want) | both_nan
-    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    with np.errstate(invalid="ignore"):  # inf - inf where both are the same infinity (already in `same`)
+        err = np.abs(got.astype(np.float64) - want.astype(np.float64))
     ok = same | (err <= rtol * np.abs(want.astype(np.float64)) + atol)
     if not ok.all():
         bad = np.argwhere(~ok)

@@ -1,4 +1,5 @@
-// Activation-times-gate entry points for gfx950: act_mul, unary_bias, and the biased gated-MLP activation over
+// The unary family (sycl_be::unary, src/backend/sycl/sycl_kernels.h:21-25; cpu-ref semantics ops.cpp:209-258) and the
+// activation-times-gate entry points for gfx950: act_mul, unary_bias, and the biased gated-MLP activation over
 // row-strided operands (the SwiGLU of a gated MLP: reference src/models/common/blocks.cpp:23-27, fused by the SYCL
 // planner as unary_bias + act_mul, src/backend/sycl/sycl_backend.cpp:1004-1047). All run the 2-D kernel of ew.h.
 #include "ew.h"
@@ -20,6 +21,21 @@ bool act_ok(xs_unary_op act) {
 using namespace xs_hip;
 
 extern "C" {
+
+int xs_hip_unary(void* stream, xs_unary_op op, xs_dtype x_dtype, const void* x, xs_dtype y_dtype, void* y, int64_t n,
+                 float a, float b) {
+    if (static_cast<int>(op) < XS_UNARY_SCALE || static_cast<int>(op) > XS_UNARY_GELU)
+        return fail(XS_HIP_EINVAL, "xs_hip_unary: unknown op " + i2s(op));
+    if (n < 0) return fail(XS_HIP_EINVAL, "xs_hip_unary: n " + i2s(n));
+    if (n == 0) return XS_HIP_OK;
+    if (x == nullptr || y == nullptr) return fail(XS_HIP_EINVAL, "xs_hip_unary: null buffer");
+    if (op == XS_UNARY_SOFTCAP && !(a != 0.0f))
+        return fail(XS_HIP_EINVAL, "xs_hip_unary: softcap " + std::to_string(a) + " must be nonzero");
+    Ew2D e{x, nullptr, nullptr, y, n, 0, 0, n, 1, n, ew::kUnary, op};
+    e.pa = a;
+    e.pb = b;
+    return ew::dispatch_unary(as_stream(stream), e, x_dtype, y_dtype, "xs_hip_unary");
+}
 
 int xs_hip_act_mul(void* stream, xs_unary_op act, xs_dtype x_dtype, const void* x, const void* b, xs_dtype y_dtype,
                    void* y, int64_t n) {

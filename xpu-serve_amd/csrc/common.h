@@ -187,10 +187,27 @@ __device__ __forceinline__ float group_reduce(float v) {
     return v;
 }
 
-// f64 sum over aligned groups of W lanes (shuffles of the two halves).
+template <int Ctrl>
+__device__ __forceinline__ double dpp_d(double v) {
+    const uint64_t u = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(static_cast<int>(u), static_cast<int>(u), Ctrl, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(static_cast<int>(u >> 32), static_cast<int>(u >> 32), Ctrl, 0xF, 0xF,
+                                               false);
+    return __longlong_as_double(static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                                                     static_cast<uint32_t>(lo)));
+}
+
+// f64 sum over aligned groups of W lanes: the DPP steps of group_reduce on the two halves of each value, then
+// shuffles across 16-lane rows. Every lane of a group ends with identical bits.
 template <int W>
 __device__ __forceinline__ double group_sum_f64(double v) {
-    for (int off = 1; off < W; off <<= 1) v += __shfl_xor(v, off, 64);
+    static_assert(W >= 1 && W <= 64 && (W & (W - 1)) == 0, "group width");
+    if constexpr (W >= 2) v += dpp_d<dpp::kQuadXor1>(v);
+    if constexpr (W >= 4) v += dpp_d<dpp::kQuadXor2>(v);
+    if constexpr (W >= 8) v += dpp_d<dpp::kRowHalfMirror>(v);
+    if constexpr (W >= 16) v += dpp_d<dpp::kRowMirror>(v);
+    if constexpr (W >= 32) v += __shfl_xor(v, 16, 64);
+    if constexpr (W >= 64) v += __shfl_xor(v, 32, 64);
     return v;
 }
 

@@ -21,11 +21,11 @@
 namespace xs_hip {
 namespace ew {
 
-enum Op : int { kCopy = 0, kAdd, kMul, kDiv, kActMul, kAddMul, kAdd3, kActBias, kActBiasMul };
+enum Op : int { kCopy = 0, kAdd, kMul, kDiv, kActMul, kAddMul, kAdd3, kActBias, kActBiasMul, kUnary };
 
-constexpr bool reads_b(int op) { return op != kCopy && op != kActBias; }
+constexpr bool reads_b(int op) { return op != kCopy && op != kActBias && op != kUnary; }
 constexpr bool reads_c(int op) { return op == kAddMul || op == kAdd3 || op == kActBias || op == kActBiasMul; }
-constexpr bool has_act(int op) { return op == kActMul || op == kActBias || op == kActBiasMul; }
+constexpr bool has_act(int op) { return op == kActMul || op == kActBias || op == kActBiasMul || op == kUnary; }
 
 // Below this input the fast forms' exponential leaves the normal f32 range; a chunk holding one takes the f64 path.
 constexpr float kTinyExp = -80.0f;
@@ -44,6 +44,36 @@ __device__ __forceinline__ float act_exact(float x) {
         return static_cast<float>(0.5 * d * (1.0 + tanh(inner)));
     } else {
         return static_cast<float>(0.5 * d * (1.0 + erf(d / 1.41421356237309504880)));
+    }
+}
+
+// Every op of the unary family as cpu-ref evaluates it (ops.cpp:209-258), `pa` / `pb` the op's parameters (the scale
+// factor, the softcap, the clamp bounds): f32 arithmetic for Scale and Clamp, f64 for the transcendental ones, rounded
+// once. Clamp is std::min(std::max(v, lo), hi), which keeps a NaN v.
+// An empty register barrier: hides the value's origin from the optimizer. Used on unary results before they are
+// narrowed, where the compiler would otherwise fold the narrowing of a libm copysign into a bf16 copysign that it
+// cannot select on gfx950.
+__device__ __forceinline__ float opaque(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+template <int ACT>
+__device__ __forceinline__ float unary_exact(float x, float pa, float pb) {
+    if constexpr (ACT == XS_UNARY_SCALE) {
+        return x * pa;
+    } else if constexpr (ACT == XS_UNARY_TANH) {
+        return static_cast<float>(tanh(static_cast<double>(x)));
+    } else if constexpr (ACT == XS_UNARY_SOFTCAP) {
+        return static_cast<float>(static_cast<double>(pa) * tanh(static_cast<double>(x) / pa));
+    } else if constexpr (ACT == XS_UNARY_SOFTPLUS) {
+        const double d = x;
+        return static_cast<float>(d > 20.0 ? d : log1p(exp(d)));
+    } else if constexpr (ACT == XS_UNARY_CLAMP) {
+        const float lo = x < pa ? pa : x;
+        return pb < lo ? pb : lo;
+    } else {
+        return act_exact<ACT>(x);
     }
 }
 
@@ -72,7 +102,7 @@ __device__ __forceinline__ float pre(float a, float b, float c) {
     else if constexpr (OP == kAdd) return a + b;
     else if constexpr (OP == kMul) return a * b;
     else if constexpr (OP == kDiv) return a / b;
-    else if constexpr (OP == kActMul) return a;
+    else if constexpr (OP == kActMul || OP == kUnary) return a;
     else if constexpr (OP == kAddMul) return a + b * c;
     else if constexpr (OP == kAdd3) return a + (b + c);
     else return a + c;  // kActBias, kActBiasMul
@@ -80,7 +110,7 @@ __device__ __forceinline__ float pre(float a, float b, float c) {
 
 // Applies op OP with activation ACT to 8 elements (pre-activation values in v, gate values in b).
 template <int OP, int ACT, bool EXACT_ARG>
-__device__ __forceinline__ void finish8(float* v, const float* b) {
+__device__ __forceinline__ void finish8(float* v, const float* b, float pa, float pb) {
     if constexpr (has_act(OP)) {
         bool slow = !act_fast_ok(ACT);
         if constexpr (act_fast_ok(ACT)) {
@@ -90,7 +120,10 @@ __device__ __forceinline__ void finish8(float* v, const float* b) {
         }
         if (slow) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = act_exact<ACT>(v[i]);
+            for (int i = 0; i < 8; ++i) {
+                v[i] = unary_exact<ACT>(v[i], pa, pb);
+                if constexpr (OP == kUnary) v[i] = opaque(v[i]);
+            }
         } else {
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[i] = act_fast<ACT, EXACT_ARG>(v[i]);
@@ -110,6 +143,7 @@ struct Ew2D {
     int64_t sa, sb, sc, sy;  // row strides in elements (0: the row repeats)
     int64_t rows, cols;
     int op, act;
+    float pa = 0.0f, pb = 0.0f;  // kUnary's parameters
 };
 
 // 8 elements of T at p (two 128-bit loads for f32, one for 16-bit types); NT marks streaming data read once.
@@ -174,7 +208,7 @@ __global__ __launch_bounds__(kBlock) void ew2d_vec(Ew2D e, uint32_t units, FastD
                 float v[8];
 #pragma unroll
                 for (int i = 0; i < 8; ++i) v[i] = pre<OP>(fa[k][i], RB ? fb[k][i] : 0.0f, RC ? fc[k][i] : 0.0f);
-                finish8<OP, ACT, EXACT_ARG>(v, fb[k]);
+                finish8<OP, ACT, EXACT_ARG>(v, fb[k], e.pa, e.pb);
                 store8<TY, true>(y + row[k] * e.sy + col[k], v);
             }
         }
@@ -200,7 +234,8 @@ __global__ __launch_bounds__(kBlock) void ew2d_any(Ew2D e) {
         const float fc = RC ? TX::load(c[r * e.sc + col]) : 0.0f;
         float v = pre<OP>(fa, fb, fc);
         if constexpr (has_act(OP)) {
-            v = act_exact<ACT>(v);
+            v = unary_exact<ACT>(v, e.pa, e.pb);
+            if constexpr (OP == kUnary) v = opaque(v);
             if constexpr (OP == kActMul || OP == kActBiasMul) v = v * fb;
         }
         y[r * e.sy + col] = TY::store(v);
@@ -214,6 +249,26 @@ int launch(hipStream_t s, const Ew2D& e, const char* what) {
     const bool vec = e.cols % 8 == 0 && aligned16(e.a) && aligned16(e.y) && (!RB || aligned16(e.b)) &&
                      (!RC || aligned16(e.c)) && e.sa % 8 == 0 && e.sy % 8 == 0 && (!RB || e.sb % 8 == 0) &&
                      (!RC || e.sc % 8 == 0);
+    // A single row (a flat tensor) whose length is no multiple of 8: the vector kernel takes all whole chunks and the
+    // scalar one the last cols % 8 elements.
+    if (!vec && e.rows == 1 && e.cols > 8 && e.cols % 8 != 0) {
+        Ew2D head = e;
+        head.cols = e.cols / 8 * 8;
+        const bool head_vec = aligned16(e.a) && aligned16(e.y) && (!RB || aligned16(e.b)) && (!RC || aligned16(e.c));
+        if (head_vec) {
+            Ew2D tail = e;
+            const int64_t skip = head.cols;
+            tail.cols = e.cols - skip;
+            tail.a = static_cast<const typename TX::storage*>(e.a) + skip;
+            if (RB) tail.b = static_cast<const typename TX::storage*>(e.b) + skip;
+            if (RC) tail.c = static_cast<const typename TX::storage*>(e.c) + skip;
+            tail.y = static_cast<typename TY::storage*>(e.y) + skip;
+            const int rc = launch<TX, TY, OP, ACT>(s, head, what);
+            if (rc != XS_HIP_OK) return rc;
+            ew2d_any<TX, TY, OP, ACT><<<1, kBlock, 0, s>>>(tail);
+            return check_launch(what);
+        }
+    }
     const int64_t cpr = e.cols / 8;
     const int64_t units = e.rows * cpr;
     if (vec && units < (int64_t{1} << 31)) {
@@ -249,6 +304,22 @@ int dispatch(hipStream_t s, const Ew2D& e, xs_dtype x_dtype, xs_dtype y_dtype, c
         default:
             return fail(XS_HIP_EINVAL, std::string(what) + ": operands must be f32, f16 or bf16, got " +
                                            dtype_name(x_dtype));
+    }
+}
+
+// The unary family (kUnary) with a run-time op: one template instance per op.
+inline int dispatch_unary(hipStream_t s, const Ew2D& e, xs_dtype x_dtype, xs_dtype y_dtype, const char* what) {
+    switch (e.act) {
+        case XS_UNARY_SCALE: return dispatch<kUnary, XS_UNARY_SCALE>(s, e, x_dtype, y_dtype, what);
+        case XS_UNARY_TANH: return dispatch<kUnary, XS_UNARY_TANH>(s, e, x_dtype, y_dtype, what);
+        case XS_UNARY_GELU_TANH: return dispatch<kUnary, XS_UNARY_GELU_TANH>(s, e, x_dtype, y_dtype, what);
+        case XS_UNARY_SOFTCAP: return dispatch<kUnary, XS_UNARY_SOFTCAP>(s, e, x_dtype, y_dtype, what);
+        case XS_UNARY_SIGMOID: return dispatch<kUnary, XS_UNARY_SIGMOID>(s, e, x_dtype, y_dtype, what);
+        case XS_UNARY_SILU: return dispatch<kUnary, XS_UNARY_SILU>(s, e, x_dtype, y_dtype, what);
+        case XS_UNARY_SOFTPLUS: return dispatch<kUnary, XS_UNARY_SOFTPLUS>(s, e, x_dtype, y_dtype, what);
+        case XS_UNARY_CLAMP: return dispatch<kUnary, XS_UNARY_CLAMP>(s, e, x_dtype, y_dtype, what);
+        case XS_UNARY_GELU: return dispatch<kUnary, XS_UNARY_GELU>(s, e, x_dtype, y_dtype, what);
+        default: return fail(XS_HIP_EINVAL, std::string(what) + ": unknown unary op " + std::to_string(e.act));
     }
 }
 

@@ -85,12 +85,16 @@ _SIGS = {
     "xs_hip_binary_period": [_P, _INT, _INT, _P, _P, _INT, _P, _I64, _I64],
     "xs_hip_add_mul": [_P, _P, _P, _P, _INT, _P, _I64, _I64],
     "xs_hip_add3": [_P, _P, _P, _P, _INT, _P, _I64, _I64],
+    "xs_hip_unary": [_P, _INT, _INT, _P, _INT, _P, _I64, _F, _F],
     "xs_hip_act_mul": [_P, _INT, _INT, _P, _P, _INT, _P, _I64],
     "xs_hip_unary_bias": [_P, _INT, _P, _P, _INT, _P, _I64, _I64],
     "xs_hip_act_bias_mul_2d": [_P, _INT, _INT, _P, _I64, _P, _I64, _P, _INT, _P, _I64, _I64, _I64],
     "xs_hip_convert": [_P, _INT, _P, _INT, _P, _I64],
     "xs_hip_rms_norm": [_P, _INT, _P, _P, _P, _INT, _P, _I64, _I64, _F],
     "xs_hip_add_rms_norm": [_P, _P, _P, _P, _P, _P, _INT, _P, _I64, _I64, _F],
+    "xs_hip_layer_norm": [_P, _INT, _P, _P, _P, _P, _INT, _P, _I64, _I64, _F],
+    "xs_hip_l2_clip": [_P, _P, _P, _I64, _I64, _F, _F],
+    "xs_hip_reduce_sum": [_P, _P, _P, _I64, _I64, _I64],
     "xs_hip_softmax": [_P, _P, _P, _I64, _I64],
     "xs_hip_softmax_masked": [_P, _P, _P, _I64, _I64, _I64, _F, _P, _I64, _P],
     "xs_hip_softmax_scratch": [_I64, _I64],
@@ -284,6 +288,46 @@ def rms_norm(x: DeviceTensor, weight: Optional[DeviceTensor], eps: float, y_dtyp
     y = DeviceTensor.empty(y_dtype, x.shape)
     call("xs_hip_rms_norm", stream, x.dtype, C.c_void_p(x.ptr), C.c_void_p(weight.ptr if weight else 0), None,
          y_dtype, C.c_void_p(y.ptr), rows, width, C.c_float(eps))
+    return y
+
+
+def layer_norm(x: DeviceTensor, weight: Optional[DeviceTensor], bias: Optional[DeviceTensor], eps: float,
+               shift: Optional[DeviceTensor] = None, y_dtype: int = F32, stream=None) -> DeviceTensor:
+    """cpu_ref::layer_norm (ops.cpp:595-614) over the last dim of x (+ shift row, added first)."""
+    width = x.shape[-1]
+    rows = x.numel // width
+    y = DeviceTensor.empty(y_dtype, x.shape)
+    ptr = lambda t: C.c_void_p(t.ptr if t is not None else 0)  # noqa: E731
+    call("xs_hip_layer_norm", stream, x.dtype, C.c_void_p(x.ptr), ptr(shift), ptr(weight), ptr(bias), y_dtype,
+         C.c_void_p(y.ptr), rows, width, C.c_float(eps))
+    return y
+
+
+def l2_clip(x: DeviceTensor, threshold: float, eps: float = 1e-6, stream=None) -> DeviceTensor:
+    """cpu_ref::l2_clip (ops.cpp:401-412) of the rows of x (f32)."""
+    width = x.shape[-1]
+    y = DeviceTensor.empty(F32, x.shape)
+    call("xs_hip_l2_clip", stream, C.c_void_p(x.ptr), C.c_void_p(y.ptr), x.numel // width, width,
+         C.c_float(threshold), C.c_float(eps))
+    return y
+
+
+def reduce_sum(x: DeviceTensor, axis: int, stream=None) -> DeviceTensor:
+    """cpu_ref::reduce_sum (ops.cpp:686-705): the sum over `axis` of x (f32), which is removed."""
+    outer = int(np.prod(x.shape[:axis], dtype=np.int64))
+    dim = x.shape[axis]
+    inner = int(np.prod(x.shape[axis + 1:], dtype=np.int64))
+    y = DeviceTensor.empty(F32, x.shape[:axis] + x.shape[axis + 1:])
+    call("xs_hip_reduce_sum", stream, C.c_void_p(x.ptr), C.c_void_p(y.ptr), outer, dim, inner)
+    return y
+
+
+def unary(op: int, x: DeviceTensor, a: float = 0.0, b: float = 0.0, y_dtype: Optional[int] = None,
+          stream=None) -> DeviceTensor:
+    """y = op(x) for the unary family (SCALE ... GELU), a / b the op's parameters."""
+    y = DeviceTensor.empty(x.dtype if y_dtype is None else y_dtype, x.shape)
+    call("xs_hip_unary", stream, op, x.dtype, C.c_void_p(x.ptr), y.dtype, C.c_void_p(y.ptr), x.numel, C.c_float(a),
+         C.c_float(b))
     return y
 
 
