@@ -304,6 +304,32 @@ def op_kv_dequantize(inputs):
               "dequantize_i8_vec")
 
 
+def op_attention_i8(inputs):
+    """One decode step (1 query token, 32 query heads) over the int8 cache of config 4's K and V."""
+    rows, dim, k0, v0 = inputs
+    kv_heads, q_heads = 8, 32
+    kv_len = rows // kv_heads
+    kc0, ks0 = X.quantize_kv(k0)
+    vc0, vs0 = X.quantize_kv(v0)
+    rng = np.random.default_rng(0x5EED0005)
+    q0 = X.DeviceTensor.from_numpy(rng.standard_normal((1, q_heads, dim)).astype(np.float32))
+    split = int(X.lib().xs_hip_attention_i8_split(1, kv_heads, kv_len))
+    nscratch = int(X.lib().xs_hip_attention_i8_scratch(1, q_heads, dim, split))
+
+    def mk():
+        s = (dcopy(kc0), dcopy(ks0), dcopy(vc0), dcopy(vs0), dcopy(q0), X.DeviceTensor.empty(X.F32, (1, q_heads, dim)),
+             X.DeviceBuffer(nscratch))
+        need(s[0], rows * dim, "attention k codes")
+        return s
+
+    def go(s, stream):
+        kc, ks, vc, vs, q, out, scratch = s
+        X.call("xs_hip_attention_i8", stream, vp(q), vp(kc), vp(ks), vp(vc), vp(vs), vp(out), 1, q_heads, kv_heads,
+               dim, kv_len, C.c_float(1.0 / math.sqrt(dim)), C.c_float(0.0), 0, 1, split, C.c_void_p(scratch.ptr))
+    return Op("attention_i8_decode", W.ALGO_BYTES["attention_i8_decode"], W.ALGO_BYTES["attention_i8_decode"], mk, go,
+              2, "attention_i8_rows")
+
+
 def op_copy(n=256 << 20):
     """Bytes per call n (default 256 MiB): the kernel the hardware byte counters are calibrated against."""
     x0 = X.DeviceBuffer(n)
@@ -321,7 +347,7 @@ def op_copy(n=256 << 20):
 
 
 OP_ORDER = ["swiglu_bias", "swiglu_bias_strided", "rmsnorm_residual", "softmax_masked", "argmax", "rope_qk",
-            "rope_qk_separate", "kv_quantize", "kv_dequantize"]
+            "rope_qk_separate", "kv_quantize", "kv_dequantize", "attention_i8_decode"]
 
 
 def build_ops(only):
@@ -329,12 +355,13 @@ def build_ops(only):
     names = OP_ORDER if only is None else [n for n in OP_ORDER + ["copy"] if n in only]
     kv = None
     for name in names:
-        if name in ("kv_quantize", "kv_dequantize") and kv is None:
+        if name in ("kv_quantize", "kv_dequantize", "attention_i8_decode") and kv is None:
             kv = _kv_inputs()
         yield {"swiglu_bias": op_swiglu, "swiglu_bias_strided": op_swiglu_strided, "rmsnorm_residual": op_rmsnorm,
                "softmax_masked": op_softmax, "argmax": op_argmax, "rope_qk": op_rope,
                "rope_qk_separate": lambda: op_rope(True), "copy": op_copy,
-               "kv_quantize": lambda: op_kv_quantize(kv), "kv_dequantize": lambda: op_kv_dequantize(kv)}[name]()
+               "kv_quantize": lambda: op_kv_quantize(kv), "kv_dequantize": lambda: op_kv_dequantize(kv),
+               "attention_i8_decode": lambda: op_attention_i8(kv)}[name]()
 
 
 # ---------------------------------------------------------------------------------------------------------------

@@ -249,6 +249,28 @@ int xs_hip_quantize_kv(void* stream, xs_kv_format format, xs_dtype x_dtype, cons
 int xs_hip_dequantize_kv(void* stream, xs_kv_format format, const void* codes, const void* scales, xs_dtype out_dtype,
                          void* out, int64_t rows, int64_t width);
 
+/* ---- Attention over the int8 KV cache ------------------------------------------------------------------------ */
+
+/* Decode attention reading the int8 cache in place: q f32 [tokens, q_heads, head_dim]; keys and values as
+ * xs_hip_quantize_kv writes them, codes int8 [kv_len, kv_heads, head_dim] and scales f32 [kv_len, kv_heads]; out f32
+ * [tokens, q_heads, head_dim]. Query head h reads KV head h / (q_heads / kv_heads). Query t sits at position
+ * kv_len - tokens + t; causal: keys up to it; window > 0: keys within window - 1 of it (both sides when not causal);
+ * otherwise every key. s = scale * q . k (softcap > 0: softcap * tanh(s / softcap)), softmax, weighted sum of the
+ * values fl32(code * scale) -- cpu_ref::attention over the values the int8 cache stores (ops.cpp:113-156, 535-594;
+ * quant.cpp:269-277), to the reference's device tolerance for a quantized cache (device_attention.cpp:23-27: f32
+ * atol 1e-4, rtol 1e-4). head_dim 64, 128 or 256; 1 to 8 query heads per KV head; q, out, codes 16-byte aligned.
+ * `split` > 1 divides each query's keys over that many waves (flash decoding) and needs
+ * xs_hip_attention_i8_scratch bytes of `scratch` (16-byte aligned) for their partial rows; xs_hip_attention_i8_split
+ * suggests a split that fills the device. Replaces sycl_be::attention_rows_quantized + attention_combine
+ * (sycl_kernels.h:238-240) for the I8 format; key bias, groups, blocks, relative bias and anchored windows are not
+ * taken. */
+int xs_hip_attention_i8(void* stream, const float* q, const void* k_codes, const void* k_scales, const void* v_codes,
+                        const void* v_scales, float* out, int64_t tokens, int64_t q_heads, int64_t kv_heads,
+                        int64_t head_dim, int64_t kv_len, float scale, float softcap, int64_t window, int causal,
+                        int64_t split, void* scratch);
+int64_t xs_hip_attention_i8_split(int64_t tokens, int64_t kv_heads, int64_t kv_len);
+size_t xs_hip_attention_i8_scratch(int64_t tokens, int64_t q_heads, int64_t head_dim, int64_t split);
+
 /* ---- Measurement helper -------------------------------------------------------------------------------------- */
 
 /* y = x, `bytes` bytes (a multiple of 16, 16-byte aligned), with the 128-bit streaming loads and stores of the

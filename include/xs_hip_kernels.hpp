@@ -285,6 +285,45 @@ void dequantize_kv(Stream q, const KvStream& s, CT* out, int64_t rows, int64_t w
                   "dequantize_kv");
 }
 
+// ---- Attention over the quantized KV cache -------------------------------------------------------------------------
+
+struct KvQuantized {  // sycl_kernels.h:206-208
+    KvStream k, v;
+};
+
+// The shape fields of sycl_be::AttentionShape (sycl_kernels.h:158-180) this device takes: causal or full attention with
+// an optional sliding window and softcap.
+struct AttentionShape {
+    int64_t tokens = 0;
+    int64_t q_heads = 0;
+    int64_t kv_heads = 0;
+    int64_t head_dim = 0;
+    int64_t kv_len = 0;
+    float scale = 1.0f;
+    float softcap = 0.0f;
+    int64_t window = 0;
+    bool causal = true;
+};
+
+inline int64_t attention_split(const AttentionShape& s) {
+    return xs_hip_attention_i8_split(s.tokens, s.kv_heads, s.kv_len);
+}
+inline size_t attention_scratch(const AttentionShape& s, int64_t split) {
+    return xs_hip_attention_i8_scratch(s.tokens, s.q_heads, s.head_dim, split);
+}
+
+// attention_rows_quantized + attention_combine (sycl_kernels.h:238-240) for int8 keys and values: `part` holds
+// attention_scratch(s, split) bytes when split > 1.
+inline void attention_rows_quantized(Stream q, const float* qp, const KvQuantized& kv, float* out,
+                                     const AttentionShape& s, int64_t split, float* part) {
+    if (kv.k.format != KvFormat::I8 || kv.v.format != KvFormat::I8)
+        throw Error("hip_be::attention_rows_quantized: only int8 keys and values are read on this device");
+    detail::check(xs_hip_attention_i8(q, qp, kv.k.codes, kv.k.scales, kv.v.codes, kv.v.scales, out, s.tokens,
+                                      s.q_heads, s.kv_heads, s.head_dim, s.kv_len, s.scale, s.softcap, s.window,
+                                      s.causal ? 1 : 0, split, part),
+                  "attention_rows_quantized");
+}
+
 // ---- Device memory -------------------------------------------------------------------------------------------------
 
 // Owns `bytes` of device memory, freed on destruction; the counterpart of the SYCL backend's USM DeviceBuffer

@@ -21,6 +21,8 @@
 //   ora_layer_norm             invariants (zero mean, unit variance of the unweighted output), goldens
 //   ora_l2_clip                invariants (output norm = min(|x|, threshold) to rounding), goldens
 //   ora_reduce_sum             exact sums of small integers, numpy f64 sum, goldens
+//   ora_attention              one-key and equal-key closed forms, a numpy f64 evaluation, window/causal ranges by
+//                              brute force; goldens
 //   ora_softmax                f64 evaluation, sum to 1, masked = 0, shift invariance; goldens
 //   ora_topk                   the reference's tie KATs (tests/unit/backend/moe_ops_cases.h:76-122); sort brute force
 //   ora_rope                   norm preservation per pair, position 0 identity, inv_freq 0 identity, the planted
@@ -326,6 +328,57 @@ void ora_reduce_sum(const float* x, float* y, int64_t outer, int64_t dim, int64_
             double sum = 0;
             for (int64_t d = 0; d < dim; ++d) sum += x[(o * dim + d) * inner + i];
             y[o * inner + i] = static_cast<float>(sum);
+        }
+    }
+}
+
+// cpu_ref::attention / attend_one (ops.cpp:113-156, 535-594) for causal or full attention with an optional sliding
+// window and softcap (no key bias, groups, blocks, relative bias or anchors): q [T, Hq, D], k and v [N, Hkv, D] f32
+// (for an int8 cache, the values it stores), out [T, Hq, D]. Scores, softmax and the weighted sum in f64, the dot
+// product with cpu-ref's four partial sums (ops.cpp:96-108).
+void ora_attention(const float* q, const float* k, const float* v, float* out, int64_t tokens, int64_t q_heads,
+                   int64_t kv_heads, int64_t head_dim, int64_t kv_len, float scale, float softcap, int64_t window,
+                   int causal) {
+    const int64_t per_kv = q_heads / kv_heads;
+    std::vector<double> scores(static_cast<size_t>(kv_len)), acc(static_cast<size_t>(head_dim));
+    for (int64_t t = 0; t < tokens; ++t) {
+        const int64_t pos = kv_len - tokens + t;
+        int64_t first = window > 0 ? std::max<int64_t>(0, pos - window + 1) : 0;
+        int64_t last = causal ? pos : kv_len - 1;
+        if (window > 0) last = std::min(last, pos + window - 1);
+        for (int64_t h = 0; h < q_heads; ++h) {
+            const float* qh = q + (t * q_heads + h) * head_dim;
+            const int64_t kvh = h / per_kv;
+            double max_score = -std::numeric_limits<double>::infinity();
+            for (int64_t j = first; j <= last; ++j) {
+                const float* kj = k + (j * kv_heads + kvh) * head_dim;
+                double s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+                int64_t i = 0;
+                for (; i + 4 <= head_dim; i += 4) {
+                    s0 += static_cast<double>(qh[i]) * kj[i];
+                    s1 += static_cast<double>(qh[i + 1]) * kj[i + 1];
+                    s2 += static_cast<double>(qh[i + 2]) * kj[i + 2];
+                    s3 += static_cast<double>(qh[i + 3]) * kj[i + 3];
+                }
+                for (; i < head_dim; ++i) s0 += static_cast<double>(qh[i]) * kj[i];
+                double sc = scale * ((s0 + s1) + (s2 + s3));
+                if (softcap > 0.0f) sc = softcap * std::tanh(sc / softcap);
+                scores[static_cast<size_t>(j)] = sc;
+                max_score = std::max(max_score, sc);
+            }
+            double denom = 0;
+            for (int64_t j = first; j <= last; ++j) {
+                scores[static_cast<size_t>(j)] = std::exp(scores[static_cast<size_t>(j)] - max_score);
+                denom += scores[static_cast<size_t>(j)];
+            }
+            std::fill(acc.begin(), acc.end(), 0.0);
+            for (int64_t j = first; j <= last; ++j) {
+                const double p = scores[static_cast<size_t>(j)] / denom;
+                const float* vj = v + (j * kv_heads + kvh) * head_dim;
+                for (int64_t d = 0; d < head_dim; ++d) acc[static_cast<size_t>(d)] += p * vj[d];
+            }
+            float* o = out + (t * q_heads + h) * head_dim;
+            for (int64_t d = 0; d < head_dim; ++d) o[d] = static_cast<float>(acc[static_cast<size_t>(d)]);
         }
     }
 }

@@ -92,6 +92,7 @@ class Oracle(_Base):
         L.ora_layer_norm.argtypes = [_fp, _P, _P, _P, C.c_float, _fp, _L, _L]
         L.ora_l2_clip.argtypes = [_fp, _fp, _L, _L, C.c_float, C.c_float]
         L.ora_reduce_sum.argtypes = [_fp, _fp, _L, _L, _L]
+        L.ora_attention.argtypes = [_fp, _fp, _fp, _fp, _L, _L, _L, _L, _L, C.c_float, C.c_float, _L, C.c_int]
         L.ora_rms_norm.argtypes = [_fp, _P, C.c_float, _fp, _L, _L]
         L.ora_add_rms_norm.argtypes = [_fp, _fp, _P, _P, C.c_float, _fp, _fp, _L, _L]
         L.ora_softmax.argtypes = [_fp, _fp, _L, _L]
@@ -186,6 +187,15 @@ class Oracle(_Base):
         y = np.empty(x.shape[:axis] + x.shape[axis + 1:], np.float32)
         self.lib.ora_reduce_sum(x, y, outer, dim, inner)
         return y
+
+    def attention(self, q, k, v, scale, softcap=0.0, window=0, causal=True):
+        """q [T, Hq, D], k and v [N, Hkv, D] f32 -> [T, Hq, D]."""
+        q, k, v = (np.ascontiguousarray(t, np.float32) for t in (q, k, v))
+        tokens, q_heads, d = q.shape
+        out = np.empty_like(q)
+        self.lib.ora_attention(q, k, v, out, tokens, q_heads, k.shape[1], d, k.shape[0], scale, softcap, window,
+                               int(causal))
+        return out
 
     def rms_norm(self, x, weight, eps):
         x = np.ascontiguousarray(x, np.float32)
@@ -297,6 +307,8 @@ class Reference(_Base):
         L.xsref_layer_norm.argtypes = [_fp, _P, _fp, _fp, C.c_float, _L, _L, _fp]
         L.xsref_l2_clip.argtypes = [_fp, _L, _L, C.c_float, C.c_float, _fp]
         L.xsref_reduce_sum.argtypes = [_fp, _L, _L, _L, _fp]
+        L.xsref_attention.argtypes = [_fp, _fp, _fp, _L, _L, _L, _L, _L, C.c_float, C.c_float, _L, C.c_int, C.c_int,
+                                      _fp]
         L.xsref_quantize_kv_row_i8.argtypes = [_fp, _L, _i8]
         L.xsref_quantize_kv_row_i8.restype = C.c_float
         L.xsref_round_trip_kv_i8.argtypes = [_fp, _L, _L]
@@ -356,6 +368,23 @@ class Reference(_Base):
             v = np.ascontiguousarray(valid_len, np.int64)
             self._check(self.lib.xsref_softmax_masked(x, rows, width, scale, _ptr(v), 0, 1, out))
         return out
+
+    def attention(self, q, k, v, scale, softcap=0.0, window=0, causal=True, kv_i8=False, q_fill=None):
+        """q [T, Hq, D] over k, v [N, Hkv, D]. Causal, windowed or int8-cached attention runs as one prefill step of N
+        tokens (queries [N, Hq, D]: `q_fill` rows, or zeros, before q's T rows) and returns its last T rows."""
+        q, k, v = (np.ascontiguousarray(t, np.float32) for t in (q, k, v))
+        tokens, q_heads, d = q.shape
+        n = k.shape[0]
+        cached = causal or window > 0 or kv_i8
+        if cached and tokens != n:
+            fill = np.zeros((n - tokens, q_heads, d), np.float32) if q_fill is None else q_fill
+            qq = np.ascontiguousarray(np.concatenate([fill, q]), np.float32)
+        else:
+            qq = q
+        out = np.empty_like(qq)
+        self._check(self.lib.xsref_attention(qq, k, v, qq.shape[0], q_heads, k.shape[1], d, n, scale, softcap, window,
+                                             int(causal), int(kv_i8), out))
+        return out[-tokens:] if cached else out
 
     def unary_op(self, op, x, a=0.0, b=0.0):
         x = np.ascontiguousarray(x, np.float32)

@@ -283,6 +283,42 @@ int xsref_reduce_sum(const float* x, int64_t outer, int64_t dim, int64_t inner, 
     });
 }
 
+// Attention with AttentionAttrs {scale, sliding_window, softcap, causal}. Causal or windowed attention is driven as the
+// engine drives it: one prefill step of `kv_len` tokens whose keys and values go through a KvCache slot (kv_i8: the
+// session's int8 cache, so the backend itself stores the round-tripped values) and whose queries q [kv_len, Hq, D] all
+// attend; the caller keeps the rows it wants. Otherwise q [tokens, Hq, D] attends to k, v [kv_len, Hkv, D] directly.
+int xsref_attention(const float* q, const float* k, const float* v, int64_t tokens, int64_t q_heads, int64_t kv_heads,
+                    int64_t head_dim, int64_t kv_len, float scale, float softcap, int64_t window, int causal, int kv_i8,
+                    float* out) {
+    return guarded([&] {
+        Graph g;
+        AttentionAttrs attrs;
+        attrs.scale = scale;
+        attrs.softcap = softcap;
+        attrs.sliding_window = window;
+        attrs.causal = causal != 0;
+        SessionOptions o;
+        TensorMap in;
+        const Dims kd{kv_len, kv_heads, head_dim};
+        if (causal || window > 0 || kv_i8) {
+            XS_CHECK(tokens == kv_len, "a cached attention step takes as many queries as keys");
+            const int slot = g.add_kv_slot(kv_heads, head_dim, 0, "kv");
+            const auto [ka, va] = g.kv_cache(slot, g.input("k", DType::F32, {kT, kv_heads, head_dim}),
+                                             g.input("v", DType::F32, {kT, kv_heads, head_dim}));
+            g.output("out", g.attention(g.input("q", DType::F32, {kT, q_heads, head_dim}), ka, va, attrs));
+            o.max_context = kv_len;
+            if (kv_i8) o.kv = quant::KvFormats{quant::KvFormat::I8, quant::KvFormat::I8};
+        } else {
+            g.output("out", g.attention(g.input("q", DType::F32, {tokens, q_heads, head_dim}),
+                                        g.input("k", DType::F32, kd), g.input("v", DType::F32, kd), attrs));
+        }
+        in.emplace("q", borrow(DType::F32, {tokens, q_heads, head_dim}, q));
+        in.emplace("k", borrow(DType::F32, kd, k));
+        in.emplace("v", borrow(DType::F32, kd, v));
+        copy_f32(run_graph(g, in, o).at("out"), out);
+    });
+}
+
 int xsref_rope_inv_freq(double theta, int64_t dim, int64_t pairs, int64_t length, float* out) {
     return guarded([&] { copy_f32(blocks::rope_inv_freq(theta, dim, pairs, length), out); });
 }

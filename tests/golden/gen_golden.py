@@ -257,3 +257,22 @@ save("norms2", {"ln_x": lx, "ln_w": lw, "ln_b": lb, "ln_shift": lsh,
                 "l2_x": cx, "l2_out": ref.l2_clip(cx, 4.0, 1e-6),
                 "rs_x": rx, "rs_axis0": ref.reduce_sum(rx, 0), "rs_axis1": ref.reduce_sum(rx, 1),
                 "rs_axis2": ref.reduce_sum(rx, 2)})
+
+# ---- attention over an int8 KV cache (ops.cpp:113-156, 535-594): the reference's KvCache with kv = i8 stores the
+# round-tripped keys and values; its attention over them. k_rt / v_rt are those stored values (quant.cpp:269-277). ----
+at_t, at_hq, at_hkv, at_d, at_n = 3, 8, 2, 64, 96
+aq = uniform((at_t, at_hq, at_d), 1.5)
+ak = uniform((at_n, at_hkv, at_d), 2.0)
+av = uniform((at_n, at_hkv, at_d), 2.0)
+ak[5, 1, :] *= 20.0  # an outlier key row
+krt = ref.round_trip_kv(ak.reshape(-1, at_d)).reshape(ak.shape)
+vrt = ref.round_trip_kv(av.reshape(-1, at_d)).reshape(av.shape)
+att = {"q": aq, "k": ak, "v": av, "k_rt": krt, "v_rt": vrt}
+for name, scale, cap, window, causal in [("causal", 0.125, 0.0, 0, True), ("window", 0.125, 0.0, 17, True),
+                                         ("full", 0.125, 0.0, 0, False), ("softcap", 0.3, 5.0, 0, True)]:
+    if causal:
+        att[name] = ref.attention(aq, ak, av, scale, cap, window, causal, kv_i8=True)
+    else:
+        att[name] = ref.attention(aq, krt, vrt, scale, cap, window, causal)
+    att[name + "_args"] = np.array([scale, cap, window, float(causal)], np.float64)
+save("attention", att)

@@ -669,3 +669,81 @@ def test_l2_clip_and_reduce_sum(ora):
         t = (rng.standard_normal(shape) * 100).astype(np.float32)
         step(f"reduce_sum {shape} axis {a}")
         assert_f32_close(X.reduce_sum(dev(t), a).numpy(), ora.reduce_sum(t, a), what=f"reduce_sum {shape}")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Decode attention over the int8 KV cache
+
+def assert_attention_close(got, want, what, atol=1e-5, rtol=1e-4):
+    """The reference's device bar for attention at f32 (tests/unit/backend/device_attention.cpp:23):
+    |got - want| <= atol + rtol |want|."""
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    ok = err <= atol + rtol * np.abs(want.astype(np.float64))
+    if not ok.all():
+        i = tuple(np.argwhere(~ok)[0])
+        raise AssertionError(f"{what}: {int((~ok).sum())} of {got.size} beyond atol {atol} rtol {rtol}; first at {i}: "
+                             f"got {got[i]!r} want {want[i]!r}")
+
+
+def cache_i8(x):
+    """Quantizes x [N, Hkv, D] on the device: (codes, scales) as the int8 cache holds them."""
+    n, hkv, d = x.shape
+    return X.quantize_kv(dev(np.ascontiguousarray(x.reshape(n * hkv, d))))
+
+
+def test_attention_i8_goldens(ora):
+    g = golden("attention")
+    kc, ks = cache_i8(g["k"])
+    vc, vs = cache_i8(g["v"])
+    hkv = g["k"].shape[1]
+    for name in ("causal", "window", "full", "softcap"):
+        scale, cap, window, causal = g[name + "_args"]
+        for split in (1, 4, 0):
+            step(f"attention_i8 golden {name} split {split}")
+            y = X.attention_i8(dev(g["q"]), kc, ks, vc, vs, hkv, float(scale), float(cap), int(window), bool(causal),
+                               split).numpy()
+            assert_attention_close(y, g[name], f"{name} split {split}")
+
+
+@pytest.mark.parametrize("t,hq,hkv,d,n,window,cap,causal", [
+    (1, 32, 8, 128, 4097, 0, 0.0, True),
+    (4, 8, 8, 64, 1000, 0, 0.0, True),
+    (2, 12, 4, 128, 777, 100, 0.0, True),
+    (1, 16, 2, 256, 3000, 0, 30.0, True),
+    (3, 6, 1, 64, 500, 0, 0.0, False),
+    (2, 16, 2, 128, 2048, 64, 0.0, False),
+    (1, 40, 5, 128, 1500, 0, 0.0, True),
+    (5, 10, 2, 64, 5, 0, 0.0, True),
+])
+def test_attention_i8_shapes(ora, t, hq, hkv, d, n, window, cap, causal):
+    rng = np.random.default_rng(60 + n)
+    q = rng.standard_normal((t, hq, d)).astype(np.float32)
+    k = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    v = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    k[rng.integers(0, n, 3)] *= 10.0
+    kc, ks = cache_i8(k)
+    vc, vs = cache_i8(v)
+    k_rt = ora.dequantize_kv(kc.numpy(), ks.numpy()).reshape(k.shape)
+    v_rt = ora.dequantize_kv(vc.numpy(), vs.numpy()).reshape(v.shape)
+    scale = 1.0 / math.sqrt(d)
+    want = ora.attention(q, k_rt, v_rt, scale, cap, window, causal)
+    for split in (1, 7, 0):
+        step(f"attention_i8 T{t} H{hq}/{hkv} D{d} N{n} w{window} cap{cap} causal {causal} split {split}")
+        y = X.attention_i8(dev(q), kc, ks, vc, vs, hkv, scale, cap, window, causal, split).numpy()
+        assert_attention_close(y, want, f"attention split {split}")
+
+
+def test_attention_i8_decode_full_size(ora):
+    """One decode step over config 4's cache: 65536 tokens x 8 KV heads x 128, 32 query heads."""
+    rng = np.random.default_rng(70)
+    n, hkv, d, hq = 65536, 8, 128, 32
+    k = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    v = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    q = rng.standard_normal((1, hq, d)).astype(np.float32) * 2
+    kc, ks = cache_i8(k)
+    vc, vs = cache_i8(v)
+    step("attention_i8 decode [1, 32, 128] over 65536 keys")
+    y = X.attention_i8(dev(q), kc, ks, vc, vs, hkv, 1.0 / math.sqrt(d)).numpy()
+    k_rt = ora.dequantize_kv(kc.numpy(), ks.numpy()).reshape(k.shape)
+    v_rt = ora.dequantize_kv(vc.numpy(), vs.numpy()).reshape(v.shape)
+    assert_attention_close(y, ora.attention(q, k_rt, v_rt, 1.0 / math.sqrt(d)), "decode full size")

@@ -480,3 +480,72 @@ def test_oracle_matches_compiled_reference_unary_and_norms(ora):
     t = rng.standard_normal((4, 33, 65)).astype(np.float32)
     for a in range(3):
         assert_exact(ora.reduce_sum(t, a), ref.reduce_sum(t, a))
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Attention (the int8 KV cache reader's semantics)
+
+def test_attention_closed_forms(ora):
+    rng = np.random.default_rng(50)
+    d = 16
+    q = rng.standard_normal((1, 2, d)).astype(np.float32)
+    v = rng.standard_normal((5, 1, d)).astype(np.float32)
+    k = np.zeros((5, 1, d), np.float32)  # equal scores: the mean of the visible values
+    out = ora.attention(q, k, v, 0.25)
+    assert np.allclose(out[0, 0], v[:, 0].astype(np.float64).mean(axis=0), rtol=1e-6, atol=1e-7)
+    # one visible key (window 1, causal): its value exactly
+    out = ora.attention(q, rng.standard_normal((5, 1, d)).astype(np.float32), v, 0.25, window=1)
+    assert_exact(out[0, 0], v[4, 0])
+    assert_exact(out[0, 1], v[4, 0])
+
+
+def test_attention_against_numpy(ora):
+    rng = np.random.default_rng(51)
+    t, hq, hkv, d, n = 3, 8, 2, 32, 40
+    q = rng.standard_normal((t, hq, d)).astype(np.float32)
+    k = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    v = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    for causal, window, cap in [(True, 0, 0.0), (True, 9, 0.0), (False, 0, 0.0), (False, 6, 0.0), (True, 0, 2.0)]:
+        got = ora.attention(q, k, v, 0.3, cap, window, causal)
+        want = np.zeros_like(got, dtype=np.float64)
+        for ti in range(t):
+            pos = n - t + ti
+            lo = max(0, pos - window + 1) if window else 0
+            hi = pos if causal else n - 1
+            if window:
+                hi = min(hi, pos + window - 1)
+            for h in range(hq):
+                kv = h // (hq // hkv)
+                s = 0.3 * (k[lo:hi + 1, kv].astype(np.float64) @ q[ti, h].astype(np.float64))
+                if cap:
+                    s = cap * np.tanh(s / cap)
+                p = np.exp(s - s.max())
+                want[ti, h] = (p / p.sum()) @ v[lo:hi + 1, kv].astype(np.float64)
+        assert np.allclose(got, want, rtol=1e-6, atol=1e-7), (causal, window, cap)
+
+
+def test_attention_goldens(ora):
+    g = golden("attention")
+    for name in ("causal", "window", "full", "softcap"):
+        a = g[name + "_args"]
+        got = ora.attention(g["q"], g["k_rt"], g["v_rt"], float(a[0]), float(a[1]), int(a[2]), bool(a[3]))
+        assert_exact(got, g[name])
+
+
+@pytest.mark.skipif(reference() is None, reason="oracle/_ref not built (no reference tree on this host)")
+def test_oracle_matches_compiled_reference_attention(ora):
+    ref = reference()
+    rng = np.random.default_rng(52)
+    t, hq, hkv, d, n = 2, 8, 2, 64, 150
+    q = rng.standard_normal((t, hq, d)).astype(np.float32)
+    k = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    v = rng.standard_normal((n, hkv, d)).astype(np.float32)
+
+    def rt(x):
+        c, s = ora.quantize_kv(x.reshape(-1, d))
+        return ora.dequantize_kv(c, s).reshape(x.shape)
+
+    # the reference's own int8 KV cache path: its KvCache stores the round-tripped values, its attention reads them
+    assert_exact(ora.attention(q, rt(k), rt(v), 0.125), ref.attention(q, k, v, 0.125, kv_i8=True))
+    assert_exact(ora.attention(q, k, v, 0.125, 0.0, 33, True), ref.attention(q, k, v, 0.125, 0.0, 33, True))
+    assert_exact(ora.attention(q, k, v, 0.125, 0.0, 0, False), ref.attention(q, k, v, 0.125, 0.0, 0, False))

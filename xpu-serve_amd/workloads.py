@@ -89,6 +89,9 @@ ALGO_BYTES: Dict[str, int] = {
     "swiglu_bias_strided": 3 * 2048 * 9728 * 2 + 9728 * 2,
     "softmax_masked": 32 * 30000 * 4 + 32 * 32768 * 4,             # valid keys read; every key written
     "argmax": 151936 * 4 + 8,
+    # one decode step over config 4's int8 cache: K and V codes [65536, 8, 128] and scales [65536, 8]; q and out
+    # [1, 32, 128] f32
+    "attention_i8_decode": 2 * (65536 * 8 * 128 + 65536 * 8 * 4) + 2 * 32 * 128 * 4,
     "rope_qk": 2 * (8192 * 32 * 128 * 2) + 2 * (8192 * 8 * 128 * 2) + 8192 * 4 + 64 * 4,
     "kv_quantize": 2 * (65536 * 8 * 128 * 2 + 65536 * 8 * 128 + 65536 * 8 * 4),
     "kv_dequantize": 2 * (65536 * 8 * 128 + 65536 * 8 * 4 + 65536 * 8 * 128 * 2),

@@ -105,8 +105,12 @@ _SIGS = {
     "xs_hip_quantize_kv": [_P, _INT, _INT, _P, _P, _P, _I64, _I64],
     "xs_hip_dequantize_kv": [_P, _INT, _P, _P, _INT, _P, _I64, _I64],
     "xs_hip_copy": [_P, _P, _P, C.c_size_t],
+    "xs_hip_attention_i8": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _F, _I64, _INT, _I64, _P],
+    "xs_hip_attention_i8_split": [_I64, _I64, _I64],
+    "xs_hip_attention_i8_scratch": [_I64, _I64, _I64, _I64],
 }
 _RESTYPES = {"xs_hip_topk_scratch": C.c_size_t, "xs_hip_softmax_scratch": C.c_size_t,
+             "xs_hip_attention_i8_split": C.c_int64, "xs_hip_attention_i8_scratch": C.c_size_t,
              "xs_hip_last_error": C.c_char_p}
 
 _lib_handle = None
@@ -329,6 +333,27 @@ def unary(op: int, x: DeviceTensor, a: float = 0.0, b: float = 0.0, y_dtype: Opt
     call("xs_hip_unary", stream, op, x.dtype, C.c_void_p(x.ptr), y.dtype, C.c_void_p(y.ptr), x.numel, C.c_float(a),
          C.c_float(b))
     return y
+
+
+def attention_i8(q: DeviceTensor, k_codes: DeviceTensor, k_scales: DeviceTensor, v_codes: DeviceTensor,
+                 v_scales: DeviceTensor, kv_heads: int, scale: float, softcap: float = 0.0, window: int = 0,
+                 causal: bool = True, split: int = 0, stream=None) -> DeviceTensor:
+    """Decode attention of q [T, Hq, D] (f32) over an int8 cache: codes [N * kv_heads, D] (or [N, kv_heads, D]) and
+    scales [N * kv_heads] from quantize_kv, for keys and values. split 0: the library's suggestion."""
+    tokens, q_heads, d = q.shape
+    kv_len = k_codes.numel // (kv_heads * d)
+    if split <= 0:
+        split = int(lib().xs_hip_attention_i8_split(tokens, kv_heads, kv_len))
+    out = DeviceTensor.empty(F32, q.shape)
+    nbytes = int(lib().xs_hip_attention_i8_scratch(tokens, q_heads, d, split))
+    scratch = DeviceBuffer(nbytes) if nbytes else None
+    call("xs_hip_attention_i8", stream, C.c_void_p(q.ptr), C.c_void_p(k_codes.ptr), C.c_void_p(k_scales.ptr),
+         C.c_void_p(v_codes.ptr), C.c_void_p(v_scales.ptr), C.c_void_p(out.ptr), tokens, q_heads, kv_heads, d, kv_len,
+         C.c_float(scale), C.c_float(softcap), window, int(causal), split,
+         C.c_void_p(scratch.ptr) if scratch else None)
+    if scratch is not None:
+        synchronize()  # the scratch is freed when this returns
+    return out
 
 
 def add_rms_norm(x: DeviceTensor, residual: DeviceTensor, weight: Optional[DeviceTensor], eps: float,
