@@ -9,14 +9,15 @@
 // Launcher replaced: sycl_be::attention_rows_quantized with attention_combine (src/backend/sycl/sycl_kernels.h:
 // 238-240), I8 rows (sycl_kv_rows.h:37-69).
 //
-// Layout: one workgroup of four waves per (token, KV head, key split). The G query heads sharing the KV head are
-// handled together, so each key and value row is read once for all of them. L lanes cover one key's head_dim
-// (DPL = head_dim / L codes a lane: one 16- or 8-byte load of key codes and one of value codes), so a wave works on
-// 64 / L keys at once; each lane group keeps four keys' loads in flight. Scores: each lane's partial dot product in f32, reduced over its L lanes by
-// DPP; times the key's scale and the softmax scale. An online softmax per head (the running max moves, and the
-// accumulator is rescaled, only when a larger score arrives) accumulates p * v_scale * codes in f32. At the end the
-// wave's key groups merge their (max, sum, accumulator) by shuffles and the four waves through LDS. With one split the wave writes the output; with
-// several it writes [head_dim partial sums, max, sum] rows that xs_hip_attention_combine merges (flash decoding).
+// Layout: one workgroup of four waves per (token, KV head, key split); the G query heads sharing the KV head are
+// handled together, so each key and value row is read once for all of them. Each wave takes every fourth tile of 64
+// consecutive keys of the split: it loads the tile's key codes into LDS and its value codes into registers, whole
+// rows per 128-bit load instruction; then a lane per key computes its key's scores against the G heads (q is the same
+// for every lane: LDS broadcasts), the tile's max per head moves the wave's running max (rescaling the
+// accumulator at most once per tile), and each key's p * v_scale goes to LDS; then each lane accumulates the value
+// rows it loaded, 8 dims each, weighted in f32. The lanes sharing dims add up (they share the running max), and the
+// four waves' (max, sum, accumulator) merge in LDS at the end. With one split the workgroup writes the output; with
+// several it writes [head_dim partial sums, max, sum] rows that a second launch merges (flash decoding).
 //
 // Accuracy: f32 accumulation where cpu-ref accumulates in f64, and the key scale applied to the dot product rather
 // than to each product -- within the reference's own device tolerance for a quantized cache
@@ -50,49 +51,44 @@ __device__ __forceinline__ void key_range(const AttnArgs& a, int64_t t, int64_t&
     if (a.window > 0 && pos + a.window - 1 < last) last = pos + a.window - 1;
 }
 
-template <int DPL>
-using Codes = typename std::conditional<DPL == 16, u32x4, uint64_t>::type;
-
-template <int DPL>
-__device__ __forceinline__ Codes<DPL> load_codes(const int8_t* p) {
-    if constexpr (DPL == 16) return ld128_nt(p);
-    else return __builtin_nontemporal_load(reinterpret_cast<const uint64_t*>(p));
-}
-
-// Code i of a lane's DPL codes, as f32.
-template <int DPL>
-__device__ __forceinline__ float code_at(const Codes<DPL>& c, int i) {
-    uint32_t w;
-    if constexpr (DPL == 16) w = c[i >> 2];
-    else w = static_cast<uint32_t>(c >> (32 * (i >> 2)));
-    return static_cast<float>(static_cast<int8_t>((w >> (8 * (i & 3))) & 0xffu));
-}
-
-constexpr int kWaves = 4;  // waves a workgroup; they split the workgroup's keys and merge in LDS
-constexpr int kUnroll = 4;  // keys a lane group has in flight
+constexpr int kWaves = 4;    // waves a workgroup; each takes every fourth tile of 64 keys, and they merge in LDS
+constexpr int kTile = 64;    // keys a wave stages at once: one a lane
 
 // Merges (m, l, acc) of another key set into this one: the online-softmax combine.
-template <int DPL>
+template <int N>
 __device__ __forceinline__ void merge(float& m, float& l, float* acc, float mo, float lo, const float* acco) {
     const float mm = fmaxf(m, mo);
     const float ca = m == -INFINITY ? 0.0f : __expf(m - mm);  // an empty side (max -inf) contributes nothing
     const float cb = mo == -INFINITY ? 0.0f : __expf(mo - mm);
     l = l * ca + lo * cb;
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) acc[i] = acc[i] * ca + acco[i] * cb;
+    for (int i = 0; i < N; ++i) acc[i] = acc[i] * ca + acco[i] * cb;
     m = mm;
 }
 
-template <int G, int DPL, int L>
-__global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a) {
-    constexpr int KG = 64 / L;        // keys a wave works on at once
-    constexpr int KGB = KG * kWaves;  // ... a workgroup
-    __shared__ float merge_buf[kWaves][G][L * DPL + 2];
+__device__ __forceinline__ float byte_f32(uint32_t w, int k) {
+    return static_cast<float>(static_cast<int8_t>((w >> (8 * k)) & 0xffu));
+}
+
+// G query heads per KV head, D head_dim (64, 128 or 256), DPL value dims a lane (8 or 16).
+template <int G, int D, int DPL>
+__global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a, const float* __restrict__ qg) {
+    using VCodes = typename std::conditional<DPL == 16, u32x4, uint64_t>::type;
+    constexpr int ROW = D + 16;            // LDS bytes a staged key row: 16 bytes of padding spread the lanes' rows
+                                           // over the banks when each lane reads its own row
+    constexpr int LPR = D / DPL;           // lanes a row with DPL-byte loads
+    constexpr int RPI = 64 / LPR;          // rows one load instruction covers
+    constexpr int VI = kTile / RPI;        // load instructions a tile
+    constexpr int TILE = kTile * ROW;
+    // Each wave's key tile; after the last tile the same LDS holds the waves' results for the merge.
+    constexpr int SMEM = kWaves * TILE > kWaves * G * (D + 2) * 4 ? kWaves * TILE : kWaves * G * (D + 2) * 4;
+    __shared__ __align__(16) uint8_t smem[SMEM];
+    __shared__ __align__(16) float ptile[kWaves][kTile][G];
+    __shared__ __align__(16) float qs[G][D];
+    auto mbuf = reinterpret_cast<float(*)[G][D + 2]>(smem);
+
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    const int li = lane % L;   // which DPL codes of the row
-    const int kg = lane / L;   // which key of the wave's KG
-    const int64_t D = a.head_dim;
     const int64_t row = blockIdx.x;  // (t, kv head)
     const int64_t t = row / a.kv_heads;
     const int64_t kvh = row - t * a.kv_heads;
@@ -106,19 +102,19 @@ __global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a) {
     int64_t k1 = k0 + per - 1;
     if (k1 > last) k1 = last;
 
-    float qv[G][DPL];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const float* qp = a.q + (t * a.q_heads + kvh * G + g) * D + li * DPL;
-#pragma unroll
-        for (int i = 0; i < DPL; i += 4) {
-            const u32x4 raw = ld128(qp + i);
-#pragma unroll
-            for (int w = 0; w < 4; ++w) qv[g][i + w] = __uint_as_float(raw[w]) * a.scale;
-        }
+    // q of the G heads, the same for every lane: in LDS, read by broadcast.
+    {
+        const float* q = qg + (t * a.q_heads + kvh * G) * D;
+        for (int i = threadIdx.x * 4; i < G * D; i += 64 * kWaves * 4)
+            *reinterpret_cast<u32x4*>(&qs[0][0] + i) = ld128(q + i);
     }
+    __syncthreads();
+
+    // Weighted sum layout: lane l accumulates dims (l % LPR) * DPL .. + DPL - 1 over the tile rows l / LPR, + RPI, ...
+    const int cl = (lane % LPR) * DPL;
+    const int rl0 = lane / LPR;
     float acc[G][DPL];
-    float m[G], l[G];
+    float m[G], l[G];  // m: the wave's running max per head; l: this lane's share of the sum of exponentials
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         m[g] = -INFINITY;
@@ -127,87 +123,157 @@ __global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a) {
         for (int i = 0; i < DPL; ++i) acc[g][i] = 0.0f;
     }
 
-    // Key j of this lane group: k0 + kg + wave * KG + n * KGB. Each pass loads kUnroll keys (clamped to the last one,
-    // whose repeats are not used), then folds them in.
-    for (int64_t jb = k0 + wave * KG + kg; jb <= k1; jb += kUnroll * KGB) {
-        Codes<DPL> kc[kUnroll], vc[kUnroll];
-        float ksc[kUnroll], vsc[kUnroll];
+    const int64_t span = k1 >= k0 ? k1 - k0 + 1 : 0;
+    const int64_t tiles = (span + kTile - 1) / kTile;
+    uint8_t* kt = smem + wave * TILE;
+    // The waves run independently: wave w takes tiles w, w + kWaves, ... and touches only its own LDS, whose writes
+    // and reads are ordered within the wave (wave_sync). Each tile's key and value codes are loaded into registers a
+    // tile ahead, so HBM reads stay in flight while the previous tile is computed.
+    auto wave_sync = [] {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    auto load_tile = [&](int64_t tile, VCodes* kw, VCodes* vw) {
+        const int64_t j0 = k0 + tile * kTile;
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const int64_t j = jb + u * KGB <= k1 ? jb + u * KGB : k1;
-            const int64_t r = j * a.kv_heads + kvh;
-            kc[u] = load_codes<DPL>(a.kc + r * D + li * DPL);
-            vc[u] = load_codes<DPL>(a.vc + r * D + li * DPL);
-            ksc[u] = a.ks[r];
-            vsc[u] = a.vs[r];
-        }
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            if (jb + u * KGB > k1) break;  // the lane group's keys end together
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float d = 0.0f;
-#pragma unroll
-                for (int i = 0; i < DPL; ++i) d = fmaf(qv[g][i], code_at<DPL>(kc[u], i), d);
-                d = group_reduce<L, OpSum>(d);
-                float sc = d * ksc[u];
-                if (a.softcap > 0.0f) sc = a.softcap * tanhf(sc / a.softcap);
-                if (sc > m[g]) {
-                    const float c = __expf(m[g] - sc);
-                    l[g] *= c;
-#pragma unroll
-                    for (int i = 0; i < DPL; ++i) acc[g][i] *= c;
-                    m[g] = sc;
-                }
-                const float p = __expf(sc - m[g]);
-                l[g] += p;
-                const float pv = p * vsc[u];
-#pragma unroll
-                for (int i = 0; i < DPL; ++i) acc[g][i] = fmaf(pv, code_at<DPL>(vc[u], i), acc[g][i]);
+        for (int i = 0; i < VI; ++i) {
+            int64_t j = j0 + i * RPI + rl0;
+            j = j <= k1 ? j : k1;
+            const int64_t off = (j * a.kv_heads + kvh) * D + cl;
+            if constexpr (DPL == 16) {
+                kw[i] = ld128_nt(a.kc + off);
+                vw[i] = ld128_nt(a.vc + off);
+            } else {
+                kw[i] = __builtin_nontemporal_load(reinterpret_cast<const uint64_t*>(a.kc + off));
+                vw[i] = __builtin_nontemporal_load(reinterpret_cast<const uint64_t*>(a.vc + off));
             }
         }
+    };
+    VCodes kw[VI], vw[VI];
+    if (wave < tiles) load_tile(wave, kw, vw);
+    for (int64_t tile = wave; tile < tiles; tile += kWaves) {
+        const int64_t j0 = k0 + tile * kTile;  // keys j0 .. j0 + 63 (those past k1 clamped to it, weights 0)
+#pragma unroll
+        for (int i = 0; i < VI; ++i) *reinterpret_cast<VCodes*>(kt + (i * RPI + rl0) * ROW + cl) = kw[i];
+        const int64_t jl = j0 + lane;  // the lane's key in the score phase
+        const bool valid = jl <= k1;
+        const int64_t rk = (valid ? jl : k1) * a.kv_heads + kvh;
+        const float ksc = a.ks[rk];
+        const float vsc = a.vs[rk];
+        VCodes vcur[VI];
+#pragma unroll
+        for (int i = 0; i < VI; ++i) vcur[i] = vw[i];
+        if (tile + kWaves < tiles) load_tile(tile + kWaves, kw, vw);
+        wave_sync();
+
+        // Scores, a lane per key: its whole row of codes against q.
+        float sc[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) sc[g] = 0.0f;
+#pragma unroll 2
+        for (int c = 0; c < D; c += 16) {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(kt + lane * ROW + c);
+            float code[16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) code[k] = byte_f32(w[k >> 2], k & 3);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+#pragma unroll
+                for (int k = 0; k < 16; k += 4) {
+                    const u32x4 qv = *reinterpret_cast<const u32x4*>(&qs[g][c + k]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) sc[g] = fmaf(__uint_as_float(qv[e]), code[k + e], sc[g]);
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float x = sc[g] * ksc * a.scale;
+            if (a.softcap > 0.0f) x = a.softcap * tanhf(x / a.softcap);
+            sc[g] = valid ? x : -INFINITY;
+        }
+        // The tile's max per head moves the running max; p = exp(s - max) per key, times the value scale, to LDS.
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float mt = group_reduce<64, OpMax>(sc[g]);
+            const float mn = fmaxf(m[g], mt);
+            if (mn > m[g]) {  // uniform across the wave
+                const float c = m[g] == -INFINITY ? 0.0f : __expf(m[g] - mn);
+                l[g] *= c;
+#pragma unroll
+                for (int i = 0; i < DPL; ++i) acc[g][i] *= c;
+                m[g] = mn;
+            }
+            const float p = valid ? __expf(sc[g] - m[g]) : 0.0f;
+            l[g] += p;
+            ptile[wave][lane][g] = p * vsc;
+        }
+        wave_sync();
+
+        // Weighted sum: the value rows in registers, each with its key's p * v_scale from LDS.
+#pragma unroll
+        for (int i = 0; i < VI; ++i) {
+            const int r = i * RPI + rl0;
+            float pv[G];
+#pragma unroll
+            for (int g = 0; g < G; ++g) pv[g] = ptile[wave][r][g];
+#pragma unroll
+            for (int k = 0; k < DPL; ++k) {
+                uint32_t word;
+                if constexpr (DPL == 16) word = vcur[i][k >> 2];
+                else word = static_cast<uint32_t>(vcur[i] >> (32 * (k >> 2)));
+                const float code = byte_f32(word, k & 3);
+#pragma unroll
+                for (int g = 0; g < G; ++g) acc[g][k] = fmaf(pv[g], code, acc[g][k]);
+            }
+            // One row at a time: keeps the compiler from widening every row's codes at once.
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        wave_sync();  // the key tile and the weights are rewritten next tile
     }
 
-    // Merge the wave's KG key groups: lanes li, li + L, ... hold the same dims of different keys.
+    // The wave's lanes that share dims hold sums over different rows with the same running max: add them. Then the
+    // four waves merge through LDS (the tiles' space: every wave has left the loop).
 #pragma unroll
-    for (int off = L; off < 64; off <<= 1) {
+    for (int off = LPR; off < 64; off <<= 1) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            float ao[DPL];
 #pragma unroll
-            for (int i = 0; i < DPL; ++i) ao[i] = __shfl_xor(acc[g][i], off, 64);
-            merge<DPL>(m[g], l[g], acc[g], __shfl_xor(m[g], off, 64), __shfl_xor(l[g], off, 64), ao);
+            for (int i = 0; i < DPL; ++i) acc[g][i] += __shfl_xor(acc[g][i], off, 64);
         }
     }
-    // ... then the workgroup's waves, through LDS.
-    if (kg == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) l[g] = group_reduce<64, OpSum>(l[g]);
+    __syncthreads();
+    if (lane < LPR) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
 #pragma unroll
-            for (int i = 0; i < DPL; ++i) merge_buf[wave][g][li * DPL + i] = acc[g][i];
-            if (li == 0) {
-                merge_buf[wave][g][L * DPL] = m[g];
-                merge_buf[wave][g][L * DPL + 1] = l[g];
+            for (int i = 0; i < DPL; ++i) mbuf[wave][g][cl + i] = acc[g][i];
+            if (lane == 0) {
+                mbuf[wave][g][D] = m[g];
+                mbuf[wave][g][D + 1] = l[g];
             }
         }
     }
     __syncthreads();
-    if (wave != 0 || kg != 0) return;  // lanes 0 .. L-1 of wave 0 finish
+    if (wave != 0 || lane >= LPR) return;
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             float ao[DPL];
 #pragma unroll
-            for (int i = 0; i < DPL; ++i) ao[i] = merge_buf[w][g][li * DPL + i];
-            merge<DPL>(m[g], l[g], acc[g], merge_buf[w][g][L * DPL], merge_buf[w][g][L * DPL + 1], ao);
+            for (int i = 0; i < DPL; ++i) ao[i] = mbuf[w][g][cl + i];
+            merge<DPL>(m[g], l[g], acc[g], mbuf[w][g][D], mbuf[w][g][D + 1], ao);
         }
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         const int64_t h = kvh * G + g;
         if (a.part == nullptr) {
-            float* o = a.out + (t * a.q_heads + h) * D + li * DPL;
+            float* o = a.out + (t * a.q_heads + h) * D + cl;
             const float inv = 1.0f / l[g];
 #pragma unroll
             for (int i = 0; i < DPL; i += 4) {
@@ -219,8 +285,8 @@ __global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a) {
         } else {
             float* pr = a.part + ((t * a.q_heads + h) * a.split + s) * (D + 2);
 #pragma unroll
-            for (int i = 0; i < DPL; ++i) pr[li * DPL + i] = acc[g][i];
-            if (li == 0) {
+            for (int i = 0; i < DPL; ++i) pr[cl + i] = acc[g][i];
+            if (lane == 0) {
                 pr[D] = m[g];
                 pr[D + 1] = l[g];
             }
@@ -228,58 +294,77 @@ __global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a) {
     }
 }
 
-// out [rows, D] from `split` partial rows [D sums, max, sum] each (sycl_be::attention_combine's layout). One wave a
-// row: the lanes take the splits for the max, the weights and the denominator, then the dims, each summing its
-// column over the splits with the weights from LDS.
+// out [rows, D] from `split` partial rows [D sums, max, sum] each (sycl_be::attention_combine's layout). A workgroup of
+// four waves a row: the threads take the splits for the max, the weights and the denominator, then (dim, split
+// quarter) pairs, each summing its share of the column with the weights from LDS; the quarters add up in LDS.
 constexpr int kMaxSplit = 256;
 
-__global__ __launch_bounds__(64) void attention_combine_rows(const float* part, float* out, int split, int64_t D) {
+__global__ __launch_bounds__(256) void attention_combine_rows(const float* part, float* out, int split, int64_t D) {
     __shared__ float weight[kMaxSplit];
+    __shared__ float red[256];
     const int64_t r = blockIdx.x;
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x;
     const float* pr = part + r * split * (D + 2);
     float mx = -INFINITY;
-    for (int s = lane; s < split; s += 64) mx = fmaxf(mx, pr[s * (D + 2) + D]);
+    for (int s = tid; s < split; s += 256) mx = fmaxf(mx, pr[s * (D + 2) + D]);
     mx = group_reduce<64, OpMax>(mx);
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
     float den = 0.0f;
-    for (int s = lane; s < split; s += 64) {
+    for (int s = tid; s < split; s += 256) {
         const float ms = pr[s * (D + 2) + D];
         const float w = ms == -INFINITY ? 0.0f : __expf(ms - mx);
         weight[s] = w;
         den += pr[s * (D + 2) + D + 1] * w;
     }
     den = group_reduce<64, OpSum>(den);
+    if ((tid & 63) == 0) red[tid >> 6] = den;
     __syncthreads();
+    den = (red[0] + red[1]) + (red[2] + red[3]);
     const float inv = 1.0f / den;
-    for (int64_t d = lane; d < D; d += 64) {
-        float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f, acc3 = 0.0f;
-        int s = 0;
-        for (; s + 4 <= split; s += 4) {
-            acc0 += pr[(s + 0) * (D + 2) + d] * weight[s + 0];
-            acc1 += pr[(s + 1) * (D + 2) + d] * weight[s + 1];
-            acc2 += pr[(s + 2) * (D + 2) + d] * weight[s + 2];
-            acc3 += pr[(s + 3) * (D + 2) + d] * weight[s + 3];
+    __syncthreads();
+    // Dims in chunks of 64: thread (d, quarter) sums splits quarter, quarter + 4, ...
+    const int dl = tid & 63, quarter = tid >> 6;
+    for (int64_t d0 = 0; d0 < D; d0 += 64) {
+        const int64_t d = d0 + dl;
+        float acc = 0.0f;
+        if (d < D) {
+            // eight loads in flight before the first is used
+            for (int s0 = quarter; s0 < split; s0 += 32) {
+                float v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int s = s0 + 4 * u;
+                    v[u] = s < split ? pr[s * (D + 2) + d] : 0.0f;
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int s = s0 + 4 * u;
+                    acc += s < split ? v[u] * weight[s] : 0.0f;
+                }
+            }
         }
-        for (; s < split; ++s) acc0 += pr[s * (D + 2) + d] * weight[s];
-        out[r * D + d] = ((acc0 + acc1) + (acc2 + acc3)) * inv;
+        red[tid] = acc;
+        __syncthreads();
+        if (quarter == 0 && d < D) out[r * D + d] = ((red[dl] + red[64 + dl]) + (red[128 + dl] + red[192 + dl])) * inv;
+        __syncthreads();
     }
 }
 
-template <int G, int DPL, int L>
+template <int G, int D>
 void launch_rows(hipStream_t s, const AttnArgs& a) {
     const dim3 grid(static_cast<unsigned>(a.tokens * a.kv_heads), static_cast<unsigned>(a.split));
-    attention_i8_rows<G, DPL, L><<<grid, 64 * kWaves, 0, s>>>(a);
+    attention_i8_rows<G, D, 8><<<grid, 64 * kWaves, 0, s>>>(a, a.q);
 }
 
-// Heads per KV head G up to 4 take 16 codes a lane, more take 8 (the registers of q and the accumulator).
 template <int G>
 int launch_g(hipStream_t s, const AttnArgs& a) {
-    constexpr int DPL = G <= 4 ? 16 : 8;
-    switch (a.head_dim / DPL) {
-        case 4: launch_rows<G, DPL, 4>(s, a); break;
-        case 8: launch_rows<G, DPL, 8>(s, a); break;
-        case 16: launch_rows<G, DPL, 16>(s, a); break;
-        case 32: launch_rows<G, DPL, 32>(s, a); break;
+    switch (a.head_dim) {
+        case 64: launch_rows<G, 64>(s, a); break;
+        case 128: launch_rows<G, 128>(s, a); break;
+        case 256: launch_rows<G, 256>(s, a); break;
         default:
             return fail(XS_HIP_EUNSUPPORTED, "xs_hip_attention_i8: head_dim " + std::to_string(a.head_dim) +
                                                  " (supported: 64, 128, 256)");
@@ -358,7 +443,7 @@ int xs_hip_attention_i8(void* stream, const float* q, const void* k_codes, const
                                                  " query heads per KV head (supported: 1 to 8)");
     }
     if (rc != XS_HIP_OK || split == 1) return rc;
-    attention_combine_rows<<<static_cast<unsigned>(tokens * q_heads), 64, 0, s>>>(
+    attention_combine_rows<<<static_cast<unsigned>(tokens * q_heads), 256, 0, s>>>(
         static_cast<const float*>(scratch), out, static_cast<int>(split), head_dim);
     return check_launch("xs_hip_attention_i8 (combine)");
 }
