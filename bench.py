@@ -188,6 +188,51 @@ def op_rmsnorm():
     return Op("rmsnorm_residual", W.ALGO_BYTES["rmsnorm_residual"], 4 * rows * width * 4, mk, go, 1, "rms_norm_vec")
 
 
+def op_row_norms(kind):
+    """layer_norm, l2_clip or reduce_sum (over the rows or the columns) of config 0's x [512, 2560] f32."""
+    a = W.config0().arrays
+    rows, width = a["x"].shape
+    x0, w0 = X.DeviceTensor.from_numpy(a["x"]), X.DeviceTensor.from_numpy(a["weight"])
+    b0 = X.DeviceTensor.from_numpy((a["weight"] - 1.0).astype(np.float32))
+    out_shape = {"reduce_sum_rows": (rows,), "reduce_sum_cols": (width,)}.get(kind, (rows, width))
+
+    def mk():
+        s = (dcopy(x0), dcopy(w0), dcopy(b0), X.DeviceTensor.empty(X.F32, out_shape))
+        need(s[0], rows * width * 4, kind)
+        return s
+
+    def go(s, stream):
+        x, w, b, y = s
+        if kind == "layer_norm":
+            X.call("xs_hip_layer_norm", stream, X.F32, vp(x), None, vp(w), vp(b), X.F32, vp(y), rows, width,
+                   C.c_float(1e-5))
+        elif kind == "l2_clip":
+            X.call("xs_hip_l2_clip", stream, vp(x), vp(y), rows, width, C.c_float(40.0), C.c_float(1e-6))
+        elif kind == "reduce_sum_rows":
+            X.call("xs_hip_reduce_sum", stream, vp(x), vp(y), rows, width, 1)
+        else:
+            X.call("xs_hip_reduce_sum", stream, vp(x), vp(y), 1, rows, width)
+    kernel = {"layer_norm": "row_norm_vec", "l2_clip": "row_norm_vec", "reduce_sum_rows": "reduce_rows",
+              "reduce_sum_cols": "reduce_cols"}[kind]
+    return Op(kind, W.ALGO_BYTES[kind], W.ALGO_BYTES[kind], mk, go, 1, kernel)
+
+
+def op_unary_softcap():
+    """softcap 30 of config 1's gate [2048, 9728], bf16 in and out."""
+    g0 = X.DeviceTensor.from_numpy(W.config1().arrays["gate"], X.BF16)
+    n = g0.numel
+
+    def mk():
+        s = (dcopy(g0), X.DeviceTensor.empty(X.BF16, g0.shape))
+        need(s[0], n * 2, "unary")
+        return s
+
+    def go(s, stream):
+        x, y = s
+        X.call("xs_hip_unary", stream, X.SOFTCAP, X.BF16, vp(x), X.BF16, vp(y), n, C.c_float(30.0), C.c_float(0.0))
+    return Op("unary_softcap", W.ALGO_BYTES["unary_softcap"], W.ALGO_BYTES["unary_softcap"], mk, go, 1, "ew2d_vec")
+
+
 def op_softmax():
     c = W.config2a()
     heads, _, keys = c.arrays["scores"].shape
@@ -347,7 +392,8 @@ def op_copy(n=256 << 20):
 
 
 OP_ORDER = ["swiglu_bias", "swiglu_bias_strided", "rmsnorm_residual", "softmax_masked", "argmax", "rope_qk",
-            "rope_qk_separate", "kv_quantize", "kv_dequantize", "attention_i8_decode"]
+            "rope_qk_separate", "kv_quantize", "kv_dequantize", "attention_i8_decode", "layer_norm", "l2_clip",
+            "reduce_sum_rows", "reduce_sum_cols", "unary_softcap"]
 
 
 def build_ops(only):
@@ -361,7 +407,10 @@ def build_ops(only):
                "softmax_masked": op_softmax, "argmax": op_argmax, "rope_qk": op_rope,
                "rope_qk_separate": lambda: op_rope(True), "copy": op_copy,
                "kv_quantize": lambda: op_kv_quantize(kv), "kv_dequantize": lambda: op_kv_dequantize(kv),
-               "attention_i8_decode": lambda: op_attention_i8(kv)}[name]()
+               "attention_i8_decode": lambda: op_attention_i8(kv), "unary_softcap": op_unary_softcap,
+               "layer_norm": lambda: op_row_norms("layer_norm"), "l2_clip": lambda: op_row_norms("l2_clip"),
+               "reduce_sum_rows": lambda: op_row_norms("reduce_sum_rows"),
+               "reduce_sum_cols": lambda: op_row_norms("reduce_sum_cols")}[name]()
 
 
 # ---------------------------------------------------------------------------------------------------------------

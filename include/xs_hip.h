@@ -145,8 +145,9 @@ int xs_hip_add3(void* stream, const float* a, const float* b, const float* c, xs
 
 /* y = op(x), n elements, x and y F32, F16 or BF16: Scale (y = x * a), Tanh, GeluTanh, Softcap (y = a tanh(x / a)),
  * Sigmoid, Silu, Softplus (identity above 20), Clamp (min(max(x, a), b), NaN kept), Gelu. Replaces sycl_be::unary
- * (sycl_kernels.h:21-25), whose x is f32; semantics cpu_ref::scale ... clamp (ops.cpp:209-258): f32 for Scale and
- * Clamp, f64 for the transcendental ops, rounded once. */
+ * (sycl_kernels.h:21-25), whose x is f32; semantics cpu_ref::scale ... clamp (ops.cpp:209-258): Scale and Clamp
+ * exactly as cpu-ref's f32 arithmetic, the GELUs in f64 as cpu-ref, Tanh / Softcap / Softplus / Sigmoid / Silu with
+ * f32 transcendentals (within 1e-5 relative of cpu-ref's f64 for f32 outputs, within one unit of a 16-bit output). */
 int xs_hip_unary(void* stream, xs_unary_op op, xs_dtype x_dtype, const void* x, xs_dtype y_dtype, void* y, int64_t n,
                  float a, float b);
 /* y = act(x) * b, same shapes, x/b in x_dtype (F32, F16, BF16), y in y_dtype; act is SILU, GELU_TANH, SIGMOID or

@@ -89,10 +89,13 @@ __global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a, con
 
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    const int64_t row = blockIdx.x;  // (t, kv head)
+    // Grid (split, token x KV head): consecutive workgroup ids are splits, so the KV heads of one split share an id
+    // residue mod 8 -- the same XCD and L2 -- and the lines of key/value rows and scales those heads share are fetched
+    // once per XCD rather than once per head.
+    const int64_t row = blockIdx.y;  // (t, kv head)
     const int64_t t = row / a.kv_heads;
     const int64_t kvh = row - t * a.kv_heads;
-    const int s = blockIdx.y;
+    const int s = blockIdx.x;
 
     int64_t first, last;
     key_range(a, t, first, last);
@@ -355,7 +358,7 @@ __global__ __launch_bounds__(256) void attention_combine_rows(const float* part,
 
 template <int G, int D>
 void launch_rows(hipStream_t s, const AttnArgs& a) {
-    const dim3 grid(static_cast<unsigned>(a.tokens * a.kv_heads), static_cast<unsigned>(a.split));
+    const dim3 grid(static_cast<unsigned>(a.split), static_cast<unsigned>(a.tokens * a.kv_heads));
     attention_i8_rows<G, D, 8><<<grid, 64 * kWaves, 0, s>>>(a, a.q);
 }
 
@@ -417,7 +420,7 @@ int xs_hip_attention_i8(void* stream, const float* q, const void* k_codes, const
     if (split > 1 && scratch == nullptr)
         return fail(XS_HIP_EINVAL, std::string(what) + ": split " + std::to_string(split) +
                                        " needs xs_hip_attention_i8_scratch bytes of scratch");
-    if (split > kMaxSplit || tokens * kv_heads > 0x7fffffffLL)
+    if (split > kMaxSplit || tokens * kv_heads > 65535)
         return fail(XS_HIP_EUNSUPPORTED, std::string(what) + ": launch too large");
     if (!aligned16(q) || !aligned16(out) || !aligned16(k_codes) || !aligned16(v_codes) || head_dim % 16 != 0 ||
         (split > 1 && reinterpret_cast<uintptr_t>(scratch) % 16 != 0))

@@ -47,9 +47,6 @@ __device__ __forceinline__ float act_exact(float x) {
     }
 }
 
-// Every op of the unary family as cpu-ref evaluates it (ops.cpp:209-258), `pa` / `pb` the op's parameters (the scale
-// factor, the softcap, the clamp bounds): f32 arithmetic for Scale and Clamp, f64 for the transcendental ones, rounded
-// once. Clamp is std::min(std::max(v, lo), hi), which keeps a NaN v.
 // An empty register barrier: hides the value's origin from the optimizer. Used on unary results before they are
 // narrowed, where the compiler would otherwise fold the narrowing of a libm copysign into a bf16 copysign that it
 // cannot select on gfx950.
@@ -58,17 +55,22 @@ __device__ __forceinline__ float opaque(float v) {
     return v;
 }
 
+// Every op of the unary family as cpu-ref evaluates it (ops.cpp:209-258), `pa` / `pb` the op's parameters (the scale
+// factor, the softcap, the clamp bounds). Scale and Clamp are the reference's f32 arithmetic exactly (Clamp is
+// std::min(std::max(v, lo), hi), which keeps a NaN v). Tanh, Softcap and Softplus, which cpu-ref evaluates in f64 and
+// rounds once, are evaluated with the device's f32 tanhf / log1pf / expf (a few units in the last f32 place, no
+// cancellation: within the parity bar of every output dtype) -- f64 transcendentals would make these memory-bound ops
+// VALU-bound. The GELUs keep the f64 formula (their 1 + tanh cancellation needs it).
 template <int ACT>
 __device__ __forceinline__ float unary_exact(float x, float pa, float pb) {
     if constexpr (ACT == XS_UNARY_SCALE) {
         return x * pa;
     } else if constexpr (ACT == XS_UNARY_TANH) {
-        return static_cast<float>(tanh(static_cast<double>(x)));
+        return tanhf(x);
     } else if constexpr (ACT == XS_UNARY_SOFTCAP) {
-        return static_cast<float>(static_cast<double>(pa) * tanh(static_cast<double>(x) / pa));
+        return pa * tanhf(x / pa);
     } else if constexpr (ACT == XS_UNARY_SOFTPLUS) {
-        const double d = x;
-        return static_cast<float>(d > 20.0 ? d : log1p(exp(d)));
+        return x > 20.0f ? x : log1pf(expf(x));
     } else if constexpr (ACT == XS_UNARY_CLAMP) {
         const float lo = x < pa ? pa : x;
         return pb < lo ? pb : lo;

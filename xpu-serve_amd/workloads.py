@@ -89,6 +89,13 @@ ALGO_BYTES: Dict[str, int] = {
     "swiglu_bias_strided": 3 * 2048 * 9728 * 2 + 9728 * 2,
     "softmax_masked": 32 * 30000 * 4 + 32 * 32768 * 4,             # valid keys read; every key written
     "argmax": 151936 * 4 + 8,
+    # the widened ops, on the BASELINE shapes: layer_norm / l2_clip over config 0's x (read x, w, b; write y),
+    # reduce_sum of config 0's x over either axis, softcap of config 1's gate (bf16 in and out)
+    "layer_norm": 2 * 512 * 2560 * 4 + 2 * 2560 * 4,
+    "l2_clip": 2 * 512 * 2560 * 4,
+    "reduce_sum_rows": 512 * 2560 * 4 + 512 * 4,
+    "reduce_sum_cols": 512 * 2560 * 4 + 2560 * 4,
+    "unary_softcap": 2 * 2048 * 9728 * 2,
     # one decode step over config 4's int8 cache: K and V codes [65536, 8, 128] and scales [65536, 8]; q and out
     # [1, 32, 128] f32
     "attention_i8_decode": 2 * (65536 * 8 * 128 + 65536 * 8 * 4) + 2 * 32 * 128 * 4,
