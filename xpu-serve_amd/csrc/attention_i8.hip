@@ -70,22 +70,32 @@ __device__ __forceinline__ float byte_f32(uint32_t w, int k) {
     return static_cast<float>(static_cast<int8_t>((w >> (8 * k)) & 0xffu));
 }
 
-// G query heads per KV head, D head_dim (64, 128 or 256), DPL value dims a lane (8 or 16).
-template <int G, int D, int DPL>
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// q of one head as a 23-bit integer per dim, Q = round(q / qs) with qs = max |q| / 2^22, written as three balanced
+// base-256 digits (hi * 65536 + mid * 256 + lo, each in [-128, 127]) so that int8 matrix cores can take it. The
+// digits are exact: qs * Q is q within 2^-23 of max |q|.
+__device__ __forceinline__ void q_digits(float q, float inv_qs, int& hi, int& mid, int& lo) {
+    const int Q = static_cast<int>(rintf(q * inv_qs));
+    lo = static_cast<int8_t>(Q & 0xff);
+    const int q1 = (Q - lo) >> 8;
+    mid = static_cast<int8_t>(q1 & 0xff);
+    hi = (q1 - mid) >> 8;
+}
+
+// G query heads per KV head, D head_dim (64, 128 or 256). Value dims a lane in the weighted sum: DPL = 8.
+template <int G, int D>
 __global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a, const float* __restrict__ qg) {
-    using VCodes = typename std::conditional<DPL == 16, u32x4, uint64_t>::type;
-    constexpr int ROW = D + 16;            // LDS bytes a staged key row: 16 bytes of padding spread the lanes' rows
-                                           // over the banks when each lane reads its own row
-    constexpr int LPR = D / DPL;           // lanes a row with DPL-byte loads
-    constexpr int RPI = 64 / LPR;          // rows one load instruction covers
-    constexpr int VI = kTile / RPI;        // load instructions a tile
-    constexpr int TILE = kTile * ROW;
-    // Each wave's key tile; after the last tile the same LDS holds the waves' results for the merge.
-    constexpr int SMEM = kWaves * TILE > kWaves * G * (D + 2) * 4 ? kWaves * TILE : kWaves * G * (D + 2) * 4;
-    __shared__ __align__(16) uint8_t smem[SMEM];
-    __shared__ __align__(16) float ptile[kWaves][kTile][G];
-    __shared__ __align__(16) float qs[G][D];
-    auto mbuf = reinterpret_cast<float(*)[G][D + 2]>(smem);
+    constexpr int DPL = 8;
+    constexpr int LPR = D / DPL;           // lanes a value row with 8-byte loads
+    constexpr int RPI = 64 / LPR;          // value rows one load instruction covers
+    constexpr int VI = kTile / RPI;        // value load instructions a tile
+    constexpr int KC = D / 64;             // 64-dim chunks of a key row: the K of one matrix-core step
+    constexpr int KB = kTile / 16;         // 16-key blocks of a tile: the M of one matrix-core step
+    static_assert(G <= 16, "the query heads of a KV head fill at most the 16 columns of a matrix-core step");
+    __shared__ __align__(16) float ptile[kWaves][kTile][G];   // p * v_scale of each key of each wave's tile
+    __shared__ __align__(16) float kscale[kWaves][kTile];     // key scales of each wave's tile
+    __shared__ float mbuf[kWaves][G][D + 2];
 
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
@@ -105,139 +115,180 @@ __global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a, con
     int64_t k1 = k0 + per - 1;
     if (k1 > last) k1 = last;
 
-    // q of the G heads, the same for every lane: in LDS, read by broadcast.
+    // Matrix-core operands. Scores S [16 keys, 16 heads] = K [16 keys, 64 dims] x Q^T [64 dims, 16 heads] per 64-dim
+    // chunk: lane l holds 16 consecutive codes of key l % 16 (dims 16 (l / 16) ..) as the A operand and the digits of
+    // head l % 16 over the same dims as the B operand; the result gives lane l the scores of keys 4 (l / 16) + r,
+    // r < 4, for head h = l % 16. Heads past G are zero columns.
+    const int h = lane & 15;
+    const int kq = lane >> 4;  // which 16 dims of a 64-dim chunk, and which 4 keys of a 16-key block
+    i32x4 qd[3][KC];           // hi, mid, lo digits
+    float qs_h;                // q scale of head h
     {
-        const float* q = qg + (t * a.q_heads + kvh * G) * D;
-        for (int i = threadIdx.x * 4; i < G * D; i += 64 * kWaves * 4)
-            *reinterpret_cast<u32x4*>(&qs[0][0] + i) = ld128(q + i);
+        float qv[KC][16];
+        float mx = 0.0f;
+        const float* q = qg + (t * a.q_heads + kvh * G + (h < G ? h : 0)) * D;
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) {
+                const u32x4 raw = ld128(q + c * 64 + kq * 16 + i);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    qv[c][i + e] = h < G ? __uint_as_float(raw[e]) : 0.0f;
+                    mx = fmaxf(mx, fabsf(qv[c][i + e]));
+                }
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));  // max |q| of head h over all its dims
+        qs_h = mx / 4194304.0f;
+        const float inv = mx > 0.0f ? 4194304.0f / mx : 0.0f;
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                uint32_t dh = 0, dm = 0, dl = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    int hi, mid, lo;
+                    q_digits(qv[c][4 * w + e], inv, hi, mid, lo);
+                    dh |= static_cast<uint32_t>(hi & 0xff) << (8 * e);
+                    dm |= static_cast<uint32_t>(mid & 0xff) << (8 * e);
+                    dl |= static_cast<uint32_t>(lo & 0xff) << (8 * e);
+                }
+                qd[0][c][w] = static_cast<int>(dh);
+                qd[1][c][w] = static_cast<int>(dm);
+                qd[2][c][w] = static_cast<int>(dl);
+            }
+        }
     }
-    __syncthreads();
+    const float score_scale = qs_h * a.scale;
 
     // Weighted sum layout: lane l accumulates dims (l % LPR) * DPL .. + DPL - 1 over the tile rows l / LPR, + RPI, ...
     const int cl = (lane % LPR) * DPL;
     const int rl0 = lane / LPR;
     float acc[G][DPL];
-    float m[G], l[G];  // m: the wave's running max per head; l: this lane's share of the sum of exponentials
+    float m[G];      // the wave's running max per head (the same in every lane)
+    float lsum = 0.0f;  // this lane's share of head h's sum of exponentials
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         m[g] = -INFINITY;
-        l[g] = 0.0f;
 #pragma unroll
         for (int i = 0; i < DPL; ++i) acc[g][i] = 0.0f;
     }
 
     const int64_t span = k1 >= k0 ? k1 - k0 + 1 : 0;
     const int64_t tiles = (span + kTile - 1) / kTile;
-    uint8_t* kt = smem + wave * TILE;
     // The waves run independently: wave w takes tiles w, w + kWaves, ... and touches only its own LDS, whose writes
-    // and reads are ordered within the wave (wave_sync). Each tile's key and value codes are loaded into registers a
-    // tile ahead, so HBM reads stay in flight while the previous tile is computed.
+    // and reads are ordered within the wave (wave_sync).
     auto wave_sync = [] {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
-    auto load_tile = [&](int64_t tile, VCodes* kw, VCodes* vw) {
-        const int64_t j0 = k0 + tile * kTile;
+    for (int64_t tile = wave; tile < tiles; tile += kWaves) {
+        const int64_t j0 = k0 + tile * kTile;  // keys j0 .. j0 + 63 (those past k1 clamped to it, weights 0)
+        // Loads: key codes in the matrix-core A layout, value rows for the weighted sum, and the tile's scales.
+        i32x4 kw[KB][KC];
+#pragma unroll
+        for (int b = 0; b < KB; ++b) {
+            int64_t j = j0 + b * 16 + h;
+            j = j <= k1 ? j : k1;
+            const int8_t* kp = a.kc + (j * a.kv_heads + kvh) * D + kq * 16;
+#pragma unroll
+            for (int c = 0; c < KC; ++c) kw[b][c] = __builtin_bit_cast(i32x4, ld128_nt(kp + c * 64));
+        }
+        uint64_t vw[VI];
 #pragma unroll
         for (int i = 0; i < VI; ++i) {
             int64_t j = j0 + i * RPI + rl0;
             j = j <= k1 ? j : k1;
-            const int64_t off = (j * a.kv_heads + kvh) * D + cl;
-            if constexpr (DPL == 16) {
-                kw[i] = ld128_nt(a.kc + off);
-                vw[i] = ld128_nt(a.vc + off);
-            } else {
-                kw[i] = __builtin_nontemporal_load(reinterpret_cast<const uint64_t*>(a.kc + off));
-                vw[i] = __builtin_nontemporal_load(reinterpret_cast<const uint64_t*>(a.vc + off));
-            }
+            vw[i] = __builtin_nontemporal_load(reinterpret_cast<const uint64_t*>(a.vc + (j * a.kv_heads + kvh) * D + cl));
         }
-    };
-    VCodes kw[VI], vw[VI];
-    if (wave < tiles) load_tile(wave, kw, vw);
-    for (int64_t tile = wave; tile < tiles; tile += kWaves) {
-        const int64_t j0 = k0 + tile * kTile;  // keys j0 .. j0 + 63 (those past k1 clamped to it, weights 0)
-#pragma unroll
-        for (int i = 0; i < VI; ++i) *reinterpret_cast<VCodes*>(kt + (i * RPI + rl0) * ROW + cl) = kw[i];
-        const int64_t jl = j0 + lane;  // the lane's key in the score phase
-        const bool valid = jl <= k1;
-        const int64_t rk = (valid ? jl : k1) * a.kv_heads + kvh;
-        const float ksc = a.ks[rk];
+        const int64_t jl = j0 + lane;
+        const int64_t rk = (jl <= k1 ? jl : k1) * a.kv_heads + kvh;
         const float vsc = a.vs[rk];
-        VCodes vcur[VI];
-#pragma unroll
-        for (int i = 0; i < VI; ++i) vcur[i] = vw[i];
-        if (tile + kWaves < tiles) load_tile(tile + kWaves, kw, vw);
+        kscale[wave][lane] = a.ks[rk];
         wave_sync();
 
-        // Scores, a lane per key: its whole row of codes against q.
-        float sc[G];
+        // Scores on the matrix cores: three digit products per 16-key block and 64-dim chunk, combined in f32.
+        float sc[KB][4];
+        float mt = -INFINITY;
 #pragma unroll
-        for (int g = 0; g < G; ++g) sc[g] = 0.0f;
-#pragma unroll 2
-        for (int c = 0; c < D; c += 16) {
-            const u32x4 w = *reinterpret_cast<const u32x4*>(kt + lane * ROW + c);
-            float code[16];
+        for (int b = 0; b < KB; ++b) {
+            i32x4 r0 = {0, 0, 0, 0}, r1 = {0, 0, 0, 0}, r2 = {0, 0, 0, 0};
 #pragma unroll
-            for (int k = 0; k < 16; ++k) code[k] = byte_f32(w[k >> 2], k & 3);
+            for (int c = 0; c < KC; ++c) {
+                r0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kw[b][c], qd[0][c], r0, 0, 0, 0);
+                r1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kw[b][c], qd[1][c], r1, 0, 0, 0);
+                r2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kw[b][c], qd[2][c], r2, 0, 0, 0);
+            }
+            const u32x4 ks4 = *reinterpret_cast<const u32x4*>(&kscale[wave][b * 16 + kq * 4]);
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
+            for (int r = 0; r < 4; ++r) {
+                const float dot = static_cast<float>(r0[r]) * 65536.0f + static_cast<float>(r1[r]) * 256.0f +
+                                  static_cast<float>(r2[r]);
+                float x = dot * score_scale * __uint_as_float(ks4[r]);
+                if (a.softcap > 0.0f) x = a.softcap * tanhf(x / a.softcap);
+                const bool valid = j0 + b * 16 + kq * 4 + r <= k1;
+                sc[b][r] = valid ? x : -INFINITY;
+                mt = fmaxf(mt, sc[b][r]);
+            }
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));  // the tile's max of head h
+        // Running max: head g's values live in lanes g, g + 16, ...: read them from lane g.
+        float mh = -INFINITY;  // running max of head h after this tile
 #pragma unroll
-                for (int k = 0; k < 16; k += 4) {
-                    const u32x4 qv = *reinterpret_cast<const u32x4*>(&qs[g][c + k]);
+        for (int g = 0; g < G; ++g) {
+            const float mtg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mt), g));
+            const float mn = fmaxf(m[g], mtg);
+            if (mn > m[g]) {  // uniform across the wave
+                const float c = m[g] == -INFINITY ? 0.0f : __expf(m[g] - mn);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) sc[g] = fmaf(__uint_as_float(qv[e]), code[k + e], sc[g]);
+                for (int i = 0; i < DPL; ++i) acc[g][i] *= c;
+                if (h == g) lsum *= c;
+                m[g] = mn;
+            }
+            if (h == g) mh = m[g];
+        }
+        // p = exp(s - max) * v_scale per (key, head) to LDS; this lane's keys: 16 b + 4 kq + r.
+        wave_sync();  // kscale reads are done before the next tile rewrites it
+        if (h < G) {
+#pragma unroll
+            for (int b = 0; b < KB; ++b) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float p = __expf(sc[b][r] - mh);  // 0 for keys past the split (-inf)
+                    lsum += p;
+                    ptile[wave][b * 16 + kq * 4 + r][h] = p;
                 }
             }
         }
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float x = sc[g] * ksc * a.scale;
-            if (a.softcap > 0.0f) x = a.softcap * tanhf(x / a.softcap);
-            sc[g] = valid ? x : -INFINITY;
-        }
-        // The tile's max per head moves the running max; p = exp(s - max) per key, times the value scale, to LDS.
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float mt = group_reduce<64, OpMax>(sc[g]);
-            const float mn = fmaxf(m[g], mt);
-            if (mn > m[g]) {  // uniform across the wave
-                const float c = m[g] == -INFINITY ? 0.0f : __expf(m[g] - mn);
-                l[g] *= c;
-#pragma unroll
-                for (int i = 0; i < DPL; ++i) acc[g][i] *= c;
-                m[g] = mn;
-            }
-            const float p = valid ? __expf(sc[g] - m[g]) : 0.0f;
-            l[g] += p;
-            ptile[wave][lane][g] = p * vsc;
-        }
         wave_sync();
 
-        // Weighted sum: the value rows in registers, each with its key's p * v_scale from LDS.
+        // Weighted sum: the value rows in registers, each with its key's p (LDS) times its value scale.
 #pragma unroll
         for (int i = 0; i < VI; ++i) {
             const int r = i * RPI + rl0;
+            const float vs_r = __builtin_bit_cast(float, __shfl(__builtin_bit_cast(int, vsc), r, 64));
             float pv[G];
 #pragma unroll
-            for (int g = 0; g < G; ++g) pv[g] = ptile[wave][r][g];
+            for (int g = 0; g < G; ++g) pv[g] = ptile[wave][r][g] * vs_r;
 #pragma unroll
             for (int k = 0; k < DPL; ++k) {
-                uint32_t word;
-                if constexpr (DPL == 16) word = vcur[i][k >> 2];
-                else word = static_cast<uint32_t>(vcur[i] >> (32 * (k >> 2)));
-                const float code = byte_f32(word, k & 3);
+                const float code = byte_f32(static_cast<uint32_t>(vw[i] >> (32 * (k >> 2))), k & 3);
 #pragma unroll
                 for (int g = 0; g < G; ++g) acc[g][k] = fmaf(pv[g], code, acc[g][k]);
             }
             // One row at a time: keeps the compiler from widening every row's codes at once.
             __builtin_amdgcn_sched_barrier(0);
         }
-        wave_sync();  // the key tile and the weights are rewritten next tile
+        wave_sync();  // the weights are rewritten next tile
     }
 
-    // The wave's lanes that share dims hold sums over different rows with the same running max: add them. Then the
-    // four waves merge through LDS (the tiles' space: every wave has left the loop).
+    // The wave's lanes that share dims hold sums over different rows with the same running max: add them. Each
+    // head's sum of exponentials is spread over the lanes of that head. Then the four waves merge through LDS.
 #pragma unroll
     for (int off = LPR; off < 64; off <<= 1) {
 #pragma unroll
@@ -246,9 +297,11 @@ __global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a, con
             for (int i = 0; i < DPL; ++i) acc[g][i] += __shfl_xor(acc[g][i], off, 64);
         }
     }
+    lsum += __shfl_xor(lsum, 16, 64);
+    lsum += __shfl_xor(lsum, 32, 64);  // head h's sum in every lane of head h
+    float l[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) l[g] = group_reduce<64, OpSum>(l[g]);
-    __syncthreads();
+    for (int g = 0; g < G; ++g) l[g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lsum), g));
     if (lane < LPR) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -274,9 +327,9 @@ __global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a, con
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        const int64_t h = kvh * G + g;
+        const int64_t hh = kvh * G + g;
         if (a.part == nullptr) {
-            float* o = a.out + (t * a.q_heads + h) * D + cl;
+            float* o = a.out + (t * a.q_heads + hh) * D + cl;
             const float inv = 1.0f / l[g];
 #pragma unroll
             for (int i = 0; i < DPL; i += 4) {
@@ -286,7 +339,7 @@ __global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a, con
                 st128(o + i, w);
             }
         } else {
-            float* pr = a.part + ((t * a.q_heads + h) * a.split + s) * (D + 2);
+            float* pr = a.part + ((t * a.q_heads + hh) * a.split + s) * (D + 2);
 #pragma unroll
             for (int i = 0; i < DPL; ++i) pr[cl + i] = acc[g][i];
             if (lane == 0) {
@@ -359,7 +412,7 @@ __global__ __launch_bounds__(256) void attention_combine_rows(const float* part,
 template <int G, int D>
 void launch_rows(hipStream_t s, const AttnArgs& a) {
     const dim3 grid(static_cast<unsigned>(a.split), static_cast<unsigned>(a.tokens * a.kv_heads));
-    attention_i8_rows<G, D, 8><<<grid, 64 * kWaves, 0, s>>>(a, a.q);
+    attention_i8_rows<G, D><<<grid, 64 * kWaves, 0, s>>>(a, a.q);
 }
 
 template <int G>
