@@ -52,7 +52,7 @@ __device__ __forceinline__ void key_range(const AttnArgs& a, int64_t t, int64_t&
 }
 
 constexpr int kWaves = 4;    // waves a workgroup; each takes every fourth tile of 64 keys, and they merge in LDS
-constexpr int kTile = 64;    // keys a wave stages at once: one a lane
+constexpr int kTile = 64;    // keys a wave works on at once (at most 64: one a lane for the scales)
 
 // Merges (m, l, acc) of another key set into this one: the online-softmax combine.
 template <int N>
@@ -83,18 +83,44 @@ __device__ __forceinline__ void q_digits(float q, float inv_qs, int& hi, int& mi
     hi = (q1 - mid) >> 8;
 }
 
-// G query heads per KV head, D head_dim (64, 128 or 256). Value dims a lane in the weighted sum: DPL = 8.
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+// Reads 8 bytes a lane from LDS with the transpose of ds_read_b64_tr_b8: within each group of 16 lanes, with C_j the
+// 8 bytes at lane j's address, lane i receives byte i % 8 of C_{2k + i / 8} as its byte k (k < 8). Lane j pointing at
+// row base + j / 2, column col + 8 (j % 2) of a row-major byte tile thus gives lane i column col + i of rows
+// base .. base + 7: a 16-column by 8-row block, transposed.
+__device__ __forceinline__ i32x2 lds_read_tr8(const uint8_t* p) {
+    // p points into LDS: the C cast converts the generic address to the LDS address space the builtin takes.
+    return __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) i32x2*)(p));
+}
+
+// G query heads per KV head, D head_dim (64, 128 or 256).
+//
+// Both products run on the int8 matrix cores (v_mfma_i32_16x16x64_i8; 16 x 16 results, K = 64):
+//  - scores S [16 keys, 16 heads] = key codes [16 keys, 64 dims] x digits of q [64 dims, 16 heads], a 64-dim chunk at
+//    a time. Lane l holds 16 codes of key l % 16 (dims 16 (l / 16) ..) -- a plain 16-byte load -- and the digits of
+//    head l % 16 over the same dims; it receives the scores of keys 4 (l / 16) + r (r < 4) for head l % 16.
+//  - the weighted sum O^T [16 dims, 16 heads] = value codes^T [16 dims, 64 keys] x digits of the weights
+//    [64 keys, 16 heads]. The value tile is staged in LDS row-major and read transposed (lds_read_tr8), so lane l
+//    holds 16 keys' codes of dim l % 16; the weights w = p * v_scale, as integers W = round(w / ws) with
+//    ws = max v_scale / 2^22 over the wave's keys (p <= 1), in three digits. Lane l receives dims 4 (l / 16) + r of
+//    head l % 16: exact int32 sums of the tile, added to the f32 accumulator times ws.
 template <int G, int D>
 __global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a, const float* __restrict__ qg) {
-    constexpr int DPL = 8;
-    constexpr int LPR = D / DPL;           // lanes a value row with 8-byte loads
-    constexpr int RPI = 64 / LPR;          // value rows one load instruction covers
-    constexpr int VI = kTile / RPI;        // value load instructions a tile
-    constexpr int KC = D / 64;             // 64-dim chunks of a key row: the K of one matrix-core step
-    constexpr int KB = kTile / 16;         // 16-key blocks of a tile: the M of one matrix-core step
+    constexpr int KC = D / 64;             // 64-dim chunks of a key row: the K of one score step
+    constexpr int KB = kTile / 16;         // 16-key blocks of a tile: the M of one score step
+    constexpr int DB = D / 16;             // 16-dim blocks of a value row: the M of one weighted-sum step
+    constexpr int VROW = D + 8;            // LDS bytes a staged value row (8 bytes of padding: distinct banks for the
+                                           // eight rows one transposed read covers)
+    constexpr int VLPR = D / 8;            // lanes a value row with 8-byte loads
+    constexpr int VRPI = 64 / VLPR;        // value rows one load instruction covers
+    constexpr int VI = kTile / VRPI;       // value load instructions a tile
     static_assert(G <= 16, "the query heads of a KV head fill at most the 16 columns of a matrix-core step");
-    __shared__ __align__(16) float ptile[kWaves][kTile][G];   // p * v_scale of each key of each wave's tile
-    __shared__ __align__(16) float kscale[kWaves][kTile];     // key scales of each wave's tile
+    static_assert(kTile == 64, "a weighted-sum step takes the 64 keys of a tile");
+    __shared__ __align__(16) float ptile[kWaves][G][kTile];     // p of each head and key of each wave's tile
+    __shared__ __align__(16) float vscale[kWaves][kTile];       // value scales of each wave's tile
+    __shared__ __align__(16) float kscale[kWaves][kTile];       // key scales of each wave's tile
+    __shared__ __align__(16) uint8_t vtile[kWaves][kTile * VROW];
     __shared__ float mbuf[kWaves][G][D + 2];
 
     const int wave = threadIdx.x >> 6;
@@ -114,15 +140,15 @@ __global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a, con
     const int64_t k0 = first + s * per;
     int64_t k1 = k0 + per - 1;
     if (k1 > last) k1 = last;
+    const int64_t span = k1 >= k0 ? k1 - k0 + 1 : 0;
+    const int64_t tiles = (span + kTile - 1) / kTile;
 
-    // Matrix-core operands. Scores S [16 keys, 16 heads] = K [16 keys, 64 dims] x Q^T [64 dims, 16 heads] per 64-dim
-    // chunk: lane l holds 16 consecutive codes of key l % 16 (dims 16 (l / 16) ..) as the A operand and the digits of
-    // head l % 16 over the same dims as the B operand; the result gives lane l the scores of keys 4 (l / 16) + r,
-    // r < 4, for head h = l % 16. Heads past G are zero columns.
-    const int h = lane & 15;
-    const int kq = lane >> 4;  // which 16 dims of a 64-dim chunk, and which 4 keys of a 16-key block
-    i32x4 qd[3][KC];           // hi, mid, lo digits
-    float qs_h;                // q scale of head h
+    const int h = lane & 15;   // the head (matrix-core column) of this lane
+    const int kq = lane >> 4;  // its 16-dim / 16-key / 4-row group
+
+    // q as three digits per dim (the score step's B operand), and its scale.
+    i32x4 qd[3][KC];
+    float qs_h;
     {
         float qv[KC][16];
         float mx = 0.0f;
@@ -164,21 +190,31 @@ __global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a, con
     }
     const float score_scale = qs_h * a.scale;
 
-    // Weighted sum layout: lane l accumulates dims (l % LPR) * DPL .. + DPL - 1 over the tile rows l / LPR, + RPI, ...
-    const int cl = (lane % LPR) * DPL;
-    const int rl0 = lane / LPR;
-    float acc[G][DPL];
-    float m[G];      // the wave's running max per head (the same in every lane)
-    float lsum = 0.0f;  // this lane's share of head h's sum of exponentials
+    // The weights' integer scale: the largest value scale among this wave's keys (p <= 1 bounds the weights by it).
+    float ws;
+    {
+        float mv = 0.0f;
+        for (int64_t tile = wave; tile < tiles; tile += kWaves) {
+            const int64_t j = k0 + tile * kTile + lane;
+            if (j <= k1) mv = fmaxf(mv, a.vs[j * a.kv_heads + kvh]);
+        }
+        mv = group_reduce<64, OpMax>(mv);
+        ws = mv / 4194304.0f;
+    }
+    const float inv_ws = ws > 0.0f ? 1.0f / ws : 0.0f;
+
+    float m[G];                 // the wave's running max per head (the same in every lane)
+    float lsum = 0.0f;          // this lane's share of head h's sum of exponentials
+    float mh = -INFINITY;       // the running max of head h
+    float facc[DB][4];          // head h, dims 16 db + 4 kq + r: the weighted sums
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        m[g] = -INFINITY;
+    for (int g = 0; g < G; ++g) m[g] = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) acc[g][i] = 0.0f;
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) facc[db][r] = 0.0f;
     }
 
-    const int64_t span = k1 >= k0 ? k1 - k0 + 1 : 0;
-    const int64_t tiles = (span + kTile - 1) / kTile;
     // The waves run independently: wave w takes tiles w, w + kWaves, ... and touches only its own LDS, whose writes
     // and reads are ordered within the wave (wave_sync).
     auto wave_sync = [] {
@@ -186,9 +222,10 @@ __global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a, con
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
+    uint8_t* vt = vtile[wave];
     for (int64_t tile = wave; tile < tiles; tile += kWaves) {
         const int64_t j0 = k0 + tile * kTile;  // keys j0 .. j0 + 63 (those past k1 clamped to it, weights 0)
-        // Loads: key codes in the matrix-core A layout, value rows for the weighted sum, and the tile's scales.
+        // Loads: key codes in the score step's A layout, value rows (to LDS), the tile's scales.
         i32x4 kw[KB][KC];
 #pragma unroll
         for (int b = 0; b < KB; ++b) {
@@ -201,17 +238,23 @@ __global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a, con
         uint64_t vw[VI];
 #pragma unroll
         for (int i = 0; i < VI; ++i) {
-            int64_t j = j0 + i * RPI + rl0;
+            int64_t j = j0 + i * VRPI + lane / VLPR;
             j = j <= k1 ? j : k1;
-            vw[i] = __builtin_nontemporal_load(reinterpret_cast<const uint64_t*>(a.vc + (j * a.kv_heads + kvh) * D + cl));
+            vw[i] = __builtin_nontemporal_load(
+                reinterpret_cast<const uint64_t*>(a.vc + (j * a.kv_heads + kvh) * D + (lane % VLPR) * 8));
         }
-        const int64_t jl = j0 + lane;
-        const int64_t rk = (jl <= k1 ? jl : k1) * a.kv_heads + kvh;
-        const float vsc = a.vs[rk];
-        kscale[wave][lane] = a.ks[rk];
+        {
+            const int64_t jl = j0 + lane;
+            const int64_t rk = (jl <= k1 ? jl : k1) * a.kv_heads + kvh;
+            kscale[wave][lane] = a.ks[rk];
+            vscale[wave][lane] = a.vs[rk];
+        }
+#pragma unroll
+        for (int i = 0; i < VI; ++i)
+            *reinterpret_cast<uint64_t*>(vt + (i * VRPI + lane / VLPR) * VROW + (lane % VLPR) * 8) = vw[i];
         wave_sync();
 
-        // Scores on the matrix cores: three digit products per 16-key block and 64-dim chunk, combined in f32.
+        // Scores: three digit products per 16-key block and 64-dim chunk, combined in f32.
         float sc[KB][4];
         float mt = -INFINITY;
 #pragma unroll
@@ -237,114 +280,136 @@ __global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a, con
         }
         mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
         mt = fmaxf(mt, __shfl_xor(mt, 32, 64));  // the tile's max of head h
-        // Running max: head g's values live in lanes g, g + 16, ...: read them from lane g.
-        float mh = -INFINITY;  // running max of head h after this tile
+        // A larger max for some head: flush the digit sums, rescaling each lane's head by exp(old - new).
+        const float mn = fmaxf(mh, mt);
+        bool moved = false;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const float mtg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mt), g));
-            const float mn = fmaxf(m[g], mtg);
-            if (mn > m[g]) {  // uniform across the wave
-                const float c = m[g] == -INFINITY ? 0.0f : __expf(m[g] - mn);
-#pragma unroll
-                for (int i = 0; i < DPL; ++i) acc[g][i] *= c;
-                if (h == g) lsum *= c;
-                m[g] = mn;
-            }
-            if (h == g) mh = m[g];
+            moved |= mtg > m[g];
+            m[g] = fmaxf(m[g], mtg);
         }
-        // p = exp(s - max) * v_scale per (key, head) to LDS; this lane's keys: 16 b + 4 kq + r.
-        wave_sync();  // kscale reads are done before the next tile rewrites it
+        if (moved) {  // uniform across the wave
+            const float c = mh == -INFINITY ? 0.0f : __expf(mh - mn);
+            lsum *= c;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) facc[db][r] *= c;
+            }
+        }
+        mh = mn;
+        // p = exp(s - max) per (head, key) to LDS; this lane's keys: 16 b + 4 kq + r of head h.
         if (h < G) {
 #pragma unroll
             for (int b = 0; b < KB; ++b) {
+                float p4[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float p = __expf(sc[b][r] - mh);  // 0 for keys past the split (-inf)
-                    lsum += p;
-                    ptile[wave][b * 16 + kq * 4 + r][h] = p;
+                    p4[r] = __expf(sc[b][r] - mh);  // 0 for keys past the split (-inf)
+                    lsum += p4[r];
                 }
+                *reinterpret_cast<u32x4*>(&ptile[wave][h][b * 16 + kq * 4]) =
+                    u32x4{__float_as_uint(p4[0]), __float_as_uint(p4[1]), __float_as_uint(p4[2]),
+                          __float_as_uint(p4[3])};
             }
         }
         wave_sync();
 
-        // Weighted sum: the value rows in registers, each with its key's p (LDS) times its value scale.
+        // Weights of head h over keys 16 kq .. + 15, as three digits: the weighted-sum step's B operand.
+        i32x4 wd[3];
+        {
+            float w[16];
 #pragma unroll
-        for (int i = 0; i < VI; ++i) {
-            const int r = i * RPI + rl0;
-            const float vs_r = __builtin_bit_cast(float, __shfl(__builtin_bit_cast(int, vsc), r, 64));
-            float pv[G];
+            for (int i = 0; i < 16; i += 4) {
+                const u32x4 p4 = h < G ? *reinterpret_cast<const u32x4*>(&ptile[wave][h][kq * 16 + i]) : u32x4{0, 0, 0, 0};
+                const u32x4 v4 = *reinterpret_cast<const u32x4*>(&vscale[wave][kq * 16 + i]);
 #pragma unroll
-            for (int g = 0; g < G; ++g) pv[g] = ptile[wave][r][g] * vs_r;
-#pragma unroll
-            for (int k = 0; k < DPL; ++k) {
-                const float code = byte_f32(static_cast<uint32_t>(vw[i] >> (32 * (k >> 2))), k & 3);
-#pragma unroll
-                for (int g = 0; g < G; ++g) acc[g][k] = fmaf(pv[g], code, acc[g][k]);
+                for (int e = 0; e < 4; ++e) w[i + e] = __uint_as_float(p4[e]) * __uint_as_float(v4[e]);
             }
-            // One row at a time: keeps the compiler from widening every row's codes at once.
-            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                uint32_t dh = 0, dm = 0, dl = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    int hi, mid, lo;
+                    q_digits(w[4 * q4 + e], inv_ws, hi, mid, lo);
+                    dh |= static_cast<uint32_t>(hi & 0xff) << (8 * e);
+                    dm |= static_cast<uint32_t>(mid & 0xff) << (8 * e);
+                    dl |= static_cast<uint32_t>(lo & 0xff) << (8 * e);
+                }
+                wd[0][q4] = static_cast<int>(dh);
+                wd[1][q4] = static_cast<int>(dm);
+                wd[2][q4] = static_cast<int>(dl);
+            }
         }
-        wave_sync();  // the weights are rewritten next tile
+        // Weighted sum: per 16-dim block, the transposed value codes of keys 16 kq .. + 15 against the digits.
+        const int tr_row = kq * 16 + (h >> 1);
+        const int tr_col = 8 * (h & 1);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            const i32x2 lo8 = lds_read_tr8(vt + tr_row * VROW + db * 16 + tr_col);
+            const i32x2 hi8 = lds_read_tr8(vt + (tr_row + 8) * VROW + db * 16 + tr_col);
+            const i32x4 va = {lo8[0], lo8[1], hi8[0], hi8[1]};
+            const i32x4 zero = {0, 0, 0, 0};
+            const i32x4 r0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(va, wd[0], zero, 0, 0, 0);
+            const i32x4 r1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(va, wd[1], zero, 0, 0, 0);
+            const i32x4 r2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(va, wd[2], zero, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float v = static_cast<float>(r0[r]) * 65536.0f + static_cast<float>(r1[r]) * 256.0f +
+                                static_cast<float>(r2[r]);
+                facc[db][r] = fmaf(v, ws, facc[db][r]);
+            }
+        }
+        wave_sync();  // the tiles are rewritten next time
     }
 
-    // The wave's lanes that share dims hold sums over different rows with the same running max: add them. Each
-    // head's sum of exponentials is spread over the lanes of that head. Then the four waves merge through LDS.
-#pragma unroll
-    for (int off = LPR; off < 64; off <<= 1) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-#pragma unroll
-            for (int i = 0; i < DPL; ++i) acc[g][i] += __shfl_xor(acc[g][i], off, 64);
-        }
-    }
+    // Each head's sum of exponentials is spread over the lanes of that head. Then the four waves merge through LDS;
+    // lane l holds dims 16 db + 4 kq + r of head h.
     lsum += __shfl_xor(lsum, 16, 64);
-    lsum += __shfl_xor(lsum, 32, 64);  // head h's sum in every lane of head h
-    float l[G];
+    lsum += __shfl_xor(lsum, 32, 64);
+    if (h < G) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) l[g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lsum), g));
-    if (lane < LPR) {
+        for (int db = 0; db < DB; ++db) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-#pragma unroll
-            for (int i = 0; i < DPL; ++i) mbuf[wave][g][cl + i] = acc[g][i];
-            if (lane == 0) {
-                mbuf[wave][g][D] = m[g];
-                mbuf[wave][g][D + 1] = l[g];
-            }
+            for (int r = 0; r < 4; ++r) mbuf[wave][h][db * 16 + kq * 4 + r] = facc[db][r];
+        }
+        if (kq == 0) {
+            mbuf[wave][h][D] = mh;
+            mbuf[wave][h][D + 1] = lsum;
         }
     }
     __syncthreads();
-    if (wave != 0 || lane >= LPR) return;
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float ao[DPL];
-#pragma unroll
-            for (int i = 0; i < DPL; ++i) ao[i] = mbuf[w][g][cl + i];
-            merge<DPL>(m[g], l[g], acc[g], mbuf[w][g][D], mbuf[w][g][D + 1], ao);
-        }
-    }
+    // Wave 0 merges: lane l takes dims l * D / 64 .. of every head.
+    if (wave != 0) return;
+    constexpr int DL = D / 64;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
+        float mg = mbuf[0][g][D], lg = mbuf[0][g][D + 1];
+        float ag[DL];
+#pragma unroll
+        for (int i = 0; i < DL; ++i) ag[i] = mbuf[0][g][lane * DL + i];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) {
+            float ao[DL];
+#pragma unroll
+            for (int i = 0; i < DL; ++i) ao[i] = mbuf[w][g][lane * DL + i];
+            merge<DL>(mg, lg, ag, mbuf[w][g][D], mbuf[w][g][D + 1], ao);
+        }
         const int64_t hh = kvh * G + g;
         if (a.part == nullptr) {
-            float* o = a.out + (t * a.q_heads + hh) * D + cl;
-            const float inv = 1.0f / l[g];
+            float* o = a.out + (t * a.q_heads + hh) * D + lane * DL;
+            const float inv = 1.0f / lg;
 #pragma unroll
-            for (int i = 0; i < DPL; i += 4) {
-                u32x4 w;
-#pragma unroll
-                for (int k = 0; k < 4; ++k) w[k] = __float_as_uint(acc[g][i + k] * inv);
-                st128(o + i, w);
-            }
+            for (int i = 0; i < DL; ++i) o[i] = ag[i] * inv;
         } else {
             float* pr = a.part + ((t * a.q_heads + hh) * a.split + s) * (D + 2);
 #pragma unroll
-            for (int i = 0; i < DPL; ++i) pr[cl + i] = acc[g][i];
+            for (int i = 0; i < DL; ++i) pr[lane * DL + i] = ag[i];
             if (lane == 0) {
-                pr[D] = m[g];
-                pr[D + 1] = l[g];
+                pr[D] = mg;
+                pr[D + 1] = lg;
             }
         }
     }
