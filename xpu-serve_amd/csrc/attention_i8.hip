@@ -17,7 +17,7 @@
 // accumulator at most once per tile), and each key's p * v_scale goes to LDS; then each lane accumulates the value
 // rows it loaded, 8 dims each, weighted in f32. The lanes sharing dims add up (they share the running max), and the
 // four waves' (max, sum, accumulator) merge in LDS at the end. With one split the workgroup writes the output; with
-// several it writes [head_dim partial sums, max, sum] rows that a second launch merges (flash decoding).
+// several it writes partial sums with their (max, sum of exponentials) that a second launch merges (flash decoding).
 //
 // Accuracy: f32 accumulation where cpu-ref accumulates in f64, and the key scale applied to the dot product rather
 // than to each product -- within the reference's own device tolerance for a quantized cache
@@ -37,10 +37,11 @@ struct AttnArgs {
     const int8_t* vc;     // [N, Hkv, D] value codes
     const float* vs;      // [N, Hkv] value scales
     float* out;           // [T, Hq, D], or null when `part` is written
-    float* part;          // [T * Hq * split, D + 2], or null
+    float* part;          // sums [T * Hq * split, D], then (max, sum) [T * Hq * split, 2]; or null
     int64_t tokens, q_heads, kv_heads, head_dim, kv_len, window;
     float scale, softcap;
     int causal, split;
+    int hg;  // KV heads a workgroup (8, 4, 2 or 1)
 };
 
 // The key range [first, last] of query token t (cpu_ref::attention, ops.cpp:565-575 without blocks and anchors).
@@ -51,7 +52,10 @@ __device__ __forceinline__ void key_range(const AttnArgs& a, int64_t t, int64_t&
     if (a.window > 0 && pos + a.window - 1 < last) last = pos + a.window - 1;
 }
 
-constexpr int kWaves = 4;    // waves a workgroup; each takes every fourth tile of 64 keys, and they merge in LDS
+// Waves a workgroup: eight (two a SIMD) where a wave's registers fit in 256, four for the wider cases (head_dim 256,
+// or five to eight query heads a KV head at head_dim 128).
+constexpr int waves_for(int G, int D) { return D * ((G + 3) / 4) <= 128 ? 8 : 4; }
+constexpr int kMaxWaves = 8;
 constexpr int kTile = 64;    // keys a wave works on at once (at most 64: one a lane for the scales)
 
 // Merges (m, l, acc) of another key set into this one: the online-softmax combine.
@@ -72,17 +76,6 @@ __device__ __forceinline__ float byte_f32(uint32_t w, int k) {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-// q of one head as a 23-bit integer per dim, Q = round(q / qs) with qs = max |q| / 2^22, written as three balanced
-// base-256 digits (hi * 65536 + mid * 256 + lo, each in [-128, 127]) so that int8 matrix cores can take it. The
-// digits are exact: qs * Q is q within 2^-23 of max |q|.
-__device__ __forceinline__ void q_digits(float q, float inv_qs, int& hi, int& mid, int& lo) {
-    const int Q = static_cast<int>(rintf(q * inv_qs));
-    lo = static_cast<int8_t>(Q & 0xff);
-    const int q1 = (Q - lo) >> 8;
-    mid = static_cast<int8_t>(q1 & 0xff);
-    hi = (q1 - mid) >> 8;
-}
-
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 
 // Reads 8 bytes a lane from LDS with the transpose of ds_read_b64_tr_b8: within each group of 16 lanes, with C_j the
@@ -94,44 +87,74 @@ __device__ __forceinline__ i32x2 lds_read_tr8(const uint8_t* p) {
     return __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) i32x2*)(p));
 }
 
-// G query heads per KV head, D head_dim (64, 128 or 256).
+// Byte d (d < 3) of the balanced base-256 digits of an integer |Q| < 2^23 (Q = hi 65536 + mid 256 + lo, each digit in
+// [-128, 127]); the signed byte of digit d is byte d of Q + bias_d, bias = {0, 128, 32896}: with lo + 128 in
+// [0, 255], (Q + 128) >> 8 = hi 256 + mid, and (Q + 32896) >> 16 = hi.
+__device__ __forceinline__ int digit_bias(int d) { return d == 0 ? 0 : d == 1 ? 128 : 32896; }
+
+// Packs byte `d` of each of four words into one (v_perm_b32; `sel` = d * 0x01010101 selects byte d of every source).
+__device__ __forceinline__ int pack_bytes(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, uint32_t d) {
+    // v_perm_b32(s0, s1, sel): byte selector k picks byte k of {s1 (bytes 0-3), s0 (bytes 4-7)}.
+    const uint32_t lo = __builtin_amdgcn_perm(w1, w0, 0x0c0c0400u + d * 0x0101u);  // [w0.d, w1.d, 0, 0]
+    const uint32_t hi = __builtin_amdgcn_perm(w3, w2, 0x04000c0cu + d * 0x01010000u);  // [0, 0, w2.d, w3.d]
+    return static_cast<int>(lo | hi);
+}
+
+// G query heads per KV head, D head_dim (64, 128 or 256), CAP: a softcap on the scores.
 //
-// Both products run on the int8 matrix cores (v_mfma_i32_16x16x64_i8; 16 x 16 results, K = 64):
-//  - scores S [16 keys, 16 heads] = key codes [16 keys, 64 dims] x digits of q [64 dims, 16 heads], a 64-dim chunk at
-//    a time. Lane l holds 16 codes of key l % 16 (dims 16 (l / 16) ..) -- a plain 16-byte load -- and the digits of
-//    head l % 16 over the same dims; it receives the scores of keys 4 (l / 16) + r (r < 4) for head l % 16.
-//  - the weighted sum O^T [16 dims, 16 heads] = value codes^T [16 dims, 64 keys] x digits of the weights
-//    [64 keys, 16 heads]. The value tile is staged in LDS row-major and read transposed (lds_read_tr8), so lane l
-//    holds 16 keys' codes of dim l % 16; the weights w = p * v_scale, as integers W = round(w / ws) with
-//    ws = max v_scale / 2^22 over the wave's keys (p <= 1), in three digits. Lane l receives dims 4 (l / 16) + r of
-//    head l % 16: exact int32 sums of the tile, added to the f32 accumulator times ws.
-template <int G, int D>
-__global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a, const float* __restrict__ qg) {
+// A workgroup of W waves (waves_for) takes one split of the keys of HG KV heads (HG = the largest power of two up to
+// W dividing kv_heads): wave w works on KV head w % HG and takes the split's tiles of 64 keys w / HG,
+// w / HG + W / HG, ... With HG = 8 the eight waves read the eight heads' rows of the same keys -- contiguous
+// [keys, heads, head_dim] spans -- together.
+// Each wave keeps the next tile's codes and scales loading into registers while it works on the current one.
+//
+// Both products run on the int8 matrix cores (v_mfma_i32_16x16x64_i8: A [16 x 64] x B [64 x 16], i32 results), with
+// the f32 operand written as three balanced base-256 int8 digits of an integer, so every product is exact:
+//  - scores: S^T [16 rows, 16 keys] = digits of q [16 rows, 64 dims] x key codes^T [64 dims, 16 keys], one 64-dim
+//    chunk at a time. Row 4 g + d holds digit d of head g (q / qs rounded, qs = max |q| / 2^22; row 4 g + 3 is zero),
+//    four heads a step. Lane l holds 16 codes of key l % 16, dims 16 (l / 16) .. -- a plain 16-byte load -- and
+//    receives rows 4 (l / 16) + r: the three digit sums of head l / 16 and key l % 16, combined in f32.
+//  - the weighted sum: O^T [16 dims, 16 cols] = value codes^T [16 dims, 64 keys] x weight digits [64 keys, 16 cols],
+//    column 4 g + d holding digit d of W = p v_scale / ws for head g (ws = the tile's max p v_scale / 2^22).
+//    The value tile is staged in LDS and read transposed (lds_read_tr8); lane l receives dims 4 (l / 16) + r of
+//    column l % 16, which it accumulates in f32 times ws 256^d. The digit columns of a head add up at the end.
+template <int G, int D, bool CAP>
+__global__ __launch_bounds__(64 * waves_for(G, D)) void attention_i8_rows(AttnArgs a) {
+    constexpr int kWaves = waves_for(G, D);
+    constexpr int NG = (G + 3) / 4;        // groups of four heads: one matrix-core step each
     constexpr int KC = D / 64;             // 64-dim chunks of a key row: the K of one score step
-    constexpr int KB = kTile / 16;         // 16-key blocks of a tile: the M of one score step
+    constexpr int KB = kTile / 16;         // 16-key blocks of a tile: the N of one score step
     constexpr int DB = D / 16;             // 16-dim blocks of a value row: the M of one weighted-sum step
-    constexpr int VROW = D + 8;            // LDS bytes a staged value row (8 bytes of padding: distinct banks for the
-                                           // eight rows one transposed read covers)
-    constexpr int VLPR = D / 8;            // lanes a value row with 8-byte loads
+    constexpr int VROW = D + 16;           // LDS bytes a staged value row (16 bytes of padding: the eight rows one
+                                           // transposed read covers start on distinct banks)
+    constexpr int VLPR = D / 16;           // lanes a value row with 16-byte loads
     constexpr int VRPI = 64 / VLPR;        // value rows one load instruction covers
     constexpr int VI = kTile / VRPI;       // value load instructions a tile
-    static_assert(G <= 16, "the query heads of a KV head fill at most the 16 columns of a matrix-core step");
+    constexpr int VT = kTile * VROW;       // bytes of a wave's value tile
+    constexpr int PT = NG * 4 * kTile * 4; // bytes of a wave's weight tile: W [NG * 4 heads][kTile keys]
+    constexpr int WAVE_LDS = VT + PT + 2 * kTile * 4;
+    constexpr int MROW = D + 2;            // a merge row: D sums, max, sum
+    static_assert(G >= 1 && G <= 8, "one or two groups of four heads");
     static_assert(kTile == 64, "a weighted-sum step takes the 64 keys of a tile");
-    __shared__ __align__(16) float ptile[kWaves][G][kTile];     // p of each head and key of each wave's tile
-    __shared__ __align__(16) float vscale[kWaves][kTile];       // value scales of each wave's tile
-    __shared__ __align__(16) float kscale[kWaves][kTile];       // key scales of each wave's tile
-    __shared__ __align__(16) uint8_t vtile[kWaves][kTile * VROW];
-    __shared__ float mbuf[kWaves][G][D + 2];
+    static_assert(kWaves * G * MROW * 4 <= kWaves * WAVE_LDS, "the merge rows fit in the tiles' LDS");
+    __shared__ __align__(16) uint8_t lds[kWaves * WAVE_LDS];
 
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    // Grid (split, token x KV head): consecutive workgroup ids are splits, so the KV heads of one split share an id
-    // residue mod 8 -- the same XCD and L2 -- and the lines of key/value rows and scales those heads share are fetched
-    // once per XCD rather than once per head.
-    const int64_t row = blockIdx.y;  // (t, kv head)
-    const int64_t t = row / a.kv_heads;
-    const int64_t kvh = row - t * a.kv_heads;
+    const int c16 = lane & 15;  // the key (score step) or column (weighted-sum step) of this lane
+    const int kq = lane >> 4;   // its 16-dim / 16-key / 4-row group
+    const int hg = a.hg;
+    const int np = kWaves / hg;  // waves a KV head
+    const int phase = wave / hg;
+    const int64_t groups = a.kv_heads / hg;
+    const int64_t t = blockIdx.y / groups;
+    const int64_t kvh = (blockIdx.y - t * groups) * hg + wave % hg;
     const int s = blockIdx.x;
+
+    uint8_t* const vt = lds + wave * WAVE_LDS;
+    float* const ptile = reinterpret_cast<float*>(vt + VT);  // [NG * 4][kTile]
+    float* const kscale = ptile + NG * 4 * kTile;            // [kTile]
+    float* const vscale = kscale + kTile;                    // [kTile]
 
     int64_t first, last;
     key_range(a, t, first, last);
@@ -143,259 +166,329 @@ __global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a, con
     const int64_t span = k1 >= k0 ? k1 - k0 + 1 : 0;
     const int64_t tiles = (span + kTile - 1) / kTile;
 
-    const int h = lane & 15;   // the head (matrix-core column) of this lane
-    const int kq = lane >> 4;  // its 16-dim / 16-key / 4-row group
-
-    // q as three digits per dim (the score step's B operand), and its scale.
-    i32x4 qd[3][KC];
-    float qs_h;
-    {
-        float qv[KC][16];
-        float mx = 0.0f;
-        const float* q = qg + (t * a.q_heads + kvh * G + (h < G ? h : 0)) * D;
+    // Loads of one tile into registers: key codes in the score step's B layout, value codes (for LDS), this lane's
+    // key's scales. A tile wholly inside the split addresses its rows from one base; the split's last tile clamps
+    // each key to the split's last.
+    i32x4 kw[KB][KC];
+    u32x4 vw[VI];
+    float ksv = 0.0f, vsv = 0.0f;
+    const int64_t rstride = a.kv_heads * D;  // bytes from one key's row to the next of the same KV head
+    auto load_tile = [&](int64_t j0) {
+        if (j0 + kTile - 1 <= k1) {  // uniform
+            const int8_t* kp = a.kc + ((j0 + c16) * a.kv_heads + kvh) * D + kq * 16;
+            const int8_t* vp = a.vc + ((j0 + lane / VLPR) * a.kv_heads + kvh) * D + (lane % VLPR) * 16;
 #pragma unroll
-        for (int c = 0; c < KC; ++c) {
+            for (int b = 0; b < KB; ++b) {
 #pragma unroll
-            for (int i = 0; i < 16; i += 4) {
-                const u32x4 raw = ld128(q + c * 64 + kq * 16 + i);
+                for (int c = 0; c < KC; ++c)
+                    kw[b][c] = __builtin_bit_cast(i32x4, ld128_nt(kp + b * 16 * rstride + c * 64));
+            }
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    qv[c][i + e] = h < G ? __uint_as_float(raw[e]) : 0.0f;
-                    mx = fmaxf(mx, fabsf(qv[c][i + e]));
-                }
+            for (int i = 0; i < VI; ++i) vw[i] = ld128_nt(vp + i * VRPI * rstride);
+        } else {
+#pragma unroll
+            for (int b = 0; b < KB; ++b) {
+                int64_t j = j0 + b * 16 + c16;
+                j = j <= k1 ? j : k1;
+                const int8_t* kp = a.kc + (j * a.kv_heads + kvh) * D + kq * 16;
+#pragma unroll
+                for (int c = 0; c < KC; ++c) kw[b][c] = __builtin_bit_cast(i32x4, ld128_nt(kp + c * 64));
+            }
+#pragma unroll
+            for (int i = 0; i < VI; ++i) {
+                int64_t j = j0 + i * VRPI + lane / VLPR;
+                j = j <= k1 ? j : k1;
+                vw[i] = ld128_nt(a.vc + (j * a.kv_heads + kvh) * D + (lane % VLPR) * 16);
             }
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));  // max |q| of head h over all its dims
-        qs_h = mx / 4194304.0f;
-        const float inv = mx > 0.0f ? 4194304.0f / mx : 0.0f;
+        const int64_t jl = j0 + lane;
+        const int64_t rk = (jl <= k1 ? jl : k1) * a.kv_heads + kvh;
+        ksv = a.ks[rk];
+        vsv = a.vs[rk];
+    };
+
+    // q as digit rows (the score step's A operand): lane l holds digit l % 4 of head (l % 16) / 4 + 4 ng over dims
+    // 64 c + 16 (l / 16) ..; score_scale[ng] is qs * scale of head l / 16 + 4 ng, the head of this lane's scores.
+    i32x4 qa[NG][KC];
+    float score_scale[NG];
+    {
+        const int dq = c16 & 3;
+        u32x4 raw[NG][KC][4];
 #pragma unroll
-        for (int c = 0; c < KC; ++c) {
+        for (int ng = 0; ng < NG; ++ng) {
+            const int g = (c16 >> 2) + 4 * ng;
+            const float* q = a.q + (t * a.q_heads + kvh * G + (g < G ? g : G - 1)) * D;
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                uint32_t dh = 0, dm = 0, dl = 0;
+            for (int c = 0; c < KC; ++c) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    int hi, mid, lo;
-                    q_digits(qv[c][4 * w + e], inv, hi, mid, lo);
-                    dh |= static_cast<uint32_t>(hi & 0xff) << (8 * e);
-                    dm |= static_cast<uint32_t>(mid & 0xff) << (8 * e);
-                    dl |= static_cast<uint32_t>(lo & 0xff) << (8 * e);
-                }
-                qd[0][c][w] = static_cast<int>(dh);
-                qd[1][c][w] = static_cast<int>(dm);
-                qd[2][c][w] = static_cast<int>(dl);
+                for (int i = 0; i < 4; ++i) raw[ng][c][i] = ld128(q + c * 64 + kq * 16 + 4 * i);
             }
         }
-    }
-    const float score_scale = qs_h * a.scale;
-
-    // The weights' integer scale: the largest value scale among this wave's keys (p <= 1 bounds the weights by it).
-    float ws;
-    {
-        float mv = 0.0f;
-        for (int64_t tile = wave; tile < tiles; tile += kWaves) {
-            const int64_t j = k0 + tile * kTile + lane;
-            if (j <= k1) mv = fmaxf(mv, a.vs[j * a.kv_heads + kvh]);
+        // The first tile's loads go out behind q's, to be in flight while the digits are made.
+        if (phase < tiles) load_tile(k0 + phase * kTile);
+#pragma unroll
+        for (int ng = 0; ng < NG; ++ng) {
+            float mx = 0.0f;
+#pragma unroll
+            for (int c = 0; c < KC; ++c) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) mx = fmaxf(mx, fabsf(__uint_as_float(raw[ng][c][i][e])));
+                }
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));  // max |q| of head (l % 16) / 4 + 4 ng over all its dims
+            const float inv = mx > 0.0f ? 4194304.0f / mx : 0.0f;
+            const bool live = dq < 3 && (c16 >> 2) + 4 * ng < G;
+            const int bias = digit_bias(dq);
+#pragma unroll
+            for (int c = 0; c < KC; ++c) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    uint32_t w[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        w[e] = static_cast<uint32_t>(static_cast<int>(rintf(__uint_as_float(raw[ng][c][i][e]) * inv)) +
+                                                     bias);
+                    qa[ng][c][i] = live ? pack_bytes(w[0], w[1], w[2], w[3], static_cast<uint32_t>(dq)) : 0;
+                }
+            }
+            score_scale[ng] = __shfl(mx, 4 * kq, 64) * (1.0f / 4194304.0f) * a.scale;
         }
-        mv = group_reduce<64, OpMax>(mv);
-        ws = mv / 4194304.0f;
-    }
-    const float inv_ws = ws > 0.0f ? 1.0f / ws : 0.0f;
-
-    float m[G];                 // the wave's running max per head (the same in every lane)
-    float lsum = 0.0f;          // this lane's share of head h's sum of exponentials
-    float mh = -INFINITY;       // the running max of head h
-    float facc[DB][4];          // head h, dims 16 db + 4 kq + r: the weighted sums
-#pragma unroll
-    for (int g = 0; g < G; ++g) m[g] = -INFINITY;
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) facc[db][r] = 0.0f;
     }
 
-    // The waves run independently: wave w takes tiles w, w + kWaves, ... and touches only its own LDS, whose writes
-    // and reads are ordered within the wave (wave_sync).
+    // Running state. Score lanes (row kq) follow head kq + 4 ng: its running max m and their share of its sum of
+    // exponentials. Weighted-sum lanes hold column c16 = (head (c16 / 4) + 4 ng, digit c16 % 4), dims
+    // 16 db + 4 kq + r.
+    float m[NG], lsum[NG];
+    float facc[NG][DB][4];
+#pragma unroll
+    for (int ng = 0; ng < NG; ++ng) {
+        m[ng] = -INFINITY;
+        lsum[ng] = 0.0f;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) facc[ng][db][r] = 0.0f;
+        }
+    }
+    const uint32_t dcol = static_cast<uint32_t>(c16 & 3);
+    const int wbias = digit_bias(static_cast<int>(dcol));
+    const float dscale = dcol == 0 ? 1.0f : dcol == 1 ? 256.0f : dcol == 2 ? 65536.0f : 0.0f;
+
+    // The waves run independently: each touches only its own LDS, whose writes and reads are ordered within the
+    // wave (wave_sync).
     auto wave_sync = [] {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
-    uint8_t* vt = vtile[wave];
-    for (int64_t tile = wave; tile < tiles; tile += kWaves) {
+    for (int64_t tile = phase; tile < tiles; tile += np) {
         const int64_t j0 = k0 + tile * kTile;  // keys j0 .. j0 + 63 (those past k1 clamped to it, weights 0)
-        // Loads: key codes in the score step's A layout, value rows (to LDS), the tile's scales.
-        i32x4 kw[KB][KC];
-#pragma unroll
-        for (int b = 0; b < KB; ++b) {
-            int64_t j = j0 + b * 16 + h;
-            j = j <= k1 ? j : k1;
-            const int8_t* kp = a.kc + (j * a.kv_heads + kvh) * D + kq * 16;
-#pragma unroll
-            for (int c = 0; c < KC; ++c) kw[b][c] = __builtin_bit_cast(i32x4, ld128_nt(kp + c * 64));
-        }
-        uint64_t vw[VI];
-#pragma unroll
-        for (int i = 0; i < VI; ++i) {
-            int64_t j = j0 + i * VRPI + lane / VLPR;
-            j = j <= k1 ? j : k1;
-            vw[i] = __builtin_nontemporal_load(
-                reinterpret_cast<const uint64_t*>(a.vc + (j * a.kv_heads + kvh) * D + (lane % VLPR) * 8));
-        }
-        {
-            const int64_t jl = j0 + lane;
-            const int64_t rk = (jl <= k1 ? jl : k1) * a.kv_heads + kvh;
-            kscale[wave][lane] = a.ks[rk];
-            vscale[wave][lane] = a.vs[rk];
-        }
+        // Stage: value codes and the scales to LDS.
 #pragma unroll
         for (int i = 0; i < VI; ++i)
-            *reinterpret_cast<uint64_t*>(vt + (i * VRPI + lane / VLPR) * VROW + (lane % VLPR) * 8) = vw[i];
-        wave_sync();
+            *reinterpret_cast<u32x4*>(vt + (i * VRPI + lane / VLPR) * VROW + (lane % VLPR) * 16) = vw[i];
+        kscale[lane] = ksv;
+        vscale[lane] = vsv;
 
-        // Scores: three digit products per 16-key block and 64-dim chunk, combined in f32.
-        float sc[KB][4];
-        float mt = -INFINITY;
+        // Scores, straight from the registers the key codes arrived in.
+        i32x4 sr[NG][KB];
 #pragma unroll
-        for (int b = 0; b < KB; ++b) {
-            i32x4 r0 = {0, 0, 0, 0}, r1 = {0, 0, 0, 0}, r2 = {0, 0, 0, 0};
-#pragma unroll
-            for (int c = 0; c < KC; ++c) {
-                r0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kw[b][c], qd[0][c], r0, 0, 0, 0);
-                r1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kw[b][c], qd[1][c], r1, 0, 0, 0);
-                r2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kw[b][c], qd[2][c], r2, 0, 0, 0);
-            }
-            const u32x4 ks4 = *reinterpret_cast<const u32x4*>(&kscale[wave][b * 16 + kq * 4]);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float dot = static_cast<float>(r0[r]) * 65536.0f + static_cast<float>(r1[r]) * 256.0f +
-                                  static_cast<float>(r2[r]);
-                float x = dot * score_scale * __uint_as_float(ks4[r]);
-                if (a.softcap > 0.0f) x = a.softcap * tanhf(x / a.softcap);
-                const bool valid = j0 + b * 16 + kq * 4 + r <= k1;
-                sc[b][r] = valid ? x : -INFINITY;
-                mt = fmaxf(mt, sc[b][r]);
-            }
-        }
-        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));  // the tile's max of head h
-        // A larger max for some head: flush the digit sums, rescaling each lane's head by exp(old - new).
-        const float mn = fmaxf(mh, mt);
-        bool moved = false;
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float mtg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mt), g));
-            moved |= mtg > m[g];
-            m[g] = fmaxf(m[g], mtg);
-        }
-        if (moved) {  // uniform across the wave
-            const float c = mh == -INFINITY ? 0.0f : __expf(mh - mn);
-            lsum *= c;
-#pragma unroll
-            for (int db = 0; db < DB; ++db) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) facc[db][r] *= c;
-            }
-        }
-        mh = mn;
-        // p = exp(s - max) per (head, key) to LDS; this lane's keys: 16 b + 4 kq + r of head h.
-        if (h < G) {
+        for (int ng = 0; ng < NG; ++ng) {
 #pragma unroll
             for (int b = 0; b < KB; ++b) {
-                float p4[4];
+                i32x4 acc = {0, 0, 0, 0};
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    p4[r] = __expf(sc[b][r] - mh);  // 0 for keys past the split (-inf)
-                    lsum += p4[r];
-                }
-                *reinterpret_cast<u32x4*>(&ptile[wave][h][b * 16 + kq * 4]) =
-                    u32x4{__float_as_uint(p4[0]), __float_as_uint(p4[1]), __float_as_uint(p4[2]),
-                          __float_as_uint(p4[3])};
+                for (int c = 0; c < KC; ++c) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[ng][c], kw[b][c], acc, 0, 0, 0);
+                sr[ng][b] = acc;
             }
+        }
+        // The next tile's loads, into the registers just consumed (uniform branch).
+        if (tile + np < tiles) load_tile(j0 + np * kTile);
+        wave_sync();
+
+        float ksc[KB];
+#pragma unroll
+        for (int b = 0; b < KB; ++b) ksc[b] = kscale[b * 16 + c16];
+        float sc[NG][KB];
+        float mt[NG];
+        bool moved = false;
+#pragma unroll
+        for (int ng = 0; ng < NG; ++ng) {
+            const bool head_ok = kq + 4 * ng < G;
+            mt[ng] = -INFINITY;
+#pragma unroll
+            for (int b = 0; b < KB; ++b) {
+                const float dot = fmaf(static_cast<float>(sr[ng][b][2]), 65536.0f,
+                                       fmaf(static_cast<float>(sr[ng][b][1]), 256.0f, static_cast<float>(sr[ng][b][0])));
+                float x = dot * (score_scale[ng] * ksc[b]);
+                if constexpr (CAP) x = a.softcap * tanhf(x / a.softcap);
+                const bool valid = head_ok && j0 + b * 16 + c16 <= k1;
+                sc[ng][b] = valid ? x : -INFINITY;
+                mt[ng] = fmaxf(mt[ng], sc[ng][b]);
+            }
+            mt[ng] = group_reduce<16, OpMax>(mt[ng]);  // the tile's max of head kq + 4 ng
+            moved |= mt[ng] > m[ng];
+        }
+        // A larger max for some head (uniform branch): rescale its sum and its columns' sums by exp(old - new).
+        if (__builtin_amdgcn_ballot_w64(moved) != 0) {
+#pragma unroll
+            for (int ng = 0; ng < NG; ++ng) {
+                const float mn = fmaxf(m[ng], mt[ng]);
+                const float c = m[ng] == -INFINITY ? 0.0f : __expf(m[ng] - mn);
+                lsum[ng] *= c;
+                m[ng] = mn;
+                const float cc = __shfl(c, 16 * (c16 >> 2), 64);  // the factor of this lane's column head
+#pragma unroll
+                for (int db = 0; db < DB; ++db) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) facc[ng][db][r] *= cc;
+                }
+            }
+        }
+        // p = exp(s - max) and the weights w = p v_scale; as integers W = w / ws, ws = the tile's max w of the head
+        // / 2^22, so every tile's weights keep 22 bits whatever its scores' distance from the running max. W + 1/2
+        // goes to LDS, [head][key], so that the digits' truncation rounds W to nearest (truncation alone would bias
+        // every weight down, and the errors would add up). wsc: ws times the digit's weight, for this lane's column.
+        float wsc[NG];
+#pragma unroll
+        for (int ng = 0; ng < NG; ++ng) {
+            float w[KB];
+            float wmax = 0.0f;
+#pragma unroll
+            for (int b = 0; b < KB; ++b) {
+                const float p = __expf(sc[ng][b] - m[ng]);  // 0 for masked keys (-inf)
+                lsum[ng] += p;
+                w[b] = p * vscale[b * 16 + c16];
+                wmax = fmaxf(wmax, w[b]);
+            }
+            wmax = group_reduce<16, OpMax>(wmax);  // the tile's largest weight of head kq + 4 ng
+            const float inv = wmax > 0.0f ? 4194304.0f / wmax : 0.0f;
+#pragma unroll
+            for (int b = 0; b < KB; ++b) ptile[(ng * 4 + kq) * kTile + b * 16 + c16] = fmaf(w[b], inv, 0.5f);
+            wsc[ng] = __shfl(wmax, 16 * (c16 >> 2), 64) * (1.0f / 4194304.0f) * dscale;
         }
         wave_sync();
 
-        // Weights of head h over keys 16 kq .. + 15, as three digits: the weighted-sum step's B operand.
-        i32x4 wd[3];
-        {
-            float w[16];
+        // Weight digits: column (head (c16 / 4) + 4 ng, digit c16 % 4) over keys 16 kq .. + 15.
+        i32x4 wd[NG];
 #pragma unroll
-            for (int i = 0; i < 16; i += 4) {
-                const u32x4 p4 = h < G ? *reinterpret_cast<const u32x4*>(&ptile[wave][h][kq * 16 + i]) : u32x4{0, 0, 0, 0};
-                const u32x4 v4 = *reinterpret_cast<const u32x4*>(&vscale[wave][kq * 16 + i]);
+        for (int ng = 0; ng < NG; ++ng) {
+            const float* pw = ptile + (ng * 4 + (c16 >> 2)) * kTile + kq * 16;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) w[i + e] = __uint_as_float(p4[e]) * __uint_as_float(v4[e]);
-            }
+            for (int i = 0; i < 4; ++i) {
+                const u32x4 w4 = *reinterpret_cast<const u32x4*>(pw + 4 * i);
+                uint32_t w[4];
 #pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-                uint32_t dh = 0, dm = 0, dl = 0;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    int hi, mid, lo;
-                    q_digits(w[4 * q4 + e], inv_ws, hi, mid, lo);
-                    dh |= static_cast<uint32_t>(hi & 0xff) << (8 * e);
-                    dm |= static_cast<uint32_t>(mid & 0xff) << (8 * e);
-                    dl |= static_cast<uint32_t>(lo & 0xff) << (8 * e);
-                }
-                wd[0][q4] = static_cast<int>(dh);
-                wd[1][q4] = static_cast<int>(dm);
-                wd[2][q4] = static_cast<int>(dl);
+                for (int e = 0; e < 4; ++e)
+                    w[e] = static_cast<uint32_t>(static_cast<int>(__uint_as_float(w4[e])) + wbias);
+                wd[ng][i] = pack_bytes(w[0], w[1], w[2], w[3], dcol);
             }
         }
         // Weighted sum: per 16-dim block, the transposed value codes of keys 16 kq .. + 15 against the digits.
-        const int tr_row = kq * 16 + (h >> 1);
-        const int tr_col = 8 * (h & 1);
+        const int tr_row = kq * 16 + (c16 >> 1);
+        const int tr_col = 8 * (c16 & 1);
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
             const i32x2 lo8 = lds_read_tr8(vt + tr_row * VROW + db * 16 + tr_col);
             const i32x2 hi8 = lds_read_tr8(vt + (tr_row + 8) * VROW + db * 16 + tr_col);
             const i32x4 va = {lo8[0], lo8[1], hi8[0], hi8[1]};
-            const i32x4 zero = {0, 0, 0, 0};
-            const i32x4 r0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(va, wd[0], zero, 0, 0, 0);
-            const i32x4 r1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(va, wd[1], zero, 0, 0, 0);
-            const i32x4 r2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(va, wd[2], zero, 0, 0, 0);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float v = static_cast<float>(r0[r]) * 65536.0f + static_cast<float>(r1[r]) * 256.0f +
-                                static_cast<float>(r2[r]);
-                facc[db][r] = fmaf(v, ws, facc[db][r]);
+            for (int ng = 0; ng < NG; ++ng) {
+                const i32x4 zero = {0, 0, 0, 0};
+                const i32x4 r4 = __builtin_amdgcn_mfma_i32_16x16x64_i8(va, wd[ng], zero, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) facc[ng][db][r] = fmaf(static_cast<float>(r4[r]), wsc[ng], facc[ng][db][r]);
             }
         }
         wave_sync();  // the tiles are rewritten next time
     }
 
-    // Each head's sum of exponentials is spread over the lanes of that head. Then the four waves merge through LDS;
-    // lane l holds dims 16 db + 4 kq + r of head h.
-    lsum += __shfl_xor(lsum, 16, 64);
-    lsum += __shfl_xor(lsum, 32, 64);
-    if (h < G) {
+    // The digit columns of each head add up (lanes 4 g .. 4 g + 3 of each row; the digit-3 column is zero); each
+    // head's sum of exponentials is spread over the 16 lanes of its score row.
+#pragma unroll
+    for (int ng = 0; ng < NG; ++ng) {
+        lsum[ng] = group_reduce<16, OpSum>(lsum[ng]);
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) mbuf[wave][h][db * 16 + kq * 4 + r] = facc[db][r];
+            for (int r = 0; r < 4; ++r) facc[ng][db][r] = group_reduce<4, OpSum>(facc[ng][db][r]);
+        }
+    }
+    // Lane (kq, 4 g') now holds dims 16 db + 4 kq + r of head g' + 4 ng; its max and sum come from row g'.
+    const bool writer = (c16 & 3) == 0;
+    if (np == 1) {  // uniform: this wave alone covers its head's keys of the split
+#pragma unroll
+        for (int ng = 0; ng < NG; ++ng) {
+            const int g = (c16 >> 2) + 4 * ng;
+            const float mg = __shfl(m[ng], 16 * (c16 >> 2), 64);
+            const float lg = __shfl(lsum[ng], 16 * (c16 >> 2), 64);
+            if (!writer || g >= G) continue;
+            const int64_t hh = kvh * G + g;
+            if (a.part == nullptr) {
+                float* o = a.out + (t * a.q_heads + hh) * D + 4 * kq;
+                const float inv = 1.0f / lg;
+#pragma unroll
+                for (int db = 0; db < DB; ++db)
+                    *reinterpret_cast<u32x4*>(o + 16 * db) =
+                        u32x4{__float_as_uint(facc[ng][db][0] * inv), __float_as_uint(facc[ng][db][1] * inv),
+                              __float_as_uint(facc[ng][db][2] * inv), __float_as_uint(facc[ng][db][3] * inv)};
+            } else {
+                const int64_t pi = (t * a.q_heads + hh) * a.split + s;  // partial row
+                float* pr = a.part + pi * D + 4 * kq;
+#pragma unroll
+                for (int db = 0; db < DB; ++db)
+                    *reinterpret_cast<u32x4*>(pr + 16 * db) =
+                        u32x4{__float_as_uint(facc[ng][db][0]), __float_as_uint(facc[ng][db][1]),
+                              __float_as_uint(facc[ng][db][2]), __float_as_uint(facc[ng][db][3])};
+                if (kq == 0) {
+                    float* ml = a.part + a.tokens * a.q_heads * a.split * D + 2 * pi;
+                    ml[0] = mg;
+                    ml[1] = lg;
+                }
+            }
+        }
+        return;
+    }
+    // Several waves a head: their (max, sum, sums) merge in LDS, over the tiles' space once every wave is done.
+    __syncthreads();
+    float* const mbuf = reinterpret_cast<float*>(lds);  // [kWaves][G][MROW]
+#pragma unroll
+    for (int ng = 0; ng < NG; ++ng) {
+        const int g = (c16 >> 2) + 4 * ng;
+        const float mg = __shfl(m[ng], 16 * (c16 >> 2), 64);
+        const float lg = __shfl(lsum[ng], 16 * (c16 >> 2), 64);
+        if (!writer || g >= G) continue;
+        float* mr = mbuf + (wave * G + g) * MROW;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mr[16 * db + 4 * kq + r] = facc[ng][db][r];
         }
         if (kq == 0) {
-            mbuf[wave][h][D] = mh;
-            mbuf[wave][h][D + 1] = lsum;
+            mr[D] = mg;
+            mr[D + 1] = lg;
         }
     }
     __syncthreads();
-    // Wave 0 merges: lane l takes dims l * D / 64 .. of every head.
-    if (wave != 0) return;
+    // The phase-0 wave of each head merges: lane l takes dims l * D / 64 .. of each of the head's G query heads.
+    if (phase != 0) return;
     constexpr int DL = D / 64;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        float mg = mbuf[0][g][D], lg = mbuf[0][g][D + 1];
+        const float* m0 = mbuf + (wave * G + g) * MROW;
+        float mg = m0[D], lg = m0[D + 1];
         float ag[DL];
 #pragma unroll
-        for (int i = 0; i < DL; ++i) ag[i] = mbuf[0][g][lane * DL + i];
-#pragma unroll
-        for (int w = 1; w < kWaves; ++w) {
+        for (int i = 0; i < DL; ++i) ag[i] = m0[lane * DL + i];
+        for (int p = 1; p < np; ++p) {
+            const float* mo = mbuf + ((wave + p * hg) * G + g) * MROW;
             float ao[DL];
 #pragma unroll
-            for (int i = 0; i < DL; ++i) ao[i] = mbuf[w][g][lane * DL + i];
-            merge<DL>(mg, lg, ag, mbuf[w][g][D], mbuf[w][g][D + 1], ao);
+            for (int i = 0; i < DL; ++i) ao[i] = mo[lane * DL + i];
+            merge<DL>(mg, lg, ag, mo[D], mo[D + 1], ao);
         }
         const int64_t hh = kvh * G + g;
         if (a.part == nullptr) {
@@ -404,80 +497,94 @@ __global__ __launch_bounds__(64 * kWaves) void attention_i8_rows(AttnArgs a, con
 #pragma unroll
             for (int i = 0; i < DL; ++i) o[i] = ag[i] * inv;
         } else {
-            float* pr = a.part + ((t * a.q_heads + hh) * a.split + s) * (D + 2);
+            const int64_t pi = (t * a.q_heads + hh) * a.split + s;  // partial row
+            float* pr = a.part + pi * D;
 #pragma unroll
             for (int i = 0; i < DL; ++i) pr[lane * DL + i] = ag[i];
             if (lane == 0) {
-                pr[D] = mg;
-                pr[D + 1] = lg;
+                float* ml = a.part + a.tokens * a.q_heads * a.split * D + 2 * pi;
+                ml[0] = mg;
+                ml[1] = lg;
             }
         }
     }
 }
 
-// out [rows, D] from `split` partial rows [D sums, max, sum] each (sycl_be::attention_combine's layout). A workgroup of
-// four waves a row: the threads take the splits for the max, the weights and the denominator, then (dim, split
-// quarter) pairs, each summing its share of the column with the weights from LDS; the quarters add up in LDS.
+// out [rows, D] from `split` partial results per row: sums part [rows, split, D], then (max, sum of exponentials)
+// pairs ml [rows, split, 2] (the scratch holds the two arrays back to back). A workgroup takes kCombineDims dims of one
+// row: thread (split group g, 4-dim group) loads the partial sums of splits g, g + 32, ... (all of them, up to
+// kMaxSplit, in one round of loads), and thread s the (max, sum) of split s; so every load is issued before the first
+// wait. The maximum, the weights exp(max_s - max) and the denominator come from LDS reductions; the 32 split groups'
+// weighted sums add up in LDS.
 constexpr int kMaxSplit = 256;
+constexpr int kCombineDims = 32;
 
-__global__ __launch_bounds__(256) void attention_combine_rows(const float* part, float* out, int split, int64_t D) {
+__global__ __launch_bounds__(256) void attention_combine_rows(const float* part, float* out, int split, int64_t D,
+                                                              int64_t rows) {
+    constexpr int kD4 = kCombineDims / 4;  // 4-dim groups a workgroup
+    constexpr int kGroups = 256 / kD4;     // split groups
+    constexpr int kPer = kMaxSplit / kGroups;
     __shared__ float weight[kMaxSplit];
-    __shared__ float red[256];
-    const int64_t r = blockIdx.x;
+    __shared__ float red[2][4];
+    __shared__ u32x4 acc4[kGroups][kD4];
+    const uint32_t chunks = static_cast<uint32_t>(D / kCombineDims);
+    const int64_t r = blockIdx.x / chunks;
+    const int64_t d0 = (blockIdx.x - static_cast<uint32_t>(r) * chunks) * kCombineDims;
     const int tid = threadIdx.x;
-    const float* pr = part + r * split * (D + 2);
-    float mx = -INFINITY;
-    for (int s = tid; s < split; s += 256) mx = fmaxf(mx, pr[s * (D + 2) + D]);
-    mx = group_reduce<64, OpMax>(mx);
-    if ((tid & 63) == 0) red[tid >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-    float den = 0.0f;
-    for (int s = tid; s < split; s += 256) {
-        const float ms = pr[s * (D + 2) + D];
-        const float w = ms == -INFINITY ? 0.0f : __expf(ms - mx);
-        weight[s] = w;
-        den += pr[s * (D + 2) + D + 1] * w;
-    }
-    den = group_reduce<64, OpSum>(den);
-    if ((tid & 63) == 0) red[tid >> 6] = den;
-    __syncthreads();
-    den = (red[0] + red[1]) + (red[2] + red[3]);
-    const float inv = 1.0f / den;
-    __syncthreads();
-    // Dims in chunks of 64: thread (d, quarter) sums splits quarter, quarter + 4, ...
-    const int dl = tid & 63, quarter = tid >> 6;
-    for (int64_t d0 = 0; d0 < D; d0 += 64) {
-        const int64_t d = d0 + dl;
-        float acc = 0.0f;
-        if (d < D) {
-            // eight loads in flight before the first is used
-            for (int s0 = quarter; s0 < split; s0 += 32) {
-                float v[8];
+    const int d4 = tid % kD4, grp = tid / kD4;
+    const float* ml = part + rows * split * D + r * split * 2;
+    const float2 mls = *reinterpret_cast<const float2*>(ml + 2 * (tid < split ? tid : split - 1));
+    const float ms = tid < split ? mls.x : -INFINITY, ls = tid < split ? mls.y : 0.0f;
+    u32x4 v[kPer];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int s = s0 + 4 * u;
-                    v[u] = s < split ? pr[s * (D + 2) + d] : 0.0f;
-                }
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int s = s0 + 4 * u;
-                    acc += s < split ? v[u] * weight[s] : 0.0f;
-                }
-            }
-        }
-        red[tid] = acc;
-        __syncthreads();
-        if (quarter == 0 && d < D) out[r * D + d] = ((red[dl] + red[64 + dl]) + (red[128 + dl] + red[192 + dl])) * inv;
-        __syncthreads();
+    for (int u = 0; u < kPer; ++u) {
+        const int sp = grp + u * kGroups < split ? grp + u * kGroups : split - 1;  // weight 0 past the last split
+        v[u] = ld128(part + (r * split + sp) * D + d0 + 4 * d4);
     }
+    float mx = group_reduce<64, OpMax>(ms);
+    if ((tid & 63) == 0) red[0][tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    const float w = ms == -INFINITY ? 0.0f : __expf(ms - mx);  // splits without keys (max -inf) weigh nothing
+    if (tid < kMaxSplit) weight[tid] = w;
+    float den = group_reduce<64, OpSum>(ls * w);
+    if ((tid & 63) == 0) red[1][tid >> 6] = den;
+    __syncthreads();
+    den = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int sp = grp + u * kGroups;
+        const float ws = sp < split ? weight[sp] : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] += __uint_as_float(v[u][e]) * ws;
+    }
+    acc4[grp][d4] = u32x4{__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]),
+                          __float_as_uint(acc[3])};
+    __syncthreads();
+    if (tid < kCombineDims) {
+        const int dd = tid / 4, e = tid % 4;
+        float sum = 0.0f;
+#pragma unroll 8
+        for (int g = 0; g < kGroups; ++g) sum += __uint_as_float(acc4[g][dd][e]);
+        out[r * D + d0 + tid] = sum / den;
+    }
+}
+
+// KV heads a workgroup of `waves` waves: the largest power of two up to `waves` dividing kv_heads.
+int heads_per_group(int64_t kv_heads, int waves) {
+    int hg = waves;
+    while (kv_heads % hg != 0) hg /= 2;
+    return hg;
 }
 
 template <int G, int D>
-void launch_rows(hipStream_t s, const AttnArgs& a) {
-    const dim3 grid(static_cast<unsigned>(a.split), static_cast<unsigned>(a.tokens * a.kv_heads));
-    attention_i8_rows<G, D><<<grid, 64 * kWaves, 0, s>>>(a, a.q);
+void launch_rows(hipStream_t s, AttnArgs a) {
+    constexpr int W = waves_for(G, D);
+    a.hg = heads_per_group(a.kv_heads, W);
+    const dim3 grid(static_cast<unsigned>(a.split), static_cast<unsigned>(a.tokens * (a.kv_heads / a.hg)));
+    if (a.softcap > 0.0f) attention_i8_rows<G, D, true><<<grid, 64 * W, 0, s>>>(a);
+    else attention_i8_rows<G, D, false><<<grid, 64 * W, 0, s>>>(a);
 }
 
 template <int G>
@@ -502,10 +609,11 @@ extern "C" {
 
 int64_t xs_hip_attention_i8_split(int64_t tokens, int64_t kv_heads, int64_t kv_len) {
     if (tokens <= 0 || kv_heads <= 0 || kv_len <= 0) return 1;
-    // Two workgroups (of four waves) for every CU, each with at least 256 keys.
-    const int64_t groups = tokens * kv_heads;
-    int64_t split = (2 * static_cast<int64_t>(device_cus()) + groups - 1) / groups;
-    const int64_t by_len = kv_len / 256;
+    // A workgroup (of eight waves) for every CU, each wave with at least two tiles of keys.
+    const int hg = heads_per_group(kv_heads, kMaxWaves);
+    const int64_t groups = tokens * (kv_heads / hg);
+    int64_t split = (static_cast<int64_t>(device_cus()) + groups - 1) / groups;
+    const int64_t by_len = kv_len / (2 * kTile * (kMaxWaves / hg));
     if (split > by_len) split = by_len;
     if (split > kMaxSplit) split = kMaxSplit;
     return split < 1 ? 1 : split;
@@ -547,7 +655,7 @@ int xs_hip_attention_i8(void* stream, const float* q, const void* k_codes, const
     AttnArgs a{q, static_cast<const int8_t*>(k_codes), static_cast<const float*>(k_scales),
                static_cast<const int8_t*>(v_codes), static_cast<const float*>(v_scales),
                out, split > 1 ? static_cast<float*>(scratch) : nullptr, tokens, q_heads, kv_heads, head_dim, kv_len,
-               window, scale, softcap, causal ? 1 : 0, static_cast<int>(split)};
+               window, scale, softcap, causal ? 1 : 0, static_cast<int>(split), 1};
     const hipStream_t s = as_stream(stream);
     int rc;
     switch (q_heads / kv_heads) {
@@ -564,8 +672,8 @@ int xs_hip_attention_i8(void* stream, const float* q, const void* k_codes, const
                                                  " query heads per KV head (supported: 1 to 8)");
     }
     if (rc != XS_HIP_OK || split == 1) return rc;
-    attention_combine_rows<<<static_cast<unsigned>(tokens * q_heads), 256, 0, s>>>(
-        static_cast<const float*>(scratch), out, static_cast<int>(split), head_dim);
+    attention_combine_rows<<<static_cast<unsigned>(tokens * q_heads * (head_dim / kCombineDims)), 256, 0, s>>>(
+        static_cast<const float*>(scratch), out, static_cast<int>(split), head_dim, tokens * q_heads);
     return check_launch("xs_hip_attention_i8 (combine)");
 }
 
