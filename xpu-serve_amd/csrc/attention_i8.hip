@@ -56,6 +56,10 @@ __device__ __forceinline__ void key_range(const AttnArgs& a, int64_t t, int64_t&
 // or five to eight query heads a KV head at head_dim 128).
 constexpr int waves_for(int G, int D) { return D * ((G + 3) / 4) <= 128 ? 8 : 4; }
 constexpr int kMaxWaves = 8;
+
+// Buffer resources over raw bytes (word 3: 32-bit data format, no swizzle); loads beyond num_records return zeros.
+constexpr int kBufferFlags = 0x00020000;
+constexpr int kBufferNt = 2;  // the non-temporal hint of a buffer load
 constexpr int kTile = 64;    // keys a wave works on at once (at most 64: one a lane for the scales)
 
 // Merges (m, l, acc) of another key set into this one: the online-softmax combine.
@@ -139,7 +143,7 @@ __global__ __launch_bounds__(64 * waves_for(G, D)) void attention_i8_rows(AttnAr
     static_assert(kWaves * G * MROW * 4 <= kWaves * WAVE_LDS, "the merge rows fit in the tiles' LDS");
     __shared__ __align__(16) uint8_t lds[kWaves * WAVE_LDS];
 
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int c16 = lane & 15;  // the key (score step) or column (weighted-sum step) of this lane
     const int kq = lane >> 4;   // its 16-dim / 16-key / 4-row group
@@ -167,44 +171,45 @@ __global__ __launch_bounds__(64 * waves_for(G, D)) void attention_i8_rows(AttnAr
     const int64_t tiles = (span + kTile - 1) / kTile;
 
     // Loads of one tile into registers: key codes in the score step's B layout, value codes (for LDS), this lane's
-    // key's scales. A tile wholly inside the split addresses its rows from one base; the split's last tile clamps
-    // each key to the split's last.
+    // key's scales. Buffer loads: the tile's rows of this KV head are addressed from one uniform base with 32-bit lane
+    // offsets, and the buffer's extent ends at key k1, so the rows of keys past the split's last read as zeros (their
+    // weights are 0).
     i32x4 kw[KB][KC];
     u32x4 vw[VI];
     float ksv = 0.0f, vsv = 0.0f;
     const int64_t rstride = a.kv_heads * D;  // bytes from one key's row to the next of the same KV head
+    const uint32_t koff = static_cast<uint32_t>(c16 * rstride + kq * 16);
+    const uint32_t voff = static_cast<uint32_t>((lane / VLPR) * rstride + (lane % VLPR) * 16);
+    const uint32_t soff = static_cast<uint32_t>(lane * a.kv_heads * 4);
     auto load_tile = [&](int64_t j0) {
-        if (j0 + kTile - 1 <= k1) {  // uniform
-            const int8_t* kp = a.kc + ((j0 + c16) * a.kv_heads + kvh) * D + kq * 16;
-            const int8_t* vp = a.vc + ((j0 + lane / VLPR) * a.kv_heads + kvh) * D + (lane % VLPR) * 16;
+        const int64_t row0 = j0 * a.kv_heads + kvh;  // (key j0, this KV head)
+        const int64_t rows_left = k1 - j0;           // keys after j0 within the split
+        // Extents past 2^31 - 1 bytes are clamped there: the tile's offsets stay below 64 rows.
+        const int nk = static_cast<int>(rows_left * rstride + D < 0x7fffffff ? rows_left * rstride + D : 0x7fffffff);
+        const int64_t ns64 = (rows_left * a.kv_heads + 1) * 4;
+        const int ns = static_cast<int>(ns64 < 0x7fffffff ? ns64 : 0x7fffffff);
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<int8_t*>(a.kc + row0 * D), 0, nk, kBufferFlags);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<int8_t*>(a.vc + row0 * D), 0, nk, kBufferFlags);
+        const __amdgpu_buffer_rsrc_t rks = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(a.ks + row0), 0, ns, kBufferFlags);
+        const __amdgpu_buffer_rsrc_t rvs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(a.vs + row0), 0, ns, kBufferFlags);
 #pragma unroll
-            for (int b = 0; b < KB; ++b) {
+        for (int b = 0; b < KB; ++b) {
 #pragma unroll
-                for (int c = 0; c < KC; ++c)
-                    kw[b][c] = __builtin_bit_cast(i32x4, ld128_nt(kp + b * 16 * rstride + c * 64));
-            }
-#pragma unroll
-            for (int i = 0; i < VI; ++i) vw[i] = ld128_nt(vp + i * VRPI * rstride);
-        } else {
-#pragma unroll
-            for (int b = 0; b < KB; ++b) {
-                int64_t j = j0 + b * 16 + c16;
-                j = j <= k1 ? j : k1;
-                const int8_t* kp = a.kc + (j * a.kv_heads + kvh) * D + kq * 16;
-#pragma unroll
-                for (int c = 0; c < KC; ++c) kw[b][c] = __builtin_bit_cast(i32x4, ld128_nt(kp + c * 64));
-            }
-#pragma unroll
-            for (int i = 0; i < VI; ++i) {
-                int64_t j = j0 + i * VRPI + lane / VLPR;
-                j = j <= k1 ? j : k1;
-                vw[i] = ld128_nt(a.vc + (j * a.kv_heads + kvh) * D + (lane % VLPR) * 16);
-            }
+            for (int c = 0; c < KC; ++c)
+                kw[b][c] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         rk, static_cast<int>(koff + b * 16 * rstride + c * 64), 0,
+                                                         kBufferNt));
         }
-        const int64_t jl = j0 + lane;
-        const int64_t rk = (jl <= k1 ? jl : k1) * a.kv_heads + kvh;
-        ksv = a.ks[rk];
-        vsv = a.vs[rk];
+#pragma unroll
+        for (int i = 0; i < VI; ++i)
+            vw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rv, static_cast<int>(voff + i * VRPI * rstride), 0, kBufferNt));
+        ksv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rks, static_cast<int>(soff), 0, 0));
+        vsv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rvs, static_cast<int>(soff), 0, 0));
     };
 
     // q as digit rows (the score step's A operand): lane l holds digit l % 4 of head (l % 16) / 4 + 4 ng over dims
@@ -648,6 +653,9 @@ int xs_hip_attention_i8(void* stream, const float* q, const void* k_codes, const
                                        " needs xs_hip_attention_i8_scratch bytes of scratch");
     if (split > kMaxSplit || tokens * kv_heads > 65535)
         return fail(XS_HIP_EUNSUPPORTED, std::string(what) + ": launch too large");
+    if (kv_heads * head_dim >= (int64_t{1} << 24))
+        return fail(XS_HIP_EUNSUPPORTED, std::string(what) + ": key rows of " + std::to_string(kv_heads * head_dim) +
+                                             " bytes (at most 2^24 - 1)");
     if (!aligned16(q) || !aligned16(out) || !aligned16(k_codes) || !aligned16(v_codes) || head_dim % 16 != 0 ||
         (split > 1 && reinterpret_cast<uintptr_t>(scratch) % 16 != 0))
         return fail(XS_HIP_EINVAL, std::string(what) + ": q, out, codes and scratch must be 16-byte aligned and "
