@@ -134,9 +134,9 @@ __global__ __launch_bounds__(64 * waves_for(G, D)) void attention_i8_rows(AttnAr
     constexpr int VLPR = D / 16;           // lanes a value row with 16-byte loads
     constexpr int VRPI = 64 / VLPR;        // value rows one load instruction covers
     constexpr int VI = kTile / VRPI;       // value load instructions a tile
-    constexpr int VT = kTile * VROW;       // bytes of a wave's value tile
+    constexpr int VT = kTile * VROW;       // bytes of a wave's value tile, and of its key tile
     constexpr int PT = NG * 4 * kTile * 4; // bytes of a wave's weight tile: W [NG * 4 heads][kTile keys]
-    constexpr int WAVE_LDS = VT + PT + 2 * kTile * 4;
+    constexpr int WAVE_LDS = 2 * VT + PT + 2 * kTile * 4;
     constexpr int MROW = D + 2;            // a merge row: D sums, max, sum
     static_assert(G >= 1 && G <= 8, "one or two groups of four heads");
     static_assert(kTile == 64, "a weighted-sum step takes the 64 keys of a tile");
@@ -156,7 +156,8 @@ __global__ __launch_bounds__(64 * waves_for(G, D)) void attention_i8_rows(AttnAr
     const int s = blockIdx.x;
 
     uint8_t* const vt = lds + wave * WAVE_LDS;
-    float* const ptile = reinterpret_cast<float*>(vt + VT);  // [NG * 4][kTile]
+    uint8_t* const kt = vt + VT;
+    float* const ptile = reinterpret_cast<float*>(kt + VT);  // [NG * 4][kTile]
     float* const kscale = ptile + NG * 4 * kTile;            // [kTile]
     float* const vscale = kscale + kTile;                    // [kTile]
 
@@ -174,11 +175,10 @@ __global__ __launch_bounds__(64 * waves_for(G, D)) void attention_i8_rows(AttnAr
     // key's scales. Buffer loads: the tile's rows of this KV head are addressed from one uniform base with 32-bit lane
     // offsets, and the buffer's extent ends at key k1, so the rows of keys past the split's last read as zeros (their
     // weights are 0).
-    i32x4 kw[KB][KC];
+    u32x4 kw[VI];
     u32x4 vw[VI];
     float ksv = 0.0f, vsv = 0.0f;
     const int64_t rstride = a.kv_heads * D;  // bytes from one key's row to the next of the same KV head
-    const uint32_t koff = static_cast<uint32_t>(c16 * rstride + kq * 16);
     const uint32_t voff = static_cast<uint32_t>((lane / VLPR) * rstride + (lane % VLPR) * 16);
     const uint32_t soff = static_cast<uint32_t>(lane * a.kv_heads * 4);
     auto load_tile = [&](int64_t j0) {
@@ -197,13 +197,9 @@ __global__ __launch_bounds__(64 * waves_for(G, D)) void attention_i8_rows(AttnAr
         const __amdgpu_buffer_rsrc_t rvs = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<float*>(a.vs + row0), 0, ns, kBufferFlags);
 #pragma unroll
-        for (int b = 0; b < KB; ++b) {
-#pragma unroll
-            for (int c = 0; c < KC; ++c)
-                kw[b][c] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                         rk, static_cast<int>(koff + b * 16 * rstride + c * 64), 0,
-                                                         kBufferNt));
-        }
+        for (int i = 0; i < VI; ++i)
+            kw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rk, static_cast<int>(voff + i * VRPI * rstride), 0, kBufferNt));
 #pragma unroll
         for (int i = 0; i < VI; ++i)
             vw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
@@ -291,14 +287,18 @@ __global__ __launch_bounds__(64 * waves_for(G, D)) void attention_i8_rows(AttnAr
     };
     for (int64_t tile = phase; tile < tiles; tile += np) {
         const int64_t j0 = k0 + tile * kTile;  // keys j0 .. j0 + 63 (those past k1 clamped to it, weights 0)
-        // Stage: value codes and the scales to LDS.
+        // Stage: key and value codes and the scales to LDS.
 #pragma unroll
-        for (int i = 0; i < VI; ++i)
-            *reinterpret_cast<u32x4*>(vt + (i * VRPI + lane / VLPR) * VROW + (lane % VLPR) * 16) = vw[i];
+        for (int i = 0; i < VI; ++i) {
+            const int at = (i * VRPI + lane / VLPR) * VROW + (lane % VLPR) * 16;
+            *reinterpret_cast<u32x4*>(kt + at) = kw[i];
+            *reinterpret_cast<u32x4*>(vt + at) = vw[i];
+        }
         kscale[lane] = ksv;
         vscale[lane] = vsv;
+        wave_sync();
 
-        // Scores, straight from the registers the key codes arrived in.
+        // Scores.
         i32x4 sr[NG][KB];
 #pragma unroll
         for (int ng = 0; ng < NG; ++ng) {
@@ -306,13 +306,17 @@ __global__ __launch_bounds__(64 * waves_for(G, D)) void attention_i8_rows(AttnAr
             for (int b = 0; b < KB; ++b) {
                 i32x4 acc = {0, 0, 0, 0};
 #pragma unroll
-                for (int c = 0; c < KC; ++c) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[ng][c], kw[b][c], acc, 0, 0, 0);
+                for (int c = 0; c < KC; ++c) {
+                    // key 16 b + c16, dims 64 c + 16 kq ..: 16 bytes of its staged row (the rows' 16-byte padding
+                    // spreads the 16 rows one read covers over all banks)
+                    const i32x4 kb = *reinterpret_cast<const i32x4*>(kt + (b * 16 + c16) * VROW + c * 64 + kq * 16);
+                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[ng][c], kb, acc, 0, 0, 0);
+                }
                 sr[ng][b] = acc;
             }
         }
-        // The next tile's loads, into the registers just consumed (uniform branch).
+        // The next tile's loads, into the registers just staged (uniform branch).
         if (tile + np < tiles) load_tile(j0 + np * kTile);
-        wave_sync();
 
         float ksc[KB];
 #pragma unroll
