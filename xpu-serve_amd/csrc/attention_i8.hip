@@ -9,18 +9,16 @@
 // Launcher replaced: sycl_be::attention_rows_quantized with attention_combine (src/backend/sycl/sycl_kernels.h:
 // 238-240), I8 rows (sycl_kv_rows.h:37-69).
 //
-// Layout: one workgroup of four waves per (token, KV head, key split); the G query heads sharing the KV head are
-// handled together, so each key and value row is read once for all of them. Each wave takes every fourth tile of 64
-// consecutive keys of the split: it loads the tile's key codes into LDS and its value codes into registers, whole
-// rows per 128-bit load instruction; then a lane per key computes its key's scores against the G heads (q is the same
-// for every lane: LDS broadcasts), the tile's max per head moves the wave's running max (rescaling the
-// accumulator at most once per tile), and each key's p * v_scale goes to LDS; then each lane accumulates the value
-// rows it loaded, 8 dims each, weighted in f32. The lanes sharing dims add up (they share the running max), and the
-// four waves' (max, sum, accumulator) merge in LDS at the end. With one split the workgroup writes the output; with
-// several it writes partial sums with their (max, sum of exponentials) that a second launch merges (flash decoding).
+// Layout: one workgroup per (token, group of KV heads, key split), one wave per KV head of the group (waves_for and
+// the kernel's comment give the shapes); each wave takes tiles of 64 keys of the split, loads the next tile's key and
+// value rows while it works on the current one, and runs one online softmax for the G query heads of its KV head.
+// Both products (scores and the weighted sum) run on the int8 matrix cores with exact integer dot products. With one
+// split the workgroup writes the output; with several it writes partial sums with their (max, sum of exponentials)
+// that a second launch merges (flash decoding).
 //
-// Accuracy: f32 accumulation where cpu-ref accumulates in f64, and the key scale applied to the dot product rather
-// than to each product -- within the reference's own device tolerance for a quantized cache
+// Accuracy: f32 accumulation where cpu-ref accumulates in f64, the key scale applied to the dot product rather than
+// to each product, and q and the softmax weights taken as 23-bit integers (relative 2^-23 of the head's max |q| and of
+// the tile's largest weight) -- within the reference's own device tolerance for a quantized cache
 // (tests/unit/backend/device_attention.cpp:23-27).
 #include <cmath>
 #include <type_traits>
@@ -116,7 +114,7 @@ __device__ __forceinline__ int pack_bytes(uint32_t w0, uint32_t w1, uint32_t w2,
 // the f32 operand written as three balanced base-256 int8 digits of an integer, so every product is exact:
 //  - scores: S^T [16 rows, 16 keys] = digits of q [16 rows, 64 dims] x key codes^T [64 dims, 16 keys], one 64-dim
 //    chunk at a time. Row 4 g + d holds digit d of head g (q / qs rounded, qs = max |q| / 2^22; row 4 g + 3 is zero),
-//    four heads a step. Lane l holds 16 codes of key l % 16, dims 16 (l / 16) .. -- a plain 16-byte load -- and
+//    four heads a step. Lane l reads 16 codes of key l % 16, dims 16 (l / 16) .., from the staged key tile and
 //    receives rows 4 (l / 16) + r: the three digit sums of head l / 16 and key l % 16, combined in f32.
 //  - the weighted sum: O^T [16 dims, 16 cols] = value codes^T [16 dims, 64 keys] x weight digits [64 keys, 16 cols],
 //    column 4 g + d holding digit d of W = p v_scale / ws for head g (ws = the tile's max p v_scale / 2^22).
