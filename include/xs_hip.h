@@ -272,6 +272,15 @@ int xs_hip_attention_i8(void* stream, const float* q, const void* k_codes, const
 int64_t xs_hip_attention_i8_split(int64_t tokens, int64_t kv_heads, int64_t kv_len);
 size_t xs_hip_attention_i8_scratch(int64_t tokens, int64_t q_heads, int64_t head_dim, int64_t split);
 
+/* ---- Strided copy -------------------------------------------------------------------------------------------- */
+
+/* y[r, :] = x[r, :] for `rows` rows of `row_bytes` bytes, x rows `x_row_stride` bytes apart and y rows `y_row_stride`
+ * apart: a graph Slice on an inner axis, materialized. Replaces sycl_be::slice (sycl_kernels.h:119-120): its
+ * (outer, dim, begin, len, inner) are rows = outer, x + begin * inner * elem, x_row_stride = dim * inner * elem,
+ * row_bytes = len * inner * elem. */
+int xs_hip_copy_rows(void* stream, const void* x, int64_t x_row_stride, void* y, int64_t y_row_stride, int64_t rows,
+                     int64_t row_bytes);
+
 /* ---- Measurement helper -------------------------------------------------------------------------------------- */
 
 /* y = x, `bytes` bytes (a multiple of 16, 16-byte aligned), with the 128-bit streaming loads and stores of the

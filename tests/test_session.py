@@ -1,0 +1,427 @@
+"""The HIP backend (xs::Backend "hip" and its Session) on step graphs.
+
+CPU tests: the graph builders' checks and the backend's refusals (ops it has no kernel for, float KV caches, KV
+values read by anything but attention), which come before any device work. GPU tests: graphs of the path's ops run
+through Session::run and compared with the oracle (oracle/oracle.cpp, the restatement of cpu-ref) evaluating the same
+nodes one by one in graph order -- each fused launch must equal the unfused nodes (f32 within 1e-5 relative, exact
+where the ops are), the int8 KV cache across steps must give what cpu-ref's cache of round-tripped rows gives (the
+reference's device bar for attention), and the session's state must follow Session's contract (num_cached,
+truncate, reset, `only`, a refused step leaving the state as it was).
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+
+import session_api as S
+from oracle import SILU, GELU_TANH, oracle
+from tol import assert_exact, assert_f32_close
+
+
+def _gpu():
+    try:
+        import torch
+        return torch.cuda.is_available()
+    except Exception:
+        return False
+
+
+def step(msg):
+    print(f"[gpu] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def bf16_bits(x):
+    """bf16 bit patterns of f32 values, round to nearest even."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def widen_bf16(bits):
+    return (bits.astype(np.uint32) << 16).view(np.float32)
+
+
+def attention_close(got, want, what, atol=1e-5, rtol=1e-4):
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    ok = err <= atol + rtol * np.abs(want.astype(np.float64))
+    if not ok.all():
+        i = tuple(np.argwhere(~ok)[0])
+        raise AssertionError(f"{what}: {int((~ok).sum())} of {got.size} beyond atol {atol} rtol {rtol}; first at {i}: "
+                             f"got {got[i]!r} want {want[i]!r}")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# CPU: builders and refusals.
+
+def test_backend_registry():
+    assert S.backends() == ["hip"]
+
+
+def test_builder_checks():
+    g = S.Graph()
+    x = g.input("x", S.F32, [S.T, 8])
+    y = g.input("y", S.F32, [S.T, 5])
+    with pytest.raises(S.BackendError, match="cannot broadcast"):
+        g.add(x, y)
+    w = g.constant(np.ones(4, np.float32), S.F32)
+    with pytest.raises(S.BackendError, match="rms_norm weight"):
+        g.rms_norm(x, w)
+    with pytest.raises(S.BackendError, match="topk"):
+        g.topk(x, 9)
+    with pytest.raises(S.BackendError, match="symbolic"):
+        g.slice(x, 0, 0, 2)
+    with pytest.raises(S.BackendError, match="element count"):
+        g.reshape(x, [S.T, 4])
+    with pytest.raises(S.BackendError, match="duplicate graph input"):
+        g.input("x", S.F32, [4])
+    q = g.input("q", S.F32, [S.T, 4, 64])
+    pos = g.input("pos", S.I32, [S.T])
+    with pytest.raises(S.BackendError, match="inv_freq"):
+        g.rope(q, pos, g.constant(np.ones(16, np.float32), S.F32))
+    slot = g.kv_slot(2, 64, label="a")
+    with pytest.raises(S.BackendError, match="expects k, v"):
+        g.kv_cache(slot, q, q)
+
+
+def _refusal(g, match, weights=None, kv=(S.KV_I8, S.KV_I8)):
+    with pytest.raises(S.BackendError, match=match):
+        S.Session(g, weights, kv=kv)
+
+
+def test_refuses_ops_without_kernels():
+    w = S.Weights().add("w", np.ones((4, 8), np.float32))
+    g = S.Graph()
+    x = g.input("x", S.F32, [S.T, 8])
+    g.output("y", g.matmul(x, g.weight(w, "w")))
+    _refusal(g, "MatMul.*not supported", w)
+    g = S.Graph()
+    x = g.input("x", S.F32, [3, 8])
+    g.output("y", g.transpose(x, [1, 0]))
+    _refusal(g, "Transpose.*not supported")
+
+
+def _kv_graph(extra=None):
+    g = S.Graph()
+    q = g.input("q", S.F32, [S.T, 4, 64])
+    k = g.input("k", S.F32, [S.T, 2, 64])
+    v = g.input("v", S.F32, [S.T, 2, 64])
+    slot = g.kv_slot(2, 64, label="layer0")
+    ka, va = g.kv_cache(slot, k, v)
+    o = g.attention(q, ka, va, 0.125)
+    g.output("o", o)
+    if extra:
+        extra(g, ka, va)
+    return g
+
+
+def test_refuses_float_kv_cache():
+    _refusal(_kv_graph(), "KV cache format", kv=(S.KV_FLOAT, S.KV_FLOAT))
+    _refusal(_kv_graph(), "KV cache format", kv=(S.KV_I8, S.KV_FLOAT))
+
+
+def test_refuses_kv_values_outside_attention():
+    _refusal(_kv_graph(lambda g, ka, va: g.output("s", g.softmax(ka))), "read only by attention")
+    _refusal(_kv_graph(lambda g, ka, va: g.output("k_all", ka)), "is a KV cache")
+
+
+def test_refuses_attention_over_computed_keys():
+    g = S.Graph()
+    q = g.input("q", S.F32, [4, 2, 64])
+    k = g.input("k", S.F32, [6, 2, 64])
+    g.output("o", g.attention(q, k, k, 0.125, causal=False))
+    _refusal(g, "one KV slot")
+
+
+def test_graph_validation():
+    g = S.Graph()
+    g.kv_slot(2, 64, label="unused")
+    x = g.input("x", S.F32, [S.T, 4])
+    g.output("y", g.silu(x))
+    _refusal(g, "used 0 times")
+    _refusal(S.Graph(), "no outputs")
+
+
+@pytest.mark.skipif(_gpu(), reason="checks the message of a machine without a GPU")
+def test_needs_a_device():
+    g = S.Graph()
+    g.output("y", g.silu(g.input("x", S.F32, [S.T, 4])))
+    _refusal(g, "device")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# GPU: sessions.
+
+@pytest.fixture(scope="module")
+def ora():
+    return oracle()
+
+
+@pytest.mark.gpu
+def test_swiglu_block(ora):
+    """Mul(Silu(Add(gate, bias)), up) with bf16 gate, up and bias: one act-bias-mul launch; equals cpu-ref's Add,
+    Silu, Mul in f32 on the widened inputs (blocks.cpp:23-27)."""
+    rng = np.random.default_rng(1)
+    t, c = 37, 1000
+    bias = bf16_bits(rng.standard_normal(c) * 0.02)
+    w = S.Weights().add("bias", bias, S.BF16)
+    g = S.Graph()
+    gate = g.input("gate", S.BF16, [S.T, c])
+    up = g.input("up", S.BF16, [S.T, c])
+    g.output("y", g.mul(g.silu(g.add(gate, g.weight(w, "bias"))), up))
+    step("session swiglu block")
+    s = S.Session(g, w)
+    gb = bf16_bits(rng.standard_normal((t, c)))
+    ub = bf16_bits(rng.standard_normal((t, c)))
+    y = s.run({"gate": (gb, S.BF16), "up": (ub, S.BF16)})["y"]
+    want = ora.act_bias_mul(SILU, widen_bf16(gb), widen_bf16(ub), widen_bf16(bias))
+    assert_f32_close(y, want, what="swiglu")
+
+
+@pytest.mark.gpu
+def test_swiglu_gate_up_slices(ora):
+    """The gated MLP over one fused gate|up buffer [T, 2C]: Slice(x, 1, 0, C) and Slice(x, 1, C) feed the
+    act-bias-mul in place (row stride 2C); the unfused nodes' values are the oracle's."""
+    rng = np.random.default_rng(2)
+    t, c = 19, 768
+    g = S.Graph()
+    x = g.input("x", S.F32, [S.T, 2 * c])
+    gate = g.slice(x, 1, 0, c)
+    up = g.slice(x, 1, c)
+    g.output("y", g.mul(g.unary(S.GELU_TANH, gate), up))
+    step("session gate|up slices")
+    s = S.Session(g)
+    xv = rng.standard_normal((t, 2 * c)).astype(np.float32)
+    y = s.run({"x": (xv, S.F32)})["y"]
+    want = ora.binary(1, ora.unary(GELU_TANH, xv[:, :c]), xv[:, c:])
+    assert_f32_close(y, want, what="gelu_tanh(gate) * up")
+
+
+@pytest.mark.gpu
+def test_residual_norm_and_fused_adds(ora):
+    """h = x + r (read again later), y = rms_norm(h, w) in one launch; Add(RmsNorm(h), c); a + (b + c_row);
+    a + b * c; each equal to the oracle's nodes in order."""
+    rng = np.random.default_rng(3)
+    t, d = 9, 2560
+    wv = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    cv = rng.standard_normal(d).astype(np.float32)
+    w = S.Weights().add("w", wv).add("c", cv)
+    g = S.Graph()
+    x = g.input("x", S.F32, [S.T, d])
+    r = g.input("r", S.F32, [S.T, d])
+    b = g.input("b", S.F32, [S.T, d])
+    h = g.add(x, r)
+    y = g.rms_norm(h, g.weight(w, "w"), 1e-6)
+    yb = g.add(g.rms_norm(x, g.weight(w, "w"), 1e-6), g.weight(w, "c"))
+    a3 = g.add(h, g.add(b, g.weight(w, "c")))
+    am = g.add(h, g.mul(b, g.weight(w, "c")))
+    for name, v in (("h", h), ("y", y), ("yb", yb), ("a3", a3), ("am", am)):
+        g.output(name, v)
+    step("session residual + norms")
+    s = S.Session(g, w)
+    xv, rv, bv = (rng.standard_normal((t, d)).astype(np.float32) for _ in range(3))
+    out = s.run({"x": (xv, S.F32), "r": (rv, S.F32), "b": (bv, S.F32)})
+    hv = ora.binary(0, xv, rv)
+    assert_exact(out["h"], hv, "h")
+    assert_f32_close(out["y"], ora.rms_norm(hv, wv, 1e-6), what="rms_norm(h)")
+    assert_f32_close(out["yb"], ora.binary(0, ora.rms_norm(xv, wv, 1e-6), cv), what="rms_norm(x) + c")
+    assert_exact(out["a3"], ora.binary(0, hv, ora.binary(0, bv, cv)), "h + (b + c)")
+    assert_exact(out["am"], ora.binary(0, hv, ora.binary(1, bv, cv)), "h + b * c")
+
+
+@pytest.mark.gpu
+def test_row_ops(ora):
+    """LayerNorm(Add(x, c)), l2_clip, softmax, top-k (1 and 5), reduce_sum over either axis, Div with
+    broadcasting, and the unary family with parameters."""
+    rng = np.random.default_rng(4)
+    t, d = 6, 3000
+    wv, bv, cv = (rng.standard_normal(d).astype(np.float32) for _ in range(3))
+    w = S.Weights().add("w", wv).add("b", bv).add("c", cv)
+    g = S.Graph()
+    x = g.input("x", S.F32, [S.T, d])
+    den = g.input("den", S.F32, [S.T, 1])
+    outs = {
+        "ln": g.layer_norm(g.add(x, g.weight(w, "c")), g.weight(w, "w"), g.weight(w, "b"), 1e-5),
+        "clip": g.l2_clip(x, 3.0),
+        "sm": g.softmax(g.scale(x, 0.125)),
+        "rs0": g.reduce_sum(x, 0),
+        "rs1": g.reduce_sum(x, 1),
+        "div": g.div(x, den),
+        "cap": g.unary(S.SOFTCAP, x, 2.5),
+        "clamp": g.unary(S.CLAMP, x, -0.5, 0.75),
+        "sp": g.unary(S.SOFTPLUS, x),
+    }
+    v1, i1 = g.topk(x, 1)
+    v5, i5 = g.topk(x, 5)
+    outs.update({"v1": v1, "i1": i1, "v5": v5, "i5": i5})
+    for name, v in outs.items():
+        g.output(name, v)
+    step("session row ops")
+    s = S.Session(g, w)
+    xv = rng.standard_normal((t, d)).astype(np.float32)
+    xv[2, 17] = xv[2, 2900] = 9.0  # an exact tie: the lower index first
+    dv = (1 + rng.random((t, 1))).astype(np.float32)
+    out = s.run({"x": (xv, S.F32), "den": (dv, S.F32)})
+    assert_f32_close(out["ln"], ora.layer_norm(xv, wv, bv, 1e-5, shift=cv), what="layer_norm(x + c)")
+    assert_f32_close(out["clip"], ora.l2_clip(xv, 3.0, 1e-6), what="l2_clip")
+    assert_f32_close(out["sm"], ora.softmax(ora.scale(xv, 0.125)), what="softmax")
+    assert_f32_close(out["rs0"], ora.reduce_sum(xv, 0), what="reduce_sum 0")
+    assert_f32_close(out["rs1"], ora.reduce_sum(xv, 1), what="reduce_sum 1")
+    assert_exact(out["div"], ora.binary(2, xv, dv), "x / den")
+    assert_f32_close(out["cap"], ora.unary_op(3, xv, 2.5), what="softcap")
+    assert_exact(out["clamp"], ora.unary_op(7, xv, -0.5, 0.75), "clamp")
+    assert_f32_close(out["sp"], ora.unary_op(6, xv), what="softplus")
+    for k in (1, 5):
+        want_v, want_i = ora.topk(xv, k)
+        assert_exact(out[f"v{k}"], want_v, f"top-{k} values")
+        assert_exact(out[f"i{k}"], want_i, f"top-{k} indices")
+    assert out["i1"][2, 0] == 17
+
+
+@pytest.mark.gpu
+def test_rope_pair_and_views(ora):
+    """Q and K ropes of one positions / inv_freq pair (one launch), f16 inputs, a Reshape view, and a Slice over
+    the heads axis (a copy)."""
+    rng = np.random.default_rng(5)
+    t, hq, hk, d = 11, 8, 2, 128
+    inv = ora.rope_inv_freq(1e6, d, d // 2, d // 2)
+    g = S.Graph()
+    q = g.input("q", S.F16, [S.T, hq * d])
+    k = g.input("k", S.F16, [S.T, hk, d])
+    pos = g.input("pos", S.I64, [S.T])
+    f = g.constant(inv, S.F32)
+    qr = g.rope(g.reshape(q, [S.T, hq, d]), pos, f)
+    kr = g.rope(k, pos, f)
+    g.output("qr", qr)
+    g.output("kr", kr)
+    g.output("q_mid", g.slice(qr, 1, 2, 5))
+    g.output("k_in", k)
+    step("session rope pair")
+    s = S.Session(g)
+    qv = rng.standard_normal((t, hq * d)).astype(np.float16)
+    kv = rng.standard_normal((t, hk, d)).astype(np.float16)
+    pv = (np.arange(t) * 37 + 5).astype(np.int64)
+    out = s.run({"q": (qv, S.F16), "k": (kv, S.F16), "pos": (pv, S.I64)})
+    want_q = ora.rope(qv.astype(np.float32).reshape(t, hq, d), pv, inv)
+    want_k = ora.rope(kv.astype(np.float32), pv, inv)
+    assert_f32_close(out["qr"], want_q, what="rope q")
+    assert_f32_close(out["kr"], want_k, what="rope k")
+    assert_f32_close(out["q_mid"], want_q[:, 2:5], what="slice of heads")
+    assert_exact(out["k_in"], kv.astype(np.float32), "f16 input passed through as f32")
+
+
+def _kv_programs(hq, hkv, d, window=0, softcap=0.0):
+    prefill = S.Graph()
+    q = prefill.input("q", S.F32, [S.T, hq, d])
+    k = prefill.input("k", S.F32, [S.T, hkv, d])
+    v = prefill.input("v", S.F32, [S.T, hkv, d])
+    slot = prefill.kv_slot(hkv, d, window, label="layer0")
+    ka, va = prefill.kv_cache(slot, k, v)
+    prefill.output("o", prefill.attention(q, ka, va, 1 / math.sqrt(d), window, softcap))
+    reader = S.Graph()
+    q2 = reader.input("q", S.F32, [S.T, hq, d])
+    slot2 = reader.kv_slot(hkv, d, window, label="layer0")
+    kr, vr = reader.kv_read(slot2)
+    reader.output("o", reader.attention(q2, kr, vr, 1 / math.sqrt(d), window, softcap))
+    return prefill, reader
+
+
+class _Cache:
+    """cpu-ref's cache of round-tripped rows (cpu_backend.cpp:529-544) on the oracle."""
+
+    def __init__(self, ora, hkv, d):
+        self.ora, self.k, self.v = ora, np.zeros((0, hkv, d), np.float32), np.zeros((0, hkv, d), np.float32)
+
+    def rt(self, x):
+        n, h, d = x.shape
+        codes, scales = self.ora.quantize_kv(x.reshape(n * h, d))
+        return self.ora.dequantize_kv(codes, scales).reshape(n, h, d)
+
+    def append(self, k, v):
+        self.k = np.concatenate([self.k, self.rt(k)])
+        self.v = np.concatenate([self.v, self.rt(v)])
+
+    def truncate(self, n):
+        self.k, self.v = self.k[:n], self.v[:n]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("hq,hkv,d,window,softcap", [(32, 8, 128, 0, 0.0), (12, 4, 64, 5, 0.0), (4, 1, 256, 0, 30.0)])
+def test_kv_decode_steps(ora, hq, hkv, d, window, softcap):
+    """A prefill step, decode steps, truncate and reset over the int8 KV slot; a second program reading the slot
+    (KvRead) sees what the first wrote."""
+    rng = np.random.default_rng(6 + d)
+    prefill, reader = _kv_programs(hq, hkv, d, window, softcap)
+    step(f"session kv steps H{hq}/{hkv} D{d} w{window} cap{softcap}")
+    s = S.Session([prefill, reader], max_context=64)
+    cache = _Cache(ora, hkv, d)
+    scale = 1 / math.sqrt(d)
+
+    def one(tokens, program=0):
+        q = rng.standard_normal((tokens, hq, d)).astype(np.float32)
+        inputs = {"q": (q, S.F32)}
+        if program == 0:
+            k = rng.standard_normal((tokens, hkv, d)).astype(np.float32)
+            v = rng.standard_normal((tokens, hkv, d)).astype(np.float32)
+            inputs.update({"k": (k, S.F32), "v": (v, S.F32)})
+            cache.append(k, v)
+        o = s.run(inputs, program=program)["o"]
+        want = ora.attention(q, cache.k, cache.v, scale, softcap, window, True)
+        attention_close(o, want, f"program {program}, {tokens} tokens at L {len(cache.k)}")
+
+    one(7)
+    for _ in range(3):
+        one(1)
+    assert s.num_cached() == 10 and s.num_cached(1) == 0
+    one(2, program=1)  # reads L = 10 without appending
+    assert s.num_cached() == 10
+    s.truncate(6)
+    cache.truncate(6)
+    one(1)
+    one(3)
+    assert s.num_cached() == 10
+    s.reset()
+    cache.truncate(0)
+    assert s.num_cached() == 0
+    one(4)
+
+
+@pytest.mark.gpu
+def test_refused_step_keeps_state(ora):
+    prefill, _ = _kv_programs(4, 2, 64)
+    step("session overflow")
+    s = S.Session(prefill, max_context=8)
+    rng = np.random.default_rng(7)
+
+    def inputs(t):
+        return {n: (rng.standard_normal((t, h, 64)).astype(np.float32), S.F32) for n, h in (("q", 4), ("k", 2), ("v", 2))}
+
+    s.run(inputs(6))
+    with pytest.raises(S.BackendError, match="max_context"):
+        s.run(inputs(3))
+    assert s.num_cached() == 6
+    with pytest.raises(S.BackendError, match="input 'k'"):
+        s.run({"q": inputs(1)["q"], "k": (np.zeros((1, 3, 64), np.float32), S.F32), "v": inputs(1)["v"]})
+    assert s.num_cached() == 6
+    s.run(inputs(2))
+    assert s.num_cached() == 8
+
+
+@pytest.mark.gpu
+def test_only_outputs(ora):
+    """`only` returns just the named outputs and skips what nothing named needs."""
+    rng = np.random.default_rng(8)
+    g = S.Graph()
+    x = g.input("x", S.F32, [S.T, 4096])
+    g.output("top", g.topk(x, 1)[1])
+    g.output("probs", g.softmax(x))
+    step("session only")
+    s = S.Session(g)
+    xv = rng.standard_normal((3, 4096)).astype(np.float32)
+    out = s.run({"x": (xv, S.F32)}, only=["top"])
+    assert list(out) == ["top"]
+    assert_exact(out["top"], ora.topk(xv, 1)[1], "argmax")
+    with pytest.raises(S.BackendError, match="no output 'nope'"):
+        s.run({"x": (xv, S.F32)}, only=["nope"])
+    both = s.run({"x": (xv, S.F32)})
+    assert sorted(both) == ["probs", "top"]

@@ -64,6 +64,17 @@ __global__ __launch_bounds__(kBlock) void copy_kernel(const u32x4* __restrict__ 
     if (i < n) st128_nt(y + i, ld128_nt(x + i));
 }
 
+// y[r, :] = x[r, :] for rows of `cols` elements of type E, rows `xs` / `ys` bytes apart: grid (column tiles, row
+// groups), each workgroup walking its rows gridDim.y apart.
+template <typename E>
+__global__ __launch_bounds__(kBlock) void copy_rows_kernel(const char* __restrict__ x, int64_t xs, char* __restrict__ y,
+                                                           int64_t ys, int64_t rows, int64_t cols) {
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (c >= cols) return;
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y)
+        reinterpret_cast<E*>(y + r * ys)[c] = reinterpret_cast<const E*>(x + r * xs)[c];
+}
+
 }  // namespace
 
 }  // namespace xs_hip
@@ -247,6 +258,36 @@ int xs_hip_graph_destroy(void* graph_exec) {
     return graph_exec == nullptr ? XS_HIP_OK
                                  : check_hip(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)),
                                              "hipGraphExecDestroy");
+}
+
+int xs_hip_copy_rows(void* stream, const void* x, int64_t x_row_stride, void* y, int64_t y_row_stride, int64_t rows,
+                     int64_t row_bytes) {
+    if (rows < 0 || row_bytes < 0 || x_row_stride < row_bytes || y_row_stride < row_bytes)
+        return fail(XS_HIP_EINVAL, "xs_hip_copy_rows: " + std::to_string(rows) + " rows of " +
+                                       std::to_string(row_bytes) + " bytes with strides " +
+                                       std::to_string(x_row_stride) + ", " + std::to_string(y_row_stride));
+    if (rows == 0 || row_bytes == 0) return XS_HIP_OK;
+    if (x == nullptr || y == nullptr) return fail(XS_HIP_EINVAL, "xs_hip_copy_rows: null buffer");
+    // The widest element that divides the row, both strides and both addresses.
+    const uint64_t bits = static_cast<uint64_t>(row_bytes) | static_cast<uint64_t>(x_row_stride) |
+                          static_cast<uint64_t>(y_row_stride) | reinterpret_cast<uintptr_t>(x) |
+                          reinterpret_cast<uintptr_t>(y);
+    const int64_t e = bits % 16 == 0 ? 16 : bits % 8 == 0 ? 8 : bits % 4 == 0 ? 4 : bits % 2 == 0 ? 2 : 1;
+    const int64_t cols = row_bytes / e;
+    const int64_t col_blocks = (cols + kBlock - 1) / kBlock;
+    if (col_blocks > 0x7fffffffLL) return fail(XS_HIP_EUNSUPPORTED, "xs_hip_copy_rows: rows too long");
+    const dim3 grid(static_cast<unsigned>(col_blocks), static_cast<unsigned>(rows < 65535 ? rows : 65535));
+    const hipStream_t s = as_stream(stream);
+    const char* xc = static_cast<const char*>(x);
+    char* yc = static_cast<char*>(y);
+    switch (e) {
+        case 16: copy_rows_kernel<u32x4><<<grid, kBlock, 0, s>>>(xc, x_row_stride, yc, y_row_stride, rows, cols); break;
+        case 8: copy_rows_kernel<uint64_t><<<grid, kBlock, 0, s>>>(xc, x_row_stride, yc, y_row_stride, rows, cols); break;
+        case 4: copy_rows_kernel<uint32_t><<<grid, kBlock, 0, s>>>(xc, x_row_stride, yc, y_row_stride, rows, cols); break;
+        case 2: copy_rows_kernel<uint16_t><<<grid, kBlock, 0, s>>>(xc, x_row_stride, yc, y_row_stride, rows, cols); break;
+        default: copy_rows_kernel<uint8_t><<<grid, kBlock, 0, s>>>(xc, x_row_stride, yc, y_row_stride, rows, cols); break;
+    }
+    return check_launch("xs_hip_copy_rows");
 }
 
 int xs_hip_copy(void* stream, const void* x, void* y, size_t bytes) {

@@ -105,6 +105,7 @@ _SIGS = {
     "xs_hip_quantize_kv": [_P, _INT, _INT, _P, _P, _P, _I64, _I64],
     "xs_hip_dequantize_kv": [_P, _INT, _P, _P, _INT, _P, _I64, _I64],
     "xs_hip_copy": [_P, _P, _P, C.c_size_t],
+    "xs_hip_copy_rows": [_P, _P, _I64, _P, _I64, _I64, _I64],
     "xs_hip_attention_i8": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _F, _I64, _INT, _I64, _P],
     "xs_hip_attention_i8_split": [_I64, _I64, _I64],
     "xs_hip_attention_i8_scratch": [_I64, _I64, _I64, _I64],
