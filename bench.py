@@ -349,6 +349,43 @@ def op_kv_dequantize(inputs):
               "dequantize_i8_vec")
 
 
+def op_kv_turbo(inputs, decode=False):
+    """Config 4's K and V as turbo4 (codes and f16 norms per 128 values), or decoded back to f16 (still rotated)."""
+    rows, dim, k0, v0 = inputs
+    groups = rows * dim // 128
+    name = "kv_turbo4_dequantize" if decode else "kv_turbo4_quantize"
+    if decode:
+        kc0, kn0 = X.turbo_quantize(k0, 4)
+        vc0, vn0 = X.turbo_quantize(v0, 4)
+
+    def mk():
+        if decode:
+            s = (dcopy(kc0), dcopy(kn0), dcopy(vc0), dcopy(vn0), X.DeviceTensor.empty(X.F16, (rows, dim)),
+                 X.DeviceTensor.empty(X.F16, (rows, dim)))
+        else:
+            s = (dcopy(k0), dcopy(v0), X.DeviceTensor.empty(X.U8, (groups, 64)), X.DeviceTensor.empty(X.F16, (groups,)),
+                 X.DeviceTensor.empty(X.U8, (groups, 64)), X.DeviceTensor.empty(X.F16, (groups,)))
+        if decode:
+            need(s[0], groups * 64, "turbo4 codes")
+            need(s[4], rows * dim * 2, "turbo4 out")
+        else:
+            need(s[0], rows * dim * 2, "turbo4 k")
+            need(s[2], groups * 64, "turbo4 codes")
+        return s
+
+    def go(s, stream):
+        if decode:
+            kc, kn, vc, vn, ko, vo = s
+            X.call("xs_hip_dequantize_kv", stream, X.KV_TURBO4, vp(kc), vp(kn), X.F16, vp(ko), rows, dim)
+            X.call("xs_hip_dequantize_kv", stream, X.KV_TURBO4, vp(vc), vp(vn), X.F16, vp(vo), rows, dim)
+        else:
+            k, v, kc, kn, vc, vn = s
+            X.call("xs_hip_quantize_kv", stream, X.KV_TURBO4, X.F16, vp(k), vp(kc), vp(kn), rows, dim)
+            X.call("xs_hip_quantize_kv", stream, X.KV_TURBO4, X.F16, vp(v), vp(vc), vp(vn), rows, dim)
+    return Op(name, W.ALGO_BYTES[name], W.ALGO_BYTES[name], mk, go, 2,
+              "turbo_decode_kernel" if decode else "turbo_quantize_kernel")
+
+
 def op_attention_i8(inputs):
     """One decode step (1 query token, 32 query heads) over the int8 cache of config 4's K and V."""
     rows, dim, k0, v0 = inputs
@@ -393,7 +430,7 @@ def op_copy(n=256 << 20):
 
 OP_ORDER = ["swiglu_bias", "swiglu_bias_strided", "rmsnorm_residual", "softmax_masked", "argmax", "rope_qk",
             "rope_qk_separate", "kv_quantize", "kv_dequantize", "attention_i8_decode", "layer_norm", "l2_clip",
-            "reduce_sum_rows", "reduce_sum_cols", "unary_softcap"]
+            "reduce_sum_rows", "reduce_sum_cols", "unary_softcap", "kv_turbo4_quantize", "kv_turbo4_dequantize"]
 
 
 def build_ops(only):
@@ -401,7 +438,8 @@ def build_ops(only):
     names = OP_ORDER if only is None else [n for n in OP_ORDER + ["copy"] if n in only]
     kv = None
     for name in names:
-        if name in ("kv_quantize", "kv_dequantize", "attention_i8_decode") and kv is None:
+        if name in ("kv_quantize", "kv_dequantize", "attention_i8_decode", "kv_turbo4_quantize",
+                    "kv_turbo4_dequantize") and kv is None:
             kv = _kv_inputs()
         yield {"swiglu_bias": op_swiglu, "swiglu_bias_strided": op_swiglu_strided, "rmsnorm_residual": op_rmsnorm,
                "softmax_masked": op_softmax, "argmax": op_argmax, "rope_qk": op_rope,
@@ -410,7 +448,8 @@ def build_ops(only):
                "attention_i8_decode": lambda: op_attention_i8(kv), "unary_softcap": op_unary_softcap,
                "layer_norm": lambda: op_row_norms("layer_norm"), "l2_clip": lambda: op_row_norms("l2_clip"),
                "reduce_sum_rows": lambda: op_row_norms("reduce_sum_rows"),
-               "reduce_sum_cols": lambda: op_row_norms("reduce_sum_cols")}[name]()
+               "reduce_sum_cols": lambda: op_row_norms("reduce_sum_cols"),
+               "kv_turbo4_quantize": lambda: op_kv_turbo(kv), "kv_turbo4_dequantize": lambda: op_kv_turbo(kv, True)}[name]()
 
 
 # ---------------------------------------------------------------------------------------------------------------

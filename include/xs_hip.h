@@ -238,17 +238,28 @@ int xs_hip_rope2(void* stream, xs_dtype x_dtype, const void* xa, void* ya, int64
 
 /* ---- int8 KV cache ------------------------------------------------------------------------------------------- */
 
-/* Codes and scales of x [rows, width] (x_dtype F32, F16 or BF16): per row amax = max |x|, inv = 127 / amax (f32,
- * correctly rounded; 0 for an all-zero row), code = clamp(round-half-even(x * inv), -127, 127), scale = amax / 127.
- * codes int8 [rows, width], scales f32 [rows] (kv_row_bytes I8, src/quant/kv_format.cpp:47-48). Replaces
- * sycl_be::quantize_kv (sycl_kernels.h:213-214); semantics quant::quantize_kv_row_i8 (src/quant/quant.cpp:259-267).
- * Only XS_KV_I8. */
+/* Codes and scales of x [rows, width] (x_dtype F32, F16 or BF16), by format. Replaces sycl_be::quantize_kv
+ * (sycl_kernels.h:213-214).
+ * XS_KV_I8: per row amax = max |x|, inv = 127 / amax (f32, correctly rounded; 0 for an all-zero row),
+ *   code = clamp(round-half-even(x * inv), -127, 127), scale = amax / 127; codes int8 [rows, width], scales f32 [rows]
+ *   (kv_row_bytes I8, src/quant/kv_format.cpp:47-48); semantics quant::quantize_kv_row_i8 (src/quant/quant.cpp:259-267).
+ * XS_KV_TURBO4 / TURBO3 / TURBO2: width a multiple of 128; each group of 128 values rotated (sign flips, Walsh-Hadamard,
+ *   sign flips) and each coordinate rounded to the nearest of 16 / 8 / 4 centroids; codes [rows * width / 128,
+ *   16 * bits] bytes in the group layout of kv_turbo.h:84-87 and `scales` as f16 norms [rows * width / 128] (2-byte
+ *   aligned); the same bits as quant::turbo::quantize_group (src/quant/kv_turbo.cpp:47-84). x 16-byte aligned. */
 int xs_hip_quantize_kv(void* stream, xs_kv_format format, xs_dtype x_dtype, const void* x, void* codes, void* scales,
                        int64_t rows, int64_t width);
-/* out [rows, width] (F32, F16 or BF16) = fl32(code * scale[row]) rounded to out's dtype: quant::round_trip_kv_i8
- * (quant.cpp:269-277). Replaces sycl_be::dequantize_kv (sycl_kernels.h:217-218). Only XS_KV_I8. */
+/* out [rows, width] (F32, F16 or BF16) = the values the codes store, rounded to out's dtype. Replaces
+ * sycl_be::dequantize_kv (sycl_kernels.h:217-218). XS_KV_I8: fl32(code * scale[row]), quant::round_trip_kv_i8
+ * (quant.cpp:269-277). TurboQuant: centroid(code) * norm per group, still rotated (quant::turbo::decode_group,
+ * kv_turbo.cpp:86-91; xs_hip_kv_rotate rotates back); out 16-byte aligned. */
 int xs_hip_dequantize_kv(void* stream, xs_kv_format format, const void* codes, const void* scales, xs_dtype out_dtype,
                          void* out, int64_t rows, int64_t width);
+
+/* y [rows, width] = x with each group of 128 values rotated as the TurboQuant formats rotate a row (inverse = 0), or
+ * rotated back (inverse = 1); f32, 16-byte aligned, y may be x. Replaces sycl_be::kv_rotate (sycl_kernels.h:219-221);
+ * semantics quant::turbo::rotate_group (kv_turbo.cpp:118-129). */
+int xs_hip_kv_rotate(void* stream, const float* x, float* y, int64_t rows, int64_t width, int inverse);
 
 /* ---- Attention over the int8 KV cache ------------------------------------------------------------------------ */
 

@@ -285,6 +285,12 @@ void dequantize_kv(Stream q, const KvStream& s, CT* out, int64_t rows, int64_t w
                   "dequantize_kv");
 }
 
+// y [rows, width] = x with each group of 128 values rotated as the TurboQuant formats rotate a row, or rotated back
+// (sycl_kernels.h:219-221).
+inline void kv_rotate(Stream q, const float* x, float* y, int64_t rows, int64_t width, bool inverse) {
+    detail::check(xs_hip_kv_rotate(q, x, y, rows, width, inverse ? 1 : 0), "kv_rotate");
+}
+
 // ---- Attention over the quantized KV cache -------------------------------------------------------------------------
 
 struct KvQuantized {  // sycl_kernels.h:206-208

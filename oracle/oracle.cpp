@@ -29,6 +29,10 @@
 //                              interleaved-layout control (tests/unit/backend/cpu_ops.cpp:228-251); goldens
 //   ora_rope_inv_freq          goldens of blocks::rope_inv_freq; closed form theta^(-2i/d) at exact powers
 //   ora_quantize_kv_*          |code| <= 127, round-trip error <= scale / 2, zero rows, goldens (bit-exact)
+//   ora_turbo_*                the reference's own fixtures (tests/fixtures/quant/turbo: codes and f16 norm of 43 rows
+//                              at 4, 3 and 2 bits, from the format's published implementation), nearest-centroid and
+//                              norm-restoring invariants, the rotation's orthogonality and inverse, an f64 WHT by the
+//                              Hadamard matrix, the compiled reference (oracle/_ref)
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
@@ -502,6 +506,166 @@ void ora_quantize_kv(const float* x, int8_t* codes, float* scales, int64_t rows,
 void ora_dequantize_kv(const int8_t* codes, const float* scales, float* out, int64_t rows, int64_t width) {
     for (int64_t r = 0; r < rows; ++r)
         for (int64_t i = 0; i < width; ++i) out[r * width + i] = static_cast<float>(codes[r * width + i]) * scales[r];
+}
+
+}  // extern "C"
+
+// ---- TurboQuant KV formats: src/quant/kv_turbo.h:14-105, src/quant/kv_turbo.cpp:9-144 ------------------------------
+//
+// A group of 128 values: n = its sum of squares (8-value lanes fused-multiply-added in order, the 16 lane sums added
+// pairwise 1, 2, 4, 8 lanes apart); w = the values sign-flipped, Walsh-Hadamard transformed (unnormalized butterflies
+// of spans 1 .. 64), sign-flipped again; code = sign and the count of edges e_j with w^2 >= e_j^2 * 128 * n (> for a
+// negative w); norm = f16(sqrt(n / r)), r = the chosen magnitudes' squares summed like n with plain adds (0 when n is
+// 0). Decoding gives centroid * norm, still rotated; the rotation is orthogonal with the 1 / sqrt(128) folded in.
+
+namespace {
+namespace turbo {
+
+constexpr int kGroup = 128;
+constexpr int kLanes = 16;
+constexpr int kLaneValues = 8;
+constexpr uint64_t kSignsBefore[2] = {0x42f85949e46a0359ull, 0x49f250a9a4c63bbbull};  // kv_turbo.h:27
+constexpr uint64_t kSignsAfter[2] = {0x3f628fdc16acee90ull, 0xbea56562b7a5357aull};   // kv_turbo.h:28
+// Lloyd-Max magnitudes of a Gaussian of variance 1 / 128 and the borders between them (kv_turbo.h:39-56).
+constexpr float kMags2[2] = {0.039994f, 0.133462f};
+constexpr float kEdges2[1] = {0.086728f};
+constexpr float kMags3[4] = {0.021663f, 0.066822f, 0.118786f, 0.190207f};
+constexpr float kEdges3[3] = {0.044243f, 0.092804f, 0.154496f};
+constexpr float kMags4[8] = {0.011349f, 0.034299f, 0.058050f, 0.083292f, 0.111036f, 0.143016f, 0.182877f, 0.241529f};
+constexpr float kEdges4[7] = {0.022824f, 0.046174f, 0.070671f, 0.097164f, 0.127026f, 0.162947f, 0.212203f};
+
+const float* mags(int bits) { return bits == 4 ? kMags4 : bits == 3 ? kMags3 : kMags2; }
+const float* edges(int bits) { return bits == 4 ? kEdges4 : bits == 3 ? kEdges3 : kEdges2; }
+int group_bytes(int bits) { return kGroup * bits / 8; }
+bool flipped(const uint64_t* signs, int i) { return ((signs[i / 64] >> (i % 64)) & 1u) != 0; }
+
+// Pairwise over lanes 1, 2, 4, 8 apart (every lane ends with the same sum).
+float sum_lanes(float* lane) {
+    for (int m = 1; m < kLanes; m <<= 1) {
+        float next[kLanes];
+        for (int l = 0; l < kLanes; ++l) next[l] = lane[l] + lane[l ^ m];
+        std::memcpy(lane, next, sizeof(next));
+    }
+    return lane[0];
+}
+
+void butterflies(float* x) {
+    for (int h = 1; h < kGroup; h *= 2)
+        for (int i = 0; i < kGroup; i += 2 * h)
+            for (int j = i; j < i + h; ++j) {
+                const float a = x[j], b = x[j + h];
+                x[j] = a + b;
+                x[j + h] = a - b;
+            }
+}
+
+// Code c of a magnitude index m: the upper half of the codes positive, ascending (kv_turbo.h:63-66).
+uint32_t code_of(int bits, bool negative, uint32_t m) {
+    const uint32_t half = 1u << (bits - 1);
+    return negative ? half - 1 - m : half + m;
+}
+
+float centroid(int bits, uint32_t code) {
+    const uint32_t half = 1u << (bits - 1);
+    return code >= half ? mags(bits)[code - half] : -mags(bits)[half - 1 - code];
+}
+
+// Packing (kv_turbo.h:84-87; kv_turbo.cpp:38-45, 104-109).
+void put_code(uint8_t* codes, int bits, int i, uint32_t code) {
+    if (bits == 4) {
+        codes[i / 2] |= static_cast<uint8_t>(code << (4 * (i % 2)));
+        return;
+    }
+    codes[i / 4] |= static_cast<uint8_t>((code & 3u) << (2 * (i % 4)));
+    if (bits == 3) codes[kGroup / 4 + i / 8] |= static_cast<uint8_t>((code >> 2) << (i % 8));
+}
+
+uint32_t code_at(const uint8_t* codes, int bits, int i) {
+    if (bits == 4) return (codes[i / 2] >> (4 * (i % 2))) & 15u;
+    const uint32_t low = (codes[i / 4] >> (2 * (i % 4))) & 3u;
+    if (bits == 2) return low;
+    return low | (((codes[kGroup / 4 + i / 8] >> (i % 8)) & 1u) << 2);
+}
+
+// quant::turbo::quantize_group (kv_turbo.cpp:47-84).
+uint16_t quantize_group(const float* x, int bits, uint8_t* codes) {
+    float lane[kLanes];
+    for (int l = 0; l < kLanes; ++l) {
+        float s = 0.0f;
+        for (int e = 0; e < kLaneValues; ++e) s = std::fma(x[l * kLaneValues + e], x[l * kLaneValues + e], s);
+        lane[l] = s;
+    }
+    const float n = sum_lanes(lane);
+    float w[kGroup];
+    for (int i = 0; i < kGroup; ++i) w[i] = flipped(kSignsBefore, i) ? -x[i] : x[i];
+    butterflies(w);
+    const int nm = 1 << (bits - 1);
+    float edge[7];
+    for (int j = 0; j < nm - 1; ++j) {
+        const double e = edges(bits)[j];
+        edge[j] = static_cast<float>(e * e * kGroup) * n;  // edge_sq(j) * n (kv_turbo.h:57-62)
+    }
+    std::memset(codes, 0, static_cast<size_t>(group_bytes(bits)));
+    float chosen[kGroup];
+    for (int i = 0; i < kGroup; ++i) {
+        const float v = flipped(kSignsAfter, i) ? -w[i] : w[i];
+        const bool negative = v < 0.0f;
+        const float sq = v * v;
+        uint32_t m = 0;
+        for (int j = 0; j < nm - 1; ++j) m += (negative ? sq > edge[j] : sq >= edge[j]) ? 1u : 0u;
+        put_code(codes, bits, i, code_of(bits, negative, m));
+        chosen[i] = mags(bits)[m] * mags(bits)[m];
+    }
+    for (int l = 0; l < kLanes; ++l) {
+        float s = 0.0f;
+        for (int e = 0; e < kLaneValues; ++e) s += chosen[l * kLaneValues + e];
+        lane[l] = s;
+    }
+    const float r = sum_lanes(lane);
+    return f32_to_f16(n > 0.0f ? std::sqrt(n / r) : 0.0f);
+}
+
+// quant::turbo::rotate_group (kv_turbo.cpp:118-129).
+void rotate_group(float* x, bool inverse) {
+    const uint64_t* first = inverse ? kSignsAfter : kSignsBefore;
+    const uint64_t* last = inverse ? kSignsBefore : kSignsAfter;
+    for (int i = 0; i < kGroup; ++i) x[i] = flipped(first, i) ? -x[i] : x[i];
+    butterflies(x);
+    for (int i = 0; i < kGroup; ++i) {
+        const float y = x[i] * 0.08838834764831845f;
+        x[i] = flipped(last, i) ? -y : y;
+    }
+}
+
+}  // namespace turbo
+}  // namespace
+
+extern "C" {
+
+// Codes [groups, 128 * bits / 8] and f16 norms [groups] of x [groups, 128] (quant::turbo::quantize_group).
+void ora_turbo_quantize(const float* x, int64_t groups, int bits, uint8_t* codes, uint16_t* norms) {
+    for (int64_t g = 0; g < groups; ++g)
+        norms[g] = turbo::quantize_group(x + g * turbo::kGroup, bits, codes + g * turbo::group_bytes(bits));
+}
+
+// The rotated values the groups store, centroid * norm (quant::turbo::decode_group, kv_turbo.cpp:86-91).
+void ora_turbo_decode(const uint8_t* codes, const uint16_t* norms, int64_t groups, int bits, float* out) {
+    for (int64_t g = 0; g < groups; ++g) {
+        const float scale = f16_to_f32(norms[g]);
+        for (int i = 0; i < turbo::kGroup; ++i)
+            out[g * turbo::kGroup + i] =
+                turbo::centroid(bits, turbo::code_at(codes + g * turbo::group_bytes(bits), bits, i)) * scale;
+    }
+}
+
+// Each group of 128 values rotated, or rotated back, in place (quant::turbo::rotate_group).
+void ora_turbo_rotate(float* x, int64_t groups, int inverse) {
+    for (int64_t g = 0; g < groups; ++g) turbo::rotate_group(x + g * turbo::kGroup, inverse != 0);
+}
+
+// The value each code names: 1 << bits entries (kv_turbo.h:68-80, the Tables' centroids).
+void ora_turbo_centroids(int bits, float* out) {
+    for (uint32_t c = 0; c < (1u << bits); ++c) out[c] = turbo::centroid(bits, c);
 }
 
 }  // extern "C"

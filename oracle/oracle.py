@@ -32,6 +32,7 @@ GELU_TANH, SIGMOID, SILU, GELU = 2, 4, 5, 8
 _fp = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _u16 = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
 _i8 = np.ctypeslib.ndpointer(dtype=np.int8, flags="C_CONTIGUOUS")
+_u8 = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
 _i32 = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
 _i64 = np.ctypeslib.ndpointer(dtype=np.int64, flags="C_CONTIGUOUS")
 _P = C.c_void_p
@@ -66,7 +67,37 @@ class _Base:
         return out.view(np.float16) if dtype == F16 else out
 
 
-class Oracle(_Base):
+class _Turbo:
+    """TurboQuant groups (src/quant/kv_turbo.{h,cpp}) through `_tq`, `_td`, `_tr` of the library."""
+
+    def turbo_quantize(self, x, bits):
+        """x [..., 128k] f32 -> codes uint8 [groups, 16 bits] and f16 norm bits uint16 [groups]."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, 128)
+        codes = np.zeros((x.shape[0], 16 * bits), np.uint8)
+        norms = np.zeros(x.shape[0], np.uint16)
+        self._tq(x, x.shape[0], bits, codes, norms)
+        return codes, norms
+
+    def turbo_decode(self, codes, norms, bits):
+        """The rotated values the groups store, f32 [groups, 128]."""
+        codes = np.ascontiguousarray(codes, np.uint8).reshape(-1, 16 * bits)
+        norms = np.ascontiguousarray(norms, np.uint16)
+        out = np.empty((codes.shape[0], 128), np.float32)
+        self._td(codes, norms, codes.shape[0], bits, out)
+        return out
+
+    def turbo_rotate(self, x, inverse=False):
+        y = np.ascontiguousarray(x, np.float32).reshape(-1, 128).copy()
+        self._tr(y, y.shape[0], int(inverse))
+        return y.reshape(np.shape(x))
+
+    def turbo_round_trip(self, x, bits):
+        """quant::turbo::round_trip: each row's groups replaced by what they store, rotated back."""
+        codes, norms = self.turbo_quantize(x, bits)
+        return self.turbo_rotate(self.turbo_decode(codes, norms, bits), inverse=True).reshape(np.shape(x))
+
+
+class Oracle(_Base, _Turbo):
     """The restatement (oracle/oracle.cpp)."""
 
     def __init__(self, path: str = ORACLE_LIB):
@@ -104,7 +135,25 @@ class Oracle(_Base):
         L.ora_quantize_kv_row_i8.restype = C.c_float
         L.ora_quantize_kv.argtypes = [_fp, _i8, _fp, _L, _L]
         L.ora_dequantize_kv.argtypes = [_i8, _fp, _fp, _L, _L]
+        L.ora_turbo_quantize.argtypes = [_fp, _L, C.c_int, _u8, _u16]
+        L.ora_turbo_decode.argtypes = [_u8, _u16, _L, C.c_int, _fp]
+        L.ora_turbo_rotate.argtypes = [_fp, _L, C.c_int]
+        L.ora_turbo_centroids.argtypes = [C.c_int, _fp]
         self.lib = L
+
+    def _tq(self, *a):
+        self.lib.ora_turbo_quantize(*a)
+
+    def _td(self, *a):
+        self.lib.ora_turbo_decode(*a)
+
+    def _tr(self, *a):
+        self.lib.ora_turbo_rotate(*a)
+
+    def turbo_centroids(self, bits):
+        out = np.empty(1 << bits, np.float32)
+        self.lib.ora_turbo_centroids(bits, out)
+        return out
 
     def _widen(self, dtype, x, out):
         self.lib.ora_widen(dtype, _ptr(x), out, x.size)
@@ -283,7 +332,7 @@ class RefError(RuntimeError):
     pass
 
 
-class Reference(_Base):
+class Reference(_Base, _Turbo):
     """The reference's own cpu-ref backend (oracle/_ref/libxsref.so), one Session step per call."""
 
     def __init__(self, path: str = REF_LIB):
@@ -313,7 +362,19 @@ class Reference(_Base):
         L.xsref_quantize_kv_row_i8.restype = C.c_float
         L.xsref_round_trip_kv_i8.argtypes = [_fp, _L, _L]
         L.xsref_kv_cache_i8.argtypes = [C.c_int, _P, _P, _L, _L, _L, _fp, _fp]
+        L.xsref_turbo_quantize.argtypes = [_fp, _L, C.c_int, _u8, _u16]
+        L.xsref_turbo_decode.argtypes = [_u8, _u16, _L, C.c_int, _fp]
+        L.xsref_turbo_rotate.argtypes = [_fp, _L, C.c_int]
         self.lib = L
+
+    def _tq(self, *a):
+        self.lib.xsref_turbo_quantize(*a)
+
+    def _td(self, *a):
+        self.lib.xsref_turbo_decode(*a)
+
+    def _tr(self, *a):
+        self.lib.xsref_turbo_rotate(*a)
 
     def _check(self, rc):
         if rc != 0:

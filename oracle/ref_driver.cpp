@@ -22,6 +22,7 @@
 #include "graph/graph.h"
 #include "models/common/blocks.h"
 #include "quant/kv_format.h"
+#include "quant/kv_turbo.h"
 #include "quant/quant.h"
 #include "tensor/tensor.h"
 #include "util/error.h"
@@ -349,6 +350,24 @@ int xsref_kv_cache_i8(int dtype, const void* k, const void* v, int64_t tokens, i
         copy_f32(res.at("k_all"), k_out);
         copy_f32(res.at("v_all"), v_out);
     });
+}
+
+// TurboQuant groups through the reference's own functions (src/quant/kv_turbo.cpp): codes, f16 norms, decoded
+// (rotated) values, the rotation.
+void xsref_turbo_quantize(const float* x, int64_t groups, int bits, uint8_t* codes, uint16_t* norms) {
+    for (int64_t g = 0; g < groups; ++g)
+        norms[g] = quant::turbo::quantize_group(x + g * quant::turbo::kGroup, bits,
+                                                codes + g * quant::turbo::group_bytes(bits));
+}
+
+void xsref_turbo_decode(const uint8_t* codes, const uint16_t* norms, int64_t groups, int bits, float* out) {
+    for (int64_t g = 0; g < groups; ++g)
+        quant::turbo::decode_group(codes + g * quant::turbo::group_bytes(bits), norms[g], bits,
+                                   out + g * quant::turbo::kGroup);
+}
+
+void xsref_turbo_rotate(float* x, int64_t groups, int inverse) {
+    for (int64_t g = 0; g < groups; ++g) quant::turbo::rotate_group(x + g * quant::turbo::kGroup, inverse != 0);
 }
 
 }  // extern "C"

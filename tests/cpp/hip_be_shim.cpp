@@ -135,7 +135,7 @@ int hipbe_dequantize_kv_f16(void* q, const void* codes, const void* scales, void
 
 int hipbe_quantize_kv_turbo() {
     return guarded([&] {
-        hb::quantize_kv<float>(nullptr, hb::KvFormat::Turbo4, nullptr, nullptr, nullptr, 4, 128);
+        hb::quantize_kv<float>(nullptr, hb::KvFormat::Turbo4, nullptr, nullptr, nullptr, 4, 100);  // not whole groups
     });
 }
 

@@ -67,8 +67,11 @@ def err():
 
 
 def test_refusals_name_the_problem():
-    assert L().xs_hip_quantize_kv(None, xs_hip.KV_TURBO4, xs_hip.F16, None, None, None, 4, 128) == 2
-    assert "TurboQuant" in err()
+    # TurboQuant rows are groups of 128 values.
+    assert L().xs_hip_quantize_kv(None, xs_hip.KV_TURBO4, xs_hip.F16, None, None, None, 4, 100) == 1
+    assert "multiple of 128" in err()
+    assert L().xs_hip_kv_rotate(None, None, None, 2, 96, 0) == 1
+    assert "multiple of 128" in err()
     assert L().xs_hip_quantize_kv(None, xs_hip.KV_FLOAT, xs_hip.F16, None, None, None, 4, 128) == 1
     assert L().xs_hip_quantize_kv(None, xs_hip.KV_I8, xs_hip.F16, None, None, None, 4, 128) == 1
     assert "null buffer" in err()

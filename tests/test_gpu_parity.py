@@ -747,3 +747,107 @@ def test_attention_i8_decode_full_size(ora):
     k_rt = ora.dequantize_kv(kc.numpy(), ks.numpy()).reshape(k.shape)
     v_rt = ora.dequantize_kv(vc.numpy(), vs.numpy()).reshape(v.shape)
     assert_attention_close(y, ora.attention(q, k_rt, v_rt, 1.0 / math.sqrt(d)), "decode full size")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# TurboQuant KV formats
+
+def turbo_rows(rng, n, width, dtype):
+    x = rng.standard_normal((n, width)).astype(np.float32)
+    x[0] = 0.0                      # a zero group: norm 0
+    x[1] *= np.float32(1e-20)       # tiny
+    x[2] *= np.float32(1e15)        # huge (the sum of squares still finite)
+    x[3, 7] = 200.0                 # one spike
+    if dtype == F32:
+        return x, x
+    if dtype == BF16:
+        stored = (x.view(np.uint32) >> 16).astype(np.uint16)  # bf16 bits (truncated: any bits are an input)
+        return stored, (stored.astype(np.uint32) << 16).view(np.float32)
+    stored = x.astype(np.float16)
+    return stored, stored.astype(np.float32)
+
+
+@pytest.mark.parametrize("bits", [4, 3, 2])
+@pytest.mark.parametrize("dtype,n,width", [(F32, 300, 128), (F16, 129, 256), (BF16, 33, 384)])
+def test_turbo_quantize_decode(ora, bits, dtype, n, width):
+    """Codes and f16 norms bit for bit as quant::turbo::quantize_group, and the decoded (rotated) values as
+    decode_group -- f32 exactly, f16/bf16 as the f32 value rounded once."""
+    rng = np.random.default_rng(80 + bits + width)
+    stored, as_f32 = turbo_rows(rng, n, width, dtype)
+    if dtype == F16:  # the f16 cast can overflow row 2; keep it finite
+        stored[2] = np.float16(1000) * rng.standard_normal(width).astype(np.float16)
+        as_f32 = stored.astype(np.float32)
+    step(f"turbo{bits} quantize {fmt(dtype) if dtype != F32 else 'f32'} [{n}, {width}]")
+    codes, norms = X.turbo_quantize(dev(stored, dtype), bits)
+    want_c, want_n = ora.turbo_quantize(as_f32, bits)
+    assert_exact(codes.numpy(), want_c, f"turbo{bits} codes")
+    assert_exact(norms.numpy().view(np.uint16), want_n, f"turbo{bits} norms")
+    out = X.turbo_dequantize(codes, norms, bits, F32).numpy()
+    want = ora.turbo_decode(want_c, want_n, bits)
+    assert_exact(out, want, f"turbo{bits} decode")
+    for odt in (F16, BF16):
+        got = X.turbo_dequantize(codes, norms, bits, odt).numpy()
+        assert_exact(np.ascontiguousarray(got).view(np.uint16), np.ascontiguousarray(ora.narrow(want, odt)).view(np.uint16),
+                     f"turbo{bits} decode to {fmt(odt)}")
+
+
+@pytest.mark.parametrize("bits", [4, 3, 2])
+def test_turbo_reference_fixture_rows(ora, bits):
+    """The reference's fixture rows (tests/fixtures/quant/turbo) through the device: every nonzero row's codes as the
+    format's published implementation stored them (its rows hold no edge ties here) and the norm within one f16
+    step."""
+    rows = np.fromfile(os.path.join(GOLDEN, "turbo", "rows.f32"), np.float32).reshape(-1, 128)
+    blocks = np.fromfile(os.path.join(GOLDEN, "turbo", f"turbo{bits}.blocks"), np.uint8).reshape(rows.shape[0], -1)
+    want_norms = blocks[:, :2].copy().view(np.uint16)[:, 0]
+    step(f"turbo{bits} fixture rows")
+    codes, norms = X.turbo_quantize(dev(rows), bits)
+    got_c = codes.numpy()
+    got_n = norms.numpy().view(np.uint16)
+    assert np.abs(got_n.astype(np.int64) - want_norms.astype(np.int64)).max() <= 1
+    nz = want_norms != 0
+    assert_exact(got_c[nz], blocks[nz, 2:], f"turbo{bits} fixture codes")
+
+
+def test_turbo_nan_group(ora):
+    """A NaN in a group makes every edge test fail in f32 (all magnitude codes 0) and its norm 0."""
+    x = np.random.default_rng(90).standard_normal((3, 128)).astype(np.float32)
+    x[1, 17] = np.nan
+    for bits in (4, 3, 2):
+        step(f"turbo{bits} NaN group")
+        codes, norms = X.turbo_quantize(dev(x), bits)
+        want_c, want_n = ora.turbo_quantize(x, bits)
+        assert_exact(codes.numpy(), want_c, f"turbo{bits} codes with a NaN")
+        got_n = norms.numpy().view(np.uint16)
+        assert want_n[1] == 0  # n > 0 fails for a NaN n: the norm is 0 (kv_turbo.cpp:83)
+        assert_exact(got_n, want_n, "norms with a NaN group")
+
+
+def test_turbo_rotate(ora):
+    """The rotation and its inverse, bit for bit as rotate_group; in place too."""
+    rng = np.random.default_rng(91)
+    x = rng.standard_normal((77, 256)).astype(np.float32)
+    step("kv_rotate")
+    y = X.kv_rotate(dev(x))
+    assert_exact(y.numpy(), ora.turbo_rotate(x), "rotate")
+    back = X.kv_rotate(y, inverse=True).numpy()
+    assert_exact(back, ora.turbo_rotate(ora.turbo_rotate(x), inverse=True), "rotate back")
+    assert np.abs(back - x).max() < 1e-5
+    d = dev(x)
+    X.call("xs_hip_kv_rotate", None, C.c_void_p(d.ptr), C.c_void_p(d.ptr), 77, 256, 0)
+    assert_exact(d.numpy(), ora.turbo_rotate(x), "rotate in place")
+
+
+def test_turbo4_full_size(ora):
+    """Config 4's K cache [65536 x 8, 128] f16 as turbo4: every group's codes and norm as the oracle's, and the round
+    trip's error that of a 4-bit Lloyd-Max quantizer (the row's variance x 0.0095, within the reference's band)."""
+    k = W.config4().arrays["k"]
+    rows = k.reshape(-1, 128)
+    step("turbo4 full size [524288, 128] f16")
+    codes, norms = X.turbo_quantize(dev(rows, F16), 4)
+    want_c, want_n = ora.turbo_quantize(rows.astype(np.float32), 4)
+    assert_exact(codes.numpy(), want_c, "turbo4 codes, full size")
+    assert_exact(norms.numpy().view(np.uint16), want_n, "turbo4 norms, full size")
+    back = X.kv_rotate(X.turbo_dequantize(codes, norms, 4, F32), inverse=True).numpy()
+    x = rows.astype(np.float64)
+    rel = ((back - x) ** 2).sum() / (x ** 2).sum()
+    assert 0.008 < rel < 0.012, rel

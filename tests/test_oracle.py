@@ -549,3 +549,155 @@ def test_oracle_matches_compiled_reference_attention(ora):
     assert_exact(ora.attention(q, rt(k), rt(v), 0.125), ref.attention(q, k, v, 0.125, kv_i8=True))
     assert_exact(ora.attention(q, k, v, 0.125, 0.0, 33, True), ref.attention(q, k, v, 0.125, 0.0, 33, True))
     assert_exact(ora.attention(q, k, v, 0.125, 0.0, 0, False), ref.attention(q, k, v, 0.125, 0.0, 0, False))
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# TurboQuant KV formats (quant/kv_turbo)
+
+TURBO = os.path.join(GOLDEN, "turbo")
+SIGNS_BEFORE = (0x42F85949E46A0359, 0x49F250A9A4C63BBB)
+SIGNS_AFTER = (0x3F628FDC16ACEE90, 0xBEA56562B7A5357A)
+EDGES = {2: [0.086728], 3: [0.044243, 0.092804, 0.154496],
+         4: [0.022824, 0.046174, 0.070671, 0.097164, 0.127026, 0.162947, 0.212203]}
+
+
+def sign_vector(words):
+    return np.array([-1.0 if (words[i // 64] >> (i % 64)) & 1 else 1.0 for i in range(128)])
+
+
+def sylvester(n):
+    h = np.ones((1, 1))
+    while h.shape[0] < n:
+        h = np.block([[h, h], [h, -h]])
+    return h
+
+
+def rotated_unit(x):
+    """The group's rotation in f64 by the Hadamard matrix itself, scaled to unit norm: what the codes round."""
+    x = np.asarray(x, np.float64)
+    w = sign_vector(SIGNS_AFTER) * (sylvester(128) @ (sign_vector(SIGNS_BEFORE) * x)) / math.sqrt(128)
+    n = np.linalg.norm(x)
+    return w / n if n > 0 else w
+
+
+def code_at(c, bits, i):
+    if bits == 4:
+        return (int(c[i // 2]) >> (4 * (i % 2))) & 15
+    low = (int(c[i // 4]) >> (2 * (i % 4))) & 3
+    if bits == 2:
+        return low
+    return low | (((int(c[32 + i // 8]) >> (i % 8)) & 1) << 2)
+
+
+def fixture(bits):
+    rows = np.fromfile(os.path.join(TURBO, "rows.f32"), np.float32).reshape(-1, 128)
+    blocks = np.fromfile(os.path.join(TURBO, f"turbo{bits}.blocks"), np.uint8).reshape(rows.shape[0], -1)
+    return rows, blocks[:, 2:], blocks[:, :2].copy().view(np.uint16)[:, 0]
+
+
+@pytest.mark.parametrize("bits", [4, 3, 2])
+def test_turbo_reference_fixtures(ora, bits):
+    """tests/fixtures/quant/turbo (the format's published implementation, tests/unit/quant/test_kv_formats.cpp:142-181):
+    the codes of every row with a nonzero norm, except at most two coordinates that sit on an edge (neighbours, and
+    only there), and the f16 norm within one step."""
+    rows, want_codes, want_norms = fixture(bits)
+    assert rows.shape[0] >= 40
+    codes, norms = ora.turbo_quantize(rows, bits)
+    assert np.abs(norms.astype(np.int64) - want_norms.astype(np.int64)).max() <= 1
+    ties = 0
+    for r in range(rows.shape[0]):
+        if want_norms[r] == 0:
+            continue
+        w = rotated_unit(rows[r])
+        for i in range(128):
+            got, want = code_at(codes[r], bits, i), code_at(want_codes[r], bits, i)
+            if got != want:
+                ties += 1
+                assert abs(got - want) == 1
+                assert min([abs(abs(w[i]) - e) for e in EDGES[bits]] + [abs(w[i])]) < 2e-7
+    assert ties <= 2
+
+
+@pytest.mark.parametrize("bits", [4, 3, 2])
+def test_turbo_nearest_centroid_and_norm(ora, bits):
+    """Each code names the centroid nearest the row's rotated, normalized coordinate (the rotation by the Hadamard
+    matrix in f64); decoding gives centroid * norm exactly; the norm restores the row's own (f16)."""
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((64, 128)) * 3).astype(np.float32)
+    codes, norms = ora.turbo_quantize(x, bits)
+    cents = ora.turbo_centroids(bits)
+    assert np.all(np.diff(cents) > 0)  # ascending: code order is value order
+    decoded = ora.turbo_decode(codes, norms, bits)
+    for r in range(64):
+        w = rotated_unit(x[r])
+        c = np.array([code_at(codes[r], bits, i) for i in range(128)])
+        best = np.abs(w[:, None] - cents[None, :].astype(np.float64)).min(1)
+        assert np.all(np.abs(w - cents[c]) <= best + 1e-6)
+        nf = norms[r:r + 1].view(np.float16).astype(np.float32)[0]
+        assert_exact(decoded[r], cents[c] * nf, f"decode row {r}")
+        assert math.isclose(np.linalg.norm(decoded[r].astype(np.float64)), np.linalg.norm(x[r].astype(np.float64)),
+                            rel_tol=1e-3)
+
+
+def test_turbo_rotation(ora):
+    """The rotation is the signed, scaled Hadamard transform: orthogonal, undone by its inverse."""
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((2, 128)).astype(np.float32)
+    y = ora.turbo_rotate(x)
+    want = np.stack([rotated_unit(x[i]) * np.linalg.norm(x[i].astype(np.float64)) for i in range(2)])
+    assert np.abs(y - want).max() < 1e-5
+    assert math.isclose(float(np.dot(y[0].astype(np.float64), y[1])), float(np.dot(x[0].astype(np.float64), x[1])),
+                        rel_tol=1e-5, abs_tol=1e-5)
+    assert np.abs(ora.turbo_rotate(y, inverse=True) - x).max() < 1e-5
+    assert np.abs(y[0, 0] - x[0, 0]) > 1e-3
+
+
+def test_turbo_error_and_planted_bugs(ora):
+    """tests/unit/quant/test_kv_formats.cpp:230-270: the round trip leaves about the Lloyd-Max quantizers' error on
+    Gaussian rows (0.0095, 0.0345, 0.1175 of the variance) and no more on spiky ones; zeros stay zeros; codes read at
+    another width, or left rotated, are far from the row."""
+    rng = np.random.default_rng(21)
+    gauss = (rng.standard_normal((200, 256)) * 0.7).astype(np.float32)
+    spiky = (rng.standard_normal((200, 256)) * 0.02).astype(np.float32)
+    for r in range(200):
+        spiky[r, rng.integers(0, 256, 3)] = rng.choice([-25.0, 25.0], 3)
+
+    def rel(x, bits):
+        y = ora.turbo_round_trip(x, bits)
+        return float(((y.astype(np.float64) - x) ** 2).sum() / (x.astype(np.float64) ** 2).sum())
+
+    for bits, lo, hi in ((4, 0.008, 0.012), (3, 0.030, 0.040), (2, 0.105, 0.130)):
+        e = rel(gauss, bits)
+        assert lo < e < hi, (bits, e)
+        assert rel(spiky, bits) < hi
+        assert not ora.turbo_round_trip(np.zeros((1, 256), np.float32), bits).any()
+    x = rng.standard_normal((1, 128)).astype(np.float32)
+    codes, norms = ora.turbo_quantize(x, 4)
+    good = ora.turbo_rotate(ora.turbo_decode(codes, norms, 4), inverse=True)
+    assert np.abs(good - x).max() < 0.5
+    wrong_width = ora.turbo_rotate(ora.turbo_decode(codes[:, :48], norms, 3), inverse=True)
+    left_rotated = ora.turbo_decode(codes, norms, 4)
+    for bad in (wrong_width, left_rotated):
+        assert np.linalg.norm(bad - x) > 0.5 * np.linalg.norm(x)
+
+
+def test_turbo_against_compiled_reference(ora):
+    """The restatement and the reference's own kv_turbo.cpp, bit for bit, on Gaussian, spiky, scaled and zero
+    groups (the reference built here; skipped where its tree is absent)."""
+    ref = reference()
+    if ref is None:
+        pytest.skip("the reference was not built here")
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((300, 128)).astype(np.float32)
+    x[10] = 0.0
+    x[11] *= 1e-20
+    x[12] *= 1e20
+    x[13, 5] = 300.0
+    for bits in (4, 3, 2):
+        c1, n1 = ora.turbo_quantize(x, bits)
+        c2, n2 = ref.turbo_quantize(x, bits)
+        assert_exact(c1, c2, f"turbo{bits} codes")
+        assert_exact(n1, n2, f"turbo{bits} norms")
+        assert_exact(ora.turbo_decode(c1, n1, bits), ref.turbo_decode(c2, n2, bits), f"turbo{bits} decode")
+    assert_exact(ora.turbo_rotate(x), ref.turbo_rotate(x), "rotate")
+    assert_exact(ora.turbo_rotate(x, inverse=True), ref.turbo_rotate(x, inverse=True), "rotate back")

@@ -23,6 +23,7 @@
 // tiles: the workgroups in flight then read one contiguous window of memory, which HBM serves faster than the
 // scattered windows of a grid-stride loop.
 #include "common.h"
+#include "kv_turbo.h"
 
 namespace xs_hip {
 namespace {
@@ -222,12 +223,14 @@ int launch_dequantize(hipStream_t s, const int8_t* codes, const float* scales, v
     return check_launch("xs_hip_dequantize_kv");
 }
 
+// Bits a code of a TurboQuant format (quant::turbo_bits, src/quant/kv_format.cpp).
+int turbo_bits(xs_kv_format f) { return f == XS_KV_TURBO4 ? 4 : f == XS_KV_TURBO3 ? 3 : 2; }
+
 int check_kv_format(xs_kv_format format, const char* op) {
     if (format == XS_KV_I8) return XS_HIP_OK;
     if (format == XS_KV_FLOAT)
         return fail(XS_HIP_EINVAL, std::string(op) + ": the float format is stored as it is, not quantized");
-    if (format >= XS_KV_TURBO4 && format <= XS_KV_TURBO2)
-        return fail(XS_HIP_EUNSUPPORTED, std::string(op) + ": TurboQuant KV formats are not implemented on this device");
+    if (format >= XS_KV_TURBO4 && format <= XS_KV_TURBO2) return XS_HIP_OK;
     return fail(XS_HIP_EINVAL, std::string(op) + ": unknown KV format " + std::to_string(static_cast<int>(format)));
 }
 
@@ -242,6 +245,8 @@ int xs_hip_quantize_kv(void* stream, xs_kv_format format, xs_dtype x_dtype, cons
                        int64_t rows, int64_t width) {
     int rc = check_kv_format(format, "xs_hip_quantize_kv");
     if (rc != XS_HIP_OK) return rc;
+    if (format != XS_KV_I8)
+        return turbo_quantize(as_stream(stream), turbo_bits(format), x_dtype, x, codes, scales, rows, width);
     if (rows < 0 || width <= 0)
         return fail(XS_HIP_EINVAL, "xs_hip_quantize_kv: rows " + std::to_string(rows) + " of width " +
                                        std::to_string(width));
@@ -266,6 +271,8 @@ int xs_hip_dequantize_kv(void* stream, xs_kv_format format, const void* codes, c
                          void* out, int64_t rows, int64_t width) {
     int rc = check_kv_format(format, "xs_hip_dequantize_kv");
     if (rc != XS_HIP_OK) return rc;
+    if (format != XS_KV_I8)
+        return turbo_dequantize(as_stream(stream), turbo_bits(format), codes, scales, out_dtype, out, rows, width);
     if (rows < 0 || width <= 0)
         return fail(XS_HIP_EINVAL, "xs_hip_dequantize_kv: rows " + std::to_string(rows) + " of width " +
                                        std::to_string(width));

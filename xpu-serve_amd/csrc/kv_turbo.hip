@@ -1,0 +1,367 @@
+// TurboQuant KV formats (turbo4, turbo3, turbo2) for gfx950: quantize rows into codes and f16 norms, decode them,
+// and the rotation a query takes to be read against them.
+//
+// Semantics: quant::turbo::quantize_group / decode_group / rotate_group (reference src/quant/kv_turbo.h:14-105,
+// src/quant/kv_turbo.cpp:47-129), which every backend repeats in the same f32 arithmetic so that all store the same
+// bits. A group of 128 values: n = the sum of squares (each 8-value lane's squares fused-multiply-added in order, the
+// 16 lane sums added pairwise 1, 2, 4, 8 lanes apart); w = the values sign-flipped (kSignsBefore), through unnormalized
+// Walsh-Hadamard butterflies of spans 1 .. 64, sign-flipped again (kSignsAfter); code = the sign of w and the count of
+// edges e_j with w^2 >= fl32(e_j^2 * 128) * n (> when w < 0); norm = f16(sqrt(n / r)), r the chosen magnitudes'
+// squares summed like n with plain adds (0 when n is 0). Decoding gives centroid(code) * norm, still rotated. Launchers
+// replaced: sycl_be::quantize_kv / dequantize_kv for the Turbo formats and sycl_be::kv_rotate (src/backend/sycl/
+// sycl_kernels.h:211-221; sycl_kv_cache.cpp:51-85, 96-106, 149-163).
+//
+// Layout: a group per 16 lanes, 8 consecutive values per lane (one 16-byte load of f16/bf16, two of f32), four groups
+// a wave. The butterflies of spans 1, 2, 4 run inside a lane; spans 8, 16, 32, 64 pair lane l with l ^ 1, 2, 4, 8 of
+// the same 16 (DPP quad permutations for 1 and 2, ds_swizzle for 4 and 8). The edge test compares the bit patterns of
+// non-negative floats as integers: k = bits(w^2) + (w >= 0), and edge j counts when bits(edge_j) < k -- w^2 >= edge for
+// a non-negative w, w^2 > edge for a negative one, in one integer compare. The magnitudes' squares and the centroids
+// come from LDS tables. Codes of a group: turbo4 a nibble per value (a lane's 8 codes are one 32-bit word), turbo2 two
+// bits per value (a lane's are one 16-bit word), turbo3 the turbo2 layout of the low two bits in bytes 0..31 and the
+// third bits as one byte per lane at 32 + lane (kv_turbo.h:84-87).
+#include "common.h"
+#include "kv_turbo.h"
+
+namespace xs_hip {
+namespace {
+
+constexpr int kGroup = 128;
+constexpr int kLanes = 16;       // lanes a group
+constexpr int kLaneValues = 8;   // values a lane
+constexpr int kGroupsPerBlock = kBlock / kLanes;
+
+// The rotation's sign flips before and after the transform: bit i % 64 of word i / 64 flips value i
+// (kv_turbo.h:27-28; format constants).
+constexpr uint64_t kSignsBefore[2] = {0x42f85949e46a0359ull, 0x49f250a9a4c63bbbull};
+constexpr uint64_t kSignsAfter[2] = {0x3f628fdc16acee90ull, 0xbea56562b7a5357aull};
+
+// The codebooks: Lloyd-Max magnitudes for a Gaussian of variance 1 / 128 and the borders between neighbours
+// (kv_turbo.h:39-56; format constants).
+template <int Bits>
+struct Book;
+template <>
+struct Book<2> {
+    static constexpr float mags[2] = {0.039994f, 0.133462f};
+    static constexpr float edges[1] = {0.086728f};
+};
+template <>
+struct Book<3> {
+    static constexpr float mags[4] = {0.021663f, 0.066822f, 0.118786f, 0.190207f};
+    static constexpr float edges[3] = {0.044243f, 0.092804f, 0.154496f};
+};
+template <>
+struct Book<4> {
+    static constexpr float mags[8] = {0.011349f, 0.034299f, 0.058050f, 0.083292f,
+                                      0.111036f, 0.143016f, 0.182877f, 0.241529f};
+    static constexpr float edges[7] = {0.022824f, 0.046174f, 0.070671f, 0.097164f, 0.127026f, 0.162947f, 0.212203f};
+};
+
+template <int Bits>
+constexpr int kMagnitudes = 1 << (Bits - 1);
+
+// fl32(e_j^2 * 128), squared in f64 (kv_turbo.h:57-62).
+template <int Bits>
+constexpr float edge_sq(int j) {
+    const double e = Book<Bits>::edges[j];
+    return static_cast<float>(e * e * kGroup);
+}
+
+// Sign masks (bit 31) of lane `lane`'s 8 values.
+__device__ __forceinline__ void sign_masks(const uint64_t* signs, int lane, uint32_t* mask) {
+    const uint32_t bits = static_cast<uint32_t>((lane < 8 ? signs[0] : signs[1]) >> (8 * (lane % 8))) & 0xffu;
+#pragma unroll
+    for (int e = 0; e < kLaneValues; ++e) mask[e] = ((bits >> e) & 1u) << 31;
+}
+
+__device__ __forceinline__ float flip(float v, uint32_t mask) { return __uint_as_float(__float_as_uint(v) ^ mask); }
+
+// The value of lane l ^ M of this lane's 16 (M = 1, 2, 4, 8).
+template <int M>
+__device__ __forceinline__ float xlane(float v) {
+    if constexpr (M == 1) return dpp_f<dpp::kQuadXor1>(v);
+    else if constexpr (M == 2) return dpp_f<dpp::kQuadXor2>(v);
+    else return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1f | (M << 10)));  // bit mode, xor M
+}
+
+// The 16 lanes' values added pairwise, 1, 2, 4, 8 lanes apart: every lane ends with the same sum.
+__device__ __forceinline__ float sum_lanes(float s) {
+    s = s + xlane<1>(s);
+    s = s + xlane<2>(s);
+    s = s + xlane<4>(s);
+    return s + xlane<8>(s);
+}
+
+// Span 8 M of the butterflies: the lower lane of a pair takes a + b, the upper a - b (a the lower's value, b the
+// upper's), each as its own value negated or not plus the partner's.
+template <int M>
+__device__ __forceinline__ void cross_span(float* v, int lane) {
+    const uint32_t neg = (lane & M) ? 0x80000000u : 0u;
+#pragma unroll
+    for (int e = 0; e < kLaneValues; ++e) {
+        const float p = xlane<M>(v[e]);
+        v[e] = p + flip(v[e], neg);
+    }
+}
+
+// The unnormalized Walsh-Hadamard transform of a group, on this lane's 8 values.
+__device__ __forceinline__ void butterflies(float* v, int lane) {
+#pragma unroll
+    for (int h = 1; h < kLaneValues; h *= 2) {
+#pragma unroll
+        for (int e = 0; e < kLaneValues; ++e) {
+            if (e & h) continue;
+            const float a = v[e], b = v[e + h];
+            v[e] = a + b;
+            v[e + h] = a - b;
+        }
+    }
+    cross_span<1>(v, lane);
+    cross_span<2>(v, lane);
+    cross_span<4>(v, lane);
+    cross_span<8>(v, lane);
+}
+
+template <typename X>
+__device__ __forceinline__ void load_lane(const typename X::storage* x, float* v) {
+    if constexpr (sizeof(typename X::storage) == 4) {
+        unpack<X>(ld128_nt(x), v);
+        unpack<X>(ld128_nt(x + 4), v + 4);
+    } else {
+        unpack<X>(ld128_nt(x), v);
+    }
+}
+
+template <int Bits, typename X>
+__global__ __launch_bounds__(kBlock) void turbo_quantize_kernel(const typename X::storage* __restrict__ x,
+                                                                uint8_t* __restrict__ codes,
+                                                                uint16_t* __restrict__ norms, int64_t groups) {
+    constexpr int NM = kMagnitudes<Bits>;
+    __shared__ float mag_sq[NM];
+    if (threadIdx.x < NM) mag_sq[threadIdx.x] = Book<Bits>::mags[threadIdx.x] * Book<Bits>::mags[threadIdx.x];
+    __syncthreads();
+    const int lane = threadIdx.x % kLanes;
+    const int64_t g = static_cast<int64_t>(blockIdx.x) * kGroupsPerBlock + threadIdx.x / kLanes;
+    if (g >= groups) return;  // whole 16-lane groups leave together
+
+    float v[kLaneValues];
+    load_lane<X>(x + g * kGroup + lane * kLaneValues, v);
+    float n = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kLaneValues; ++e) n = fmaf(v[e], v[e], n);
+    n = sum_lanes(n);
+
+    uint32_t mask[kLaneValues];
+    sign_masks(kSignsBefore, lane, mask);
+#pragma unroll
+    for (int e = 0; e < kLaneValues; ++e) v[e] = flip(v[e], mask[e]);
+    butterflies(v, lane);
+    sign_masks(kSignsAfter, lane, mask);
+
+    uint32_t edge[NM - 1];
+#pragma unroll
+    for (int j = 0; j < NM - 1; ++j) edge[j] = __float_as_uint(edge_sq<Bits>(j) * n);
+    const bool defined = n == n;  // a NaN in the group: every edge test fails, as in f32
+    uint32_t packed = 0, high = 0;
+    float r = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kLaneValues; ++e) {
+        const float w = flip(v[e], mask[e]);
+        const bool negative = w < 0.0f;
+        const uint32_t k = __float_as_uint(w * w) + (negative ? 0u : 1u);
+        uint32_t m = 0;
+#pragma unroll
+        for (int j = 0; j < NM - 1; ++j) m += edge[j] < k ? 1u : 0u;
+        m = defined ? m : 0u;
+        const uint32_t code = negative ? NM - 1 - m : NM + m;
+        if constexpr (Bits == 4) {
+            packed |= code << (4 * e);
+        } else {
+            packed |= (code & 3u) << (2 * e);
+            if constexpr (Bits == 3) high |= (code >> 2) << e;
+        }
+        r += mag_sq[m];
+    }
+    r = sum_lanes(r);
+    uint8_t* gc = codes + g * (kGroup * Bits / 8);
+    if constexpr (Bits == 4) {
+        reinterpret_cast<uint32_t*>(gc)[lane] = packed;
+    } else {
+        reinterpret_cast<uint16_t*>(gc)[lane] = static_cast<uint16_t>(packed);
+        if constexpr (Bits == 3) gc[kGroup / 4 + lane] = static_cast<uint8_t>(high);
+    }
+    if (lane == 0) norms[g] = f32_to_f16(n > 0.0f ? sqrtf(n / r) : 0.0f);
+}
+
+template <int Bits, typename Y>
+__global__ __launch_bounds__(kBlock) void turbo_decode_kernel(const uint8_t* __restrict__ codes,
+                                                              const uint16_t* __restrict__ norms,
+                                                              typename Y::storage* __restrict__ out, int64_t groups) {
+    constexpr int NC = 1 << Bits;
+    constexpr int NM = kMagnitudes<Bits>;
+    __shared__ float centroid[NC];
+    if (threadIdx.x < NC) {
+        const int c = static_cast<int>(threadIdx.x);
+        centroid[c] = c >= NM ? Book<Bits>::mags[c - NM] : -Book<Bits>::mags[NM - 1 - c];
+    }
+    __syncthreads();
+    const int lane = threadIdx.x % kLanes;
+    const int64_t g = static_cast<int64_t>(blockIdx.x) * kGroupsPerBlock + threadIdx.x / kLanes;
+    if (g >= groups) return;
+    const uint8_t* gc = codes + g * (kGroup * Bits / 8);
+    uint32_t packed, high = 0;
+    if constexpr (Bits == 4) {
+        packed = reinterpret_cast<const uint32_t*>(gc)[lane];
+    } else {
+        packed = reinterpret_cast<const uint16_t*>(gc)[lane];
+        if constexpr (Bits == 3) high = gc[kGroup / 4 + lane];
+    }
+    const float norm = f16_to_f32(norms[g]);
+    float v[kLaneValues];
+#pragma unroll
+    for (int e = 0; e < kLaneValues; ++e) {
+        uint32_t code;
+        if constexpr (Bits == 4) code = (packed >> (4 * e)) & 15u;
+        else code = ((packed >> (2 * e)) & 3u) | (Bits == 3 ? ((high >> e) & 1u) << 2 : 0u);
+        v[e] = centroid[code] * norm;
+    }
+    typename Y::storage* o = out + g * kGroup + lane * kLaneValues;
+    if constexpr (sizeof(typename Y::storage) == 4) {
+        st128_nt(o, pack<Y>(v));
+        st128_nt(o + 4, pack<Y>(v + 4));
+    } else {
+        st128_nt(o, pack<Y>(v));
+    }
+}
+
+// Each group rotated (signs before, butterflies, 1 / sqrt(128), signs after) or rotated back (the two sign sets
+// swapped): quant::turbo::rotate_group (kv_turbo.cpp:118-129).
+__global__ __launch_bounds__(kBlock) void turbo_rotate_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                              int64_t groups, bool inverse) {
+    const int lane = threadIdx.x % kLanes;
+    const int64_t g = static_cast<int64_t>(blockIdx.x) * kGroupsPerBlock + threadIdx.x / kLanes;
+    if (g >= groups) return;
+    float v[kLaneValues];
+    const float* xl = x + g * kGroup + lane * kLaneValues;
+    unpack<F32>(ld128(xl), v);
+    unpack<F32>(ld128(xl + 4), v + 4);
+    uint32_t mask[kLaneValues];
+    sign_masks(inverse ? kSignsAfter : kSignsBefore, lane, mask);
+#pragma unroll
+    for (int e = 0; e < kLaneValues; ++e) v[e] = flip(v[e], mask[e]);
+    butterflies(v, lane);
+    sign_masks(inverse ? kSignsBefore : kSignsAfter, lane, mask);
+#pragma unroll
+    for (int e = 0; e < kLaneValues; ++e) v[e] = flip(v[e] * 0.08838834764831845f, mask[e]);
+    float* yl = y + g * kGroup + lane * kLaneValues;
+    st128(yl, pack<F32>(v));
+    st128(yl + 4, pack<F32>(v + 4));
+}
+
+unsigned blocks_for(int64_t groups) { return static_cast<unsigned>((groups + kGroupsPerBlock - 1) / kGroupsPerBlock); }
+
+template <int Bits>
+int quantize_bits(hipStream_t s, xs_dtype x_dtype, const void* x, uint8_t* codes, uint16_t* norms, int64_t groups) {
+    switch (x_dtype) {
+        case XS_F32:
+            turbo_quantize_kernel<Bits, F32><<<blocks_for(groups), kBlock, 0, s>>>(static_cast<const float*>(x), codes,
+                                                                                   norms, groups);
+            break;
+        case XS_F16:
+            turbo_quantize_kernel<Bits, F16><<<blocks_for(groups), kBlock, 0, s>>>(static_cast<const uint16_t*>(x),
+                                                                                   codes, norms, groups);
+            break;
+        case XS_BF16:
+            turbo_quantize_kernel<Bits, BF16><<<blocks_for(groups), kBlock, 0, s>>>(static_cast<const uint16_t*>(x),
+                                                                                    codes, norms, groups);
+            break;
+        default:
+            return fail(XS_HIP_EINVAL, std::string("xs_hip_quantize_kv: x must be f32, f16 or bf16, got ") +
+                                           dtype_name(x_dtype));
+    }
+    return check_launch("xs_hip_quantize_kv");
+}
+
+template <int Bits>
+int decode_bits(hipStream_t s, const uint8_t* codes, const uint16_t* norms, xs_dtype out_dtype, void* out,
+                int64_t groups) {
+    switch (out_dtype) {
+        case XS_F32:
+            turbo_decode_kernel<Bits, F32><<<blocks_for(groups), kBlock, 0, s>>>(codes, norms, static_cast<float*>(out),
+                                                                                 groups);
+            break;
+        case XS_F16:
+            turbo_decode_kernel<Bits, F16><<<blocks_for(groups), kBlock, 0, s>>>(codes, norms,
+                                                                                 static_cast<uint16_t*>(out), groups);
+            break;
+        case XS_BF16:
+            turbo_decode_kernel<Bits, BF16><<<blocks_for(groups), kBlock, 0, s>>>(codes, norms,
+                                                                                  static_cast<uint16_t*>(out), groups);
+            break;
+        default:
+            return fail(XS_HIP_EINVAL, std::string("xs_hip_dequantize_kv: out must be f32, f16 or bf16, got ") +
+                                           dtype_name(out_dtype));
+    }
+    return check_launch("xs_hip_dequantize_kv");
+}
+
+int check_turbo(const char* op, int64_t rows, int64_t width, const void* a, const void* b, const void* c) {
+    if (rows < 0 || width <= 0 || width % kGroup != 0)
+        return fail(XS_HIP_EINVAL, std::string(op) + ": a TurboQuant format needs rows of a multiple of 128 values, got " +
+                                       std::to_string(rows) + " rows of " + std::to_string(width));
+    if (rows > 0 && (a == nullptr || b == nullptr || c == nullptr))
+        return fail(XS_HIP_EINVAL, std::string(op) + ": null buffer");
+    if (rows * (width / kGroup) > int64_t{0x7fffffff} * kGroupsPerBlock)
+        return fail(XS_HIP_EUNSUPPORTED, std::string(op) + ": too many groups");
+    return XS_HIP_OK;
+}
+
+}  // namespace
+
+int turbo_quantize(hipStream_t s, int bits, xs_dtype x_dtype, const void* x, void* codes, void* norms, int64_t rows,
+                   int64_t width) {
+    int rc = check_turbo("xs_hip_quantize_kv", rows, width, x, codes, norms);
+    if (rc != XS_HIP_OK || rows == 0) return rc;
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(codes) % 4 != 0 ||
+        reinterpret_cast<uintptr_t>(norms) % 2 != 0)
+        return fail(XS_HIP_EINVAL, "xs_hip_quantize_kv: TurboQuant needs x 16-byte, codes 4-byte and norms 2-byte "
+                                   "aligned");
+    const int64_t groups = rows * (width / kGroup);
+    auto* c = static_cast<uint8_t*>(codes);
+    auto* nm = static_cast<uint16_t*>(norms);
+    if (bits == 4) return quantize_bits<4>(s, x_dtype, x, c, nm, groups);
+    if (bits == 3) return quantize_bits<3>(s, x_dtype, x, c, nm, groups);
+    return quantize_bits<2>(s, x_dtype, x, c, nm, groups);
+}
+
+int turbo_dequantize(hipStream_t s, int bits, const void* codes, const void* norms, xs_dtype out_dtype, void* out,
+                     int64_t rows, int64_t width) {
+    int rc = check_turbo("xs_hip_dequantize_kv", rows, width, codes, norms, out);
+    if (rc != XS_HIP_OK || rows == 0) return rc;
+    if (reinterpret_cast<uintptr_t>(out) % 16 != 0 || reinterpret_cast<uintptr_t>(codes) % 4 != 0 ||
+        reinterpret_cast<uintptr_t>(norms) % 2 != 0)
+        return fail(XS_HIP_EINVAL, "xs_hip_dequantize_kv: TurboQuant needs out 16-byte, codes 4-byte and norms "
+                                   "2-byte aligned");
+    const int64_t groups = rows * (width / kGroup);
+    const auto* c = static_cast<const uint8_t*>(codes);
+    const auto* nm = static_cast<const uint16_t*>(norms);
+    if (bits == 4) return decode_bits<4>(s, c, nm, out_dtype, out, groups);
+    if (bits == 3) return decode_bits<3>(s, c, nm, out_dtype, out, groups);
+    return decode_bits<2>(s, c, nm, out_dtype, out, groups);
+}
+
+}  // namespace xs_hip
+
+using namespace xs_hip;
+
+extern "C" {
+
+int xs_hip_kv_rotate(void* stream, const float* x, float* y, int64_t rows, int64_t width, int inverse) {
+    int rc = check_turbo("xs_hip_kv_rotate", rows, width, x, y, x);
+    if (rc != XS_HIP_OK || rows == 0) return rc;
+    if (!aligned16(x) || !aligned16(y)) return fail(XS_HIP_EINVAL, "xs_hip_kv_rotate: x and y must be 16-byte aligned");
+    const int64_t groups = rows * (width / kGroup);
+    turbo_rotate_kernel<<<blocks_for(groups), kBlock, 0, as_stream(stream)>>>(x, y, groups, inverse != 0);
+    return check_launch("xs_hip_kv_rotate");
+}
+
+}  // extern "C"

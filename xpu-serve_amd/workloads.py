@@ -102,6 +102,9 @@ ALGO_BYTES: Dict[str, int] = {
     "rope_qk": 2 * (8192 * 32 * 128 * 2) + 2 * (8192 * 8 * 128 * 2) + 8192 * 4 + 64 * 4,
     "kv_quantize": 2 * (65536 * 8 * 128 * 2 + 65536 * 8 * 128 + 65536 * 8 * 4),
     "kv_dequantize": 2 * (65536 * 8 * 128 + 65536 * 8 * 4 + 65536 * 8 * 128 * 2),
+    # turbo4: per 128 values 64 bytes of codes and a 2-byte f16 norm, beside 256 bytes of f16 values, K and V.
+    "kv_turbo4_quantize": 2 * (65536 * 8 * 128 * 2 + 65536 * 8 * 64 + 65536 * 8 * 2),
+    "kv_turbo4_dequantize": 2 * (65536 * 8 * 64 + 65536 * 8 * 2 + 65536 * 8 * 128 * 2),
 }
 
 

@@ -106,6 +106,7 @@ _SIGS = {
     "xs_hip_dequantize_kv": [_P, _INT, _P, _P, _INT, _P, _I64, _I64],
     "xs_hip_copy": [_P, _P, _P, C.c_size_t],
     "xs_hip_copy_rows": [_P, _P, _I64, _P, _I64, _I64, _I64],
+    "xs_hip_kv_rotate": [_P, _P, _P, _I64, _I64, _INT],
     "xs_hip_attention_i8": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _F, _I64, _INT, _I64, _P],
     "xs_hip_attention_i8_split": [_I64, _I64, _I64],
     "xs_hip_attention_i8_scratch": [_I64, _I64, _I64, _I64],
@@ -485,6 +486,41 @@ def dequantize_kv(codes: DeviceTensor, scales: DeviceTensor, out_dtype: int = F1
     call("xs_hip_dequantize_kv", stream, KV_I8, C.c_void_p(codes.ptr), C.c_void_p(scales.ptr), out_dtype,
          C.c_void_p(out.ptr), rows, width)
     return out
+
+
+TURBO_FORMAT = {4: KV_TURBO4, 3: KV_TURBO3, 2: KV_TURBO2}
+
+
+def turbo_quantize(x: DeviceTensor, bits: int, stream=None) -> Tuple[DeviceTensor, DeviceTensor]:
+    """TurboQuant codes u8 [groups, 16 * bits] and f16 norms [groups] of x [..., width], width a multiple of 128
+    (quant::turbo::quantize_group, src/quant/kv_turbo.cpp:47-84)."""
+    width = x.shape[-1]
+    rows = x.numel // width
+    groups = rows * width // 128
+    codes = DeviceTensor.empty(U8, (groups, 16 * bits))
+    norms = DeviceTensor.empty(F16, (groups,))
+    call("xs_hip_quantize_kv", stream, TURBO_FORMAT[bits], x.dtype, C.c_void_p(x.ptr), C.c_void_p(codes.ptr),
+         C.c_void_p(norms.ptr), rows, width)
+    return codes, norms
+
+
+def turbo_dequantize(codes: DeviceTensor, norms: DeviceTensor, bits: int, out_dtype: int = F32,
+                     stream=None) -> DeviceTensor:
+    """The rotated values the groups store, [groups, 128] in out_dtype (quant::turbo::decode_group)."""
+    groups = codes.shape[0]
+    out = DeviceTensor.empty(out_dtype, (groups, 128))
+    call("xs_hip_dequantize_kv", stream, TURBO_FORMAT[bits], C.c_void_p(codes.ptr), C.c_void_p(norms.ptr), out_dtype,
+         C.c_void_p(out.ptr), groups, 128)
+    return out
+
+
+def kv_rotate(x: DeviceTensor, inverse: bool = False, stream=None) -> DeviceTensor:
+    """Each group of 128 f32 values rotated as the TurboQuant formats rotate rows, or rotated back
+    (quant::turbo::rotate_group, kv_turbo.cpp:118-129)."""
+    width = x.shape[-1]
+    y = DeviceTensor.empty(F32, x.shape)
+    call("xs_hip_kv_rotate", stream, C.c_void_p(x.ptr), C.c_void_p(y.ptr), x.numel // width, width, int(inverse))
+    return y
 
 
 def convert(x: DeviceTensor, y_dtype: int, stream=None) -> DeviceTensor:
