@@ -12,10 +12,11 @@
 // sycl_kernels.h:211-221; sycl_kv_cache.cpp:51-85, 96-106, 149-163).
 //
 // Layout: a group per 16 lanes, 8 consecutive values per lane (one 16-byte load of f16/bf16, two of f32), four groups
-// a wave. The butterflies of spans 1, 2, 4 run inside a lane; spans 8, 16, 32, 64 pair lane l with l ^ 1, 2, 4, 8 of
-// the same 16 (DPP quad permutations for 1 and 2, ds_swizzle for 4 and 8). The edge test compares the bit patterns of
-// non-negative floats as integers: k = bits(w^2) + (w >= 0), and edge j counts when bits(edge_j) < k -- w^2 >= edge for
-// a non-negative w, w^2 > edge for a negative one, in one integer compare. The magnitudes' squares and the centroids
+// a wave; a 16-lane set quantizes kQuantRounds groups in turn. The butterflies of spans 1, 2, 4 run inside a lane;
+// spans 8, 16, 32, 64 pair lane l with l ^ 1, 2, 4, 8 of the same 16 (DPP quad permutations for 1 and 2, ds_swizzle for
+// 4 and 8), one fused multiply-add each. The edge test compares the bit patterns of non-negative floats as integers:
+// k = bits(w^2) + (w >= 0), and edge j counts when bits(edge_j) < k -- w^2 >= edge for a non-negative w, w^2 > edge
+// for a negative one, in one integer compare -- and a binary search over the ascending edges finds the count. The magnitudes' squares and the centroids
 // come from LDS tables. Codes of a group: turbo4 a nibble per value (a lane's 8 codes are one 32-bit word), turbo2 two
 // bits per value (a lane's are one 16-bit word), turbo3 the turbo2 layout of the low two bits in bytes 0..31 and the
 // third bits as one byte per lane at 32 + lane (kv_turbo.h:84-87).
@@ -78,8 +79,9 @@ __device__ __forceinline__ float flip(float v, uint32_t mask) { return __uint_as
 // The value of lane l ^ M of this lane's 16 (M = 1, 2, 4, 8).
 template <int M>
 __device__ __forceinline__ float xlane(float v) {
-    if constexpr (M == 1) return dpp_f<dpp::kQuadXor1>(v);
-    else if constexpr (M == 2) return dpp_f<dpp::kQuadXor2>(v);
+    // The quad permutations as plain DPP moves (no old value to keep), which the compiler folds into their user.
+    if constexpr (M == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), dpp::kQuadXor1, 0xF, 0xF, true));
+    else if constexpr (M == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), dpp::kQuadXor2, 0xF, 0xF, true));
     else return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1f | (M << 10)));  // bit mode, xor M
 }
 
@@ -92,19 +94,19 @@ __device__ __forceinline__ float sum_lanes(float s) {
 }
 
 // Span 8 M of the butterflies: the lower lane of a pair takes a + b, the upper a - b (a the lower's value, b the
-// upper's), each as its own value negated or not plus the partner's.
+// upper's). Each lane computes own + t * partner with t = +1 (lower) or -1 (upper) in one fused multiply-add, exact
+// since t * partner is: the upper lane so holds b - a = -(a - b), its value negated (round to nearest even commutes
+// with negation). A lane's values thus come out of the four spans negated when an odd number of its lane bits is set;
+// the caller folds that sign into the flips after the transform.
 template <int M>
-__device__ __forceinline__ void cross_span(float* v, int lane) {
-    const uint32_t neg = (lane & M) ? 0x80000000u : 0u;
+__device__ __forceinline__ void cross_span(float* v, float t) {
 #pragma unroll
-    for (int e = 0; e < kLaneValues; ++e) {
-        const float p = xlane<M>(v[e]);
-        v[e] = p + flip(v[e], neg);
-    }
+    for (int e = 0; e < kLaneValues; ++e) v[e] = fmaf(xlane<M>(v[e]), t, v[e]);
 }
 
-// The unnormalized Walsh-Hadamard transform of a group, on this lane's 8 values.
-__device__ __forceinline__ void butterflies(float* v, int lane) {
+// The unnormalized Walsh-Hadamard transform of a group, on this lane's 8 values; returns the sign mask (bit 31) the
+// cross-lane spans left on them.
+__device__ __forceinline__ uint32_t butterflies(float* v, int lane) {
 #pragma unroll
     for (int h = 1; h < kLaneValues; h *= 2) {
 #pragma unroll
@@ -115,10 +117,11 @@ __device__ __forceinline__ void butterflies(float* v, int lane) {
             v[e + h] = a - b;
         }
     }
-    cross_span<1>(v, lane);
-    cross_span<2>(v, lane);
-    cross_span<4>(v, lane);
-    cross_span<8>(v, lane);
+    cross_span<1>(v, (lane & 1) ? -1.0f : 1.0f);
+    cross_span<2>(v, (lane & 2) ? -1.0f : 1.0f);
+    cross_span<4>(v, (lane & 4) ? -1.0f : 1.0f);
+    cross_span<8>(v, (lane & 8) ? -1.0f : 1.0f);
+    return static_cast<uint32_t>(__builtin_popcount(lane & 15) & 1) << 31;
 }
 
 template <typename X>
@@ -131,6 +134,9 @@ __device__ __forceinline__ void load_lane(const typename X::storage* x, float* v
     }
 }
 
+// Groups a 16-lane set quantizes in turn: its sign masks and tables are made once for all of them.
+constexpr int kQuantRounds = 4;
+
 template <int Bits, typename X>
 __global__ __launch_bounds__(kBlock) void turbo_quantize_kernel(const typename X::storage* __restrict__ x,
                                                                 uint8_t* __restrict__ codes,
@@ -140,56 +146,73 @@ __global__ __launch_bounds__(kBlock) void turbo_quantize_kernel(const typename X
     if (threadIdx.x < NM) mag_sq[threadIdx.x] = Book<Bits>::mags[threadIdx.x] * Book<Bits>::mags[threadIdx.x];
     __syncthreads();
     const int lane = threadIdx.x % kLanes;
-    const int64_t g = static_cast<int64_t>(blockIdx.x) * kGroupsPerBlock + threadIdx.x / kLanes;
-    if (g >= groups) return;  // whole 16-lane groups leave together
+    uint32_t before[kLaneValues], after[kLaneValues];
+    sign_masks(kSignsBefore, lane, before);
+    sign_masks(kSignsAfter, lane, after);
+    const uint32_t parity = static_cast<uint32_t>(__builtin_popcount(lane & 15) & 1) << 31;
+#pragma unroll
+    for (int e = 0; e < kLaneValues; ++e) after[e] ^= parity;  // the sign the cross-lane spans leave (butterflies)
 
-    float v[kLaneValues];
-    load_lane<X>(x + g * kGroup + lane * kLaneValues, v);
-    float n = 0.0f;
 #pragma unroll
-    for (int e = 0; e < kLaneValues; ++e) n = fmaf(v[e], v[e], n);
-    n = sum_lanes(n);
+    for (int round = 0; round < kQuantRounds; ++round) {
+        const int64_t g = (static_cast<int64_t>(blockIdx.x) * kQuantRounds + round) * kGroupsPerBlock +
+                          threadIdx.x / kLanes;
+        if (g >= groups) return;  // whole 16-lane groups leave together, and the later rounds are later groups
 
-    uint32_t mask[kLaneValues];
-    sign_masks(kSignsBefore, lane, mask);
+        float v[kLaneValues];
+        load_lane<X>(x + g * kGroup + lane * kLaneValues, v);
+        float n = 0.0f;
 #pragma unroll
-    for (int e = 0; e < kLaneValues; ++e) v[e] = flip(v[e], mask[e]);
-    butterflies(v, lane);
-    sign_masks(kSignsAfter, lane, mask);
+        for (int e = 0; e < kLaneValues; ++e) n = fmaf(v[e], v[e], n);
+        n = sum_lanes(n);
+#pragma unroll
+        for (int e = 0; e < kLaneValues; ++e) v[e] = flip(v[e], before[e]);
+        butterflies(v, lane);
 
-    uint32_t edge[NM - 1];
+        // The edges as bit patterns; a NaN in the group makes every edge test fail, as in f32: all-ones edges do
+        // that.
+        uint32_t edge[NM - 1];
 #pragma unroll
-    for (int j = 0; j < NM - 1; ++j) edge[j] = __float_as_uint(edge_sq<Bits>(j) * n);
-    const bool defined = n == n;  // a NaN in the group: every edge test fails, as in f32
-    uint32_t packed = 0, high = 0;
-    float r = 0.0f;
+        for (int j = 0; j < NM - 1; ++j) edge[j] = n == n ? __float_as_uint(edge_sq<Bits>(j) * n) : 0xffffffffu;
+        uint32_t packed = 0, high = 0;
+        float r = 0.0f;
 #pragma unroll
-    for (int e = 0; e < kLaneValues; ++e) {
-        const float w = flip(v[e], mask[e]);
-        const bool negative = w < 0.0f;
-        const uint32_t k = __float_as_uint(w * w) + (negative ? 0u : 1u);
-        uint32_t m = 0;
-#pragma unroll
-        for (int j = 0; j < NM - 1; ++j) m += edge[j] < k ? 1u : 0u;
-        m = defined ? m : 0u;
-        const uint32_t code = negative ? NM - 1 - m : NM + m;
-        if constexpr (Bits == 4) {
-            packed |= code << (4 * e);
-        } else {
-            packed |= (code & 3u) << (2 * e);
-            if constexpr (Bits == 3) high |= (code >> 2) << e;
+        for (int e = 0; e < kLaneValues; ++e) {
+            const float w = flip(v[e], after[e]);
+            const bool negative = w < 0.0f;
+            const uint32_t k = __float_as_uint(w * w) + (negative ? 0u : 1u);
+            // m = the count of edges below k: a binary search over the ascending edges.
+            uint32_t m;
+            if constexpr (Bits == 4) {
+                const bool c1 = edge[3] < k;
+                const bool c2 = (c1 ? edge[5] : edge[1]) < k;
+                const uint32_t t3 = c1 ? (c2 ? edge[6] : edge[4]) : (c2 ? edge[2] : edge[0]);
+                m = (c1 ? 4u : 0u) + (c2 ? 2u : 0u) + (t3 < k ? 1u : 0u);
+            } else if constexpr (Bits == 3) {
+                const bool c1 = edge[1] < k;
+                m = (c1 ? 2u : 0u) + ((c1 ? edge[2] : edge[0]) < k ? 1u : 0u);
+            } else {
+                m = edge[0] < k ? 1u : 0u;
+            }
+            const uint32_t code = negative ? NM - 1 - m : NM + m;
+            if constexpr (Bits == 4) {
+                packed |= code << (4 * e);
+            } else {
+                packed |= (code & 3u) << (2 * e);
+                if constexpr (Bits == 3) high |= (code >> 2) << e;
+            }
+            r += mag_sq[m];
         }
-        r += mag_sq[m];
+        r = sum_lanes(r);
+        uint8_t* gc = codes + g * (kGroup * Bits / 8);
+        if constexpr (Bits == 4) {
+            reinterpret_cast<uint32_t*>(gc)[lane] = packed;
+        } else {
+            reinterpret_cast<uint16_t*>(gc)[lane] = static_cast<uint16_t>(packed);
+            if constexpr (Bits == 3) gc[kGroup / 4 + lane] = static_cast<uint8_t>(high);
+        }
+        if (lane == 0) norms[g] = f32_to_f16(n > 0.0f ? sqrtf(n / r) : 0.0f);
     }
-    r = sum_lanes(r);
-    uint8_t* gc = codes + g * (kGroup * Bits / 8);
-    if constexpr (Bits == 4) {
-        reinterpret_cast<uint32_t*>(gc)[lane] = packed;
-    } else {
-        reinterpret_cast<uint16_t*>(gc)[lane] = static_cast<uint16_t>(packed);
-        if constexpr (Bits == 3) gc[kGroup / 4 + lane] = static_cast<uint8_t>(high);
-    }
-    if (lane == 0) norms[g] = f32_to_f16(n > 0.0f ? sqrtf(n / r) : 0.0f);
 }
 
 template <int Bits, typename Y>
@@ -248,30 +271,32 @@ __global__ __launch_bounds__(kBlock) void turbo_rotate_kernel(const float* __res
     sign_masks(inverse ? kSignsAfter : kSignsBefore, lane, mask);
 #pragma unroll
     for (int e = 0; e < kLaneValues; ++e) v[e] = flip(v[e], mask[e]);
-    butterflies(v, lane);
+    const uint32_t parity = butterflies(v, lane);
     sign_masks(inverse ? kSignsBefore : kSignsAfter, lane, mask);
 #pragma unroll
-    for (int e = 0; e < kLaneValues; ++e) v[e] = flip(v[e] * 0.08838834764831845f, mask[e]);
+    for (int e = 0; e < kLaneValues; ++e) v[e] = flip(v[e] * 0.08838834764831845f, mask[e] ^ parity);
     float* yl = y + g * kGroup + lane * kLaneValues;
     st128(yl, pack<F32>(v));
     st128(yl + 4, pack<F32>(v + 4));
 }
 
-unsigned blocks_for(int64_t groups) { return static_cast<unsigned>((groups + kGroupsPerBlock - 1) / kGroupsPerBlock); }
+unsigned blocks_for(int64_t groups, int rounds = 1) {
+    return static_cast<unsigned>((groups + kGroupsPerBlock * rounds - 1) / (kGroupsPerBlock * rounds));
+}
 
 template <int Bits>
 int quantize_bits(hipStream_t s, xs_dtype x_dtype, const void* x, uint8_t* codes, uint16_t* norms, int64_t groups) {
     switch (x_dtype) {
         case XS_F32:
-            turbo_quantize_kernel<Bits, F32><<<blocks_for(groups), kBlock, 0, s>>>(static_cast<const float*>(x), codes,
+            turbo_quantize_kernel<Bits, F32><<<blocks_for(groups, kQuantRounds), kBlock, 0, s>>>(static_cast<const float*>(x), codes,
                                                                                    norms, groups);
             break;
         case XS_F16:
-            turbo_quantize_kernel<Bits, F16><<<blocks_for(groups), kBlock, 0, s>>>(static_cast<const uint16_t*>(x),
+            turbo_quantize_kernel<Bits, F16><<<blocks_for(groups, kQuantRounds), kBlock, 0, s>>>(static_cast<const uint16_t*>(x),
                                                                                    codes, norms, groups);
             break;
         case XS_BF16:
-            turbo_quantize_kernel<Bits, BF16><<<blocks_for(groups), kBlock, 0, s>>>(static_cast<const uint16_t*>(x),
+            turbo_quantize_kernel<Bits, BF16><<<blocks_for(groups, kQuantRounds), kBlock, 0, s>>>(static_cast<const uint16_t*>(x),
                                                                                     codes, norms, groups);
             break;
         default:
