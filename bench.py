@@ -272,6 +272,32 @@ def op_argmax():
     return Op("argmax", W.ALGO_BYTES["argmax"], width * 4, mk, go, 2, "argmax_chunks")
 
 
+# Top-k shapes of the reference's callers (models/common/blocks.cpp:29-52, models/drafters/dflash.cpp:362): a
+# drafter's shortlist of a vocabulary (--draft-shortlist 64), MoE routers, a drafter's candidates per draft.
+TOPK_SHAPES = {"topk_shortlist": (1, 151936, 64), "topk_moe_router": (2048, 128, 8),
+               "topk_draft_candidates": (16, 151936, 8)}
+
+
+def op_topk(name):
+    rows, width, k = TOPK_SHAPES[name]
+    rng = np.random.default_rng(0x5EED0007)
+    x0 = X.DeviceTensor.from_numpy((rng.standard_normal((rows, width)) * 2).astype(np.float32))
+    nscratch = X.lib().xs_hip_topk_scratch(rows, width, k)
+
+    def mk():
+        sc = X.DeviceBuffer(max(nscratch, 1))
+        s = (dcopy(x0), X.DeviceTensor.empty(X.F32, (rows, k)), X.DeviceTensor.empty(X.I32, (rows, k)), sc)
+        need(s[0], rows * width * 4, name)
+        return s
+
+    def go(s, stream):
+        x, v, i, sc = s
+        X.call("xs_hip_topk", stream, vp(x), vp(v), vp(i), rows, width, k, C.c_void_p(sc.ptr if nscratch else 0))
+    nbytes = rows * width * 4 + rows * k * 8
+    wide = nscratch > 0  # clear, histogram, compact, finish; else a wave per row
+    return Op(name, nbytes, nbytes, mk, go, 4 if wide else 1, "topk_wide_compact" if wide else "topk_wave_rows")
+
+
 def op_rope(separate=False):
     a = W.config3().arrays
     tokens, qh, dim = a["q"].shape
@@ -430,7 +456,8 @@ def op_copy(n=256 << 20):
 
 OP_ORDER = ["swiglu_bias", "swiglu_bias_strided", "rmsnorm_residual", "softmax_masked", "argmax", "rope_qk",
             "rope_qk_separate", "kv_quantize", "kv_dequantize", "attention_i8_decode", "layer_norm", "l2_clip",
-            "reduce_sum_rows", "reduce_sum_cols", "unary_softcap", "kv_turbo4_quantize", "kv_turbo4_dequantize"]
+            "reduce_sum_rows", "reduce_sum_cols", "unary_softcap", "kv_turbo4_quantize", "kv_turbo4_dequantize",
+            "topk_shortlist", "topk_moe_router", "topk_draft_candidates"]
 
 
 def build_ops(only):
@@ -449,7 +476,10 @@ def build_ops(only):
                "layer_norm": lambda: op_row_norms("layer_norm"), "l2_clip": lambda: op_row_norms("l2_clip"),
                "reduce_sum_rows": lambda: op_row_norms("reduce_sum_rows"),
                "reduce_sum_cols": lambda: op_row_norms("reduce_sum_cols"),
-               "kv_turbo4_quantize": lambda: op_kv_turbo(kv), "kv_turbo4_dequantize": lambda: op_kv_turbo(kv, True)}[name]()
+               "kv_turbo4_quantize": lambda: op_kv_turbo(kv), "kv_turbo4_dequantize": lambda: op_kv_turbo(kv, True),
+               "topk_shortlist": lambda: op_topk("topk_shortlist"),
+               "topk_moe_router": lambda: op_topk("topk_moe_router"),
+               "topk_draft_candidates": lambda: op_topk("topk_draft_candidates")}[name]()
 
 
 # ---------------------------------------------------------------------------------------------------------------

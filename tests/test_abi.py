@@ -116,4 +116,7 @@ def test_softmax_scratch_sizes():
 def test_topk_scratch_sizes():
     assert L().xs_hip_topk_scratch(1, 1024, 1) == 0          # one chunk: no scratch
     assert L().xs_hip_topk_scratch(1, 151936, 1) >= 149 * 8 + 4
-    assert L().xs_hip_topk_scratch(4, 151936, 5) == 0        # k > 1 selects in one block per row
+    row = (2048 + 64) * 4 + 4096 * 8                           # bins, counters and a 4096-candidate list per row
+    assert L().xs_hip_topk_scratch(4, 151936, 5) == 4 * row    # wide rows, k > 1: histogram, threshold, compact
+    assert L().xs_hip_topk_scratch(4, 4096, 64) == 0           # a wave per row holds the whole row
+    assert L().xs_hip_topk_scratch(4, 151936, 1025) == 0       # past 1024 picks: k passes in one block per row

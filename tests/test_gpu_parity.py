@@ -459,6 +459,106 @@ def test_topk_k_gt_1(ora):
         assert_exact(v.numpy(), wv)
 
 
+def topk_case(rng, rows, width, kind):
+    if kind == "gauss":
+        return (rng.standard_normal((rows, width)) * 2).astype(np.float32)
+    if kind == "ties":  # few distinct values: crowded bins and long runs of exact ties
+        return rng.integers(-3, 4, (rows, width)).astype(np.float32)
+    x = rng.standard_normal((rows, width)).astype(np.float32)
+    if kind == "signed_zeros":
+        x = -np.abs(x)
+        x[:, ::7] = 0.0  # the largest values are zeros of both signs
+        x[:, 3::7] = -0.0
+    elif kind == "nan":
+        x[:, ::3] = np.nan
+        x[0, :] = np.nan  # a row of NaN only: index 0 and x[0] for every place
+        x[-1, 5:] = np.nan  # five non-NaN values: the rest of the places as above
+    return x
+
+
+def topk_skipping_nan(x, k):
+    """Rows holding NaN, where cpu-ref's partial_sort comparator is no strict weak order and its result unspecified:
+    the kernels' rule is cpu-ref's order over the non-NaN values, then index 0 and x[0] for places left over."""
+    rows, width = x.shape
+    values = np.empty((rows, k), np.float32)
+    indices = np.zeros((rows, k), np.int32)
+    for r in range(rows):
+        ok = np.flatnonzero(~np.isnan(x[r]))
+        order = ok[np.lexsort((ok, -x[r, ok].astype(np.float64)))][:k]
+        indices[r, : len(order)] = order
+        values[r] = x[r, indices[r]]
+    return values, indices
+
+
+def test_topk_nan_rule_matches_oracle_without_nan(ora):
+    """The NaN rule above is cpu-ref's order where a row has no NaN (ties and signed zeros included)."""
+    rng = np.random.default_rng(5)
+    x = rng.integers(-3, 4, (4, 300)).astype(np.float32)
+    x[:, ::5] = -0.0
+    for a, b in zip(topk_skipping_nan(x, 40), ora.topk(x, 40)):
+        assert_exact(a, b)
+
+
+@pytest.mark.parametrize("rows,width,k,kind", [
+    (1, 151936, 64, "gauss"),      # a drafter's shortlist of the vocabulary (--draft-shortlist 64)
+    (16, 151936, 8, "gauss"),      # a drafter's candidates per draft
+    (3, 40000, 5, "gauss"),
+    (2, 20000, 1000, "gauss"),     # past 512 candidates: the bitonic sort
+    (2, 9000, 16, "ties"),         # ties across a bitonic sort of the candidates
+    (3, 40000, 16, "ties"),        # a bin past 4096 candidates: the k-pass fallback
+    (3, 10000, 40, "signed_zeros"),
+    (3, 8192, 12, "nan"),
+    (2048, 128, 8, "gauss"),       # MoE routers, a wave per row
+    (33, 4096, 64, "ties"),
+    (7, 1, 1, "gauss"),
+    (5, 65, 65, "nan"),
+])
+def test_topk_shapes(ora, rows, width, k, kind):
+    """General top-k against cpu-ref's partial_sort (values and indices exact, ties to the lower index; NaN never
+    picked, index 0 and x[0] for places a row cannot fill) on the reference callers' shapes and adversarial rows."""
+    rng = np.random.default_rng(rows * 31 + width + k)
+    x = topk_case(rng, rows, width, kind)
+    step(f"topk [{rows}, {width}] k {k} {kind}")
+    v, i = X.topk(dev(x), k)
+    wv, wi = ora.topk(x, k) if kind != "nan" else topk_skipping_nan(x, k)
+    assert_exact(i.numpy(), wi, f"indices [{rows}, {width}] k {k} {kind}")
+    assert_exact(v.numpy(), wv, f"values [{rows}, {width}] k {k} {kind}")
+
+
+def test_topk_reference_kats(ora):
+    """tests/unit/backend/moe_ops_cases.h:76-122: indices 3 before 11 on a tie; {100, 700, 1900}; {5, 6, 300,
+    20000, 39999} on a row of 40,000."""
+    x = np.zeros((1, 16), np.float32)
+    x[0, 3] = x[0, 11] = 2.0
+    step("topk KAT tie 3 before 11")
+    assert list(X.topk(dev(x), 2)[1].numpy()[0]) == [3, 11]
+    x = np.linspace(-1, 0, 2000, dtype=np.float32)[None, :].copy()
+    x[0, [100, 700, 1900]] = [5.0, 4.0, 3.0]
+    assert list(X.topk(dev(x), 3)[1].numpy()[0]) == [100, 700, 1900]
+    x = np.full((1, 40000), -1.0, np.float32)
+    picks = [5, 6, 300, 20000, 39999]
+    x[0, picks] = [9.0, 8.0, 7.0, 6.0, 5.0]
+    step("topk KAT width 40000")
+    v, i = X.topk(dev(x), 5)
+    assert list(i.numpy()[0]) == picks
+    assert list(v.numpy()[0]) == [9.0, 8.0, 7.0, 6.0, 5.0]
+    # The reference's very wide rows: five tied 4.0s, 90 near-3.0s in one block, and a second row whose largest sit
+    # in its last 30 places; 64 picks.
+    rng = np.random.default_rng(32)
+    huge = rng.uniform(-1, 1, (2, 40000)).astype(np.float32)
+    huge[0, [5, 6, 300, 39999, 20000]] = 4.0
+    at = np.arange(1024, 1024 + 90)
+    huge[0, at] = (3.0 - 0.001 * (at % 7)).astype(np.float32)
+    at = np.arange(40000 - 30, 40000)
+    huge[1, at] = (5.0 + (at % 3)).astype(np.float32)
+    step("topk KAT two rows of 40000, k 64")
+    v, i = X.topk(dev(huge), 64)
+    wv, wi = ora.topk(huge, 64)
+    assert_exact(i.numpy(), wi, "indices")
+    assert_exact(v.numpy(), wv, "values")
+    assert list(i.numpy()[0, :5]) == picks
+
+
 # ---------------------------------------------------------------------------------------------------------------
 # RoPE
 
