@@ -212,8 +212,8 @@ size_t xs_hip_topk_scratch(int64_t rows, int64_t width, int64_t k);
 /* The k largest per row of x [rows, width] f32: values f32 and indices i32 [rows, k], largest first, equal values keep
  * the lower index first (cpu_ref::topk, ops.cpp:663-684; spec graph.h:70-71). k = 1 is argmax (blocks::argmax_rows,
  * blocks.cpp:36-38). `scratch` (8-byte aligned, any contents) holds xs_hip_topk_scratch bytes: for k = 1 the per-chunk
- * partials of wide rows, for 1 < k <= 1024 on rows wider than 4096 a per-row histogram of the order keys' top 11 bits,
- * counters and the candidates at or above the k-th key's bin; concurrent calls must not share one. Replaces sycl_be::topk
+ * partials of wide rows, for 1 < k <= 1024 on rows wider than 4096 each 4096-value chunk's threshold bin, candidate
+ * count and candidates (room for max(256, 4k) words); concurrent calls must not share one. Replaces sycl_be::topk
  * (sycl_kernels.h:62-63). */
 int xs_hip_topk(void* stream, const float* x, float* values, int32_t* indices, int64_t rows, int64_t width, int64_t k,
                 void* scratch);

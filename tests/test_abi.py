@@ -116,7 +116,8 @@ def test_softmax_scratch_sizes():
 def test_topk_scratch_sizes():
     assert L().xs_hip_topk_scratch(1, 1024, 1) == 0          # one chunk: no scratch
     assert L().xs_hip_topk_scratch(1, 151936, 1) >= 149 * 8 + 4
-    row = (2048 + 64) * 4 + 4096 * 8                           # bins, counters and a 4096-candidate list per row
-    assert L().xs_hip_topk_scratch(4, 151936, 5) == 4 * row    # wide rows, k > 1: histogram, threshold, compact
+    chunks = (151936 + 4095) // 4096                           # a {bound, count} header and a candidate slot per chunk
+    assert L().xs_hip_topk_scratch(4, 151936, 5) == 4 * chunks * (16 + 256 * 8)
+    assert L().xs_hip_topk_scratch(1, 151936, 1000) == chunks * (16 + 4000 * 8)
     assert L().xs_hip_topk_scratch(4, 4096, 64) == 0           # a wave per row holds the whole row
     assert L().xs_hip_topk_scratch(4, 151936, 1025) == 0       # past 1024 picks: k passes in one block per row

@@ -507,6 +507,11 @@ def test_topk_nan_rule_matches_oracle_without_nan(ora):
     (2, 9000, 16, "ties"),         # ties across a bitonic sort of the candidates
     (3, 40000, 16, "ties"),        # a bin past 4096 candidates: the k-pass fallback
     (3, 10000, 40, "signed_zeros"),
+    (4, 30000, 300, "gauss"),      # 128 < k: narrowed to exactly k, then sorted
+    (2, 50000, 64, "ties"),
+    (1, 9_000_000, 100, "gauss"),  # past 2048 chunks: candidates gathered from the bound up
+    (1, 2048 * 4096, 50, "gauss"), # exactly 2048 chunks: the last that the prefix search covers
+    (2, 33 * 4096, 64, "gauss"),   # chunks - 1 a power of two
     (3, 8192, 12, "nan"),
     (2048, 128, 8, "gauss"),       # MoE routers, a wave per row
     (33, 4096, 64, "ties"),

@@ -17,9 +17,10 @@
 // workgroups.
 // k > 1, rows up to 4096 wide (MoE routers, centroids): a wave per row holds the row in registers and picks the k
 // winners one after another, each the wave's largest remaining element. Wider rows (a shortlist of a vocabulary, a
-// drafter's candidates): a histogram of the row's top 11 key bits finds the bin of the k-th largest, everything from
-// that bin up is compacted (a few hundred elements, typically), and one workgroup ranks those; a row whose bin is too
-// crowded, or that holds fewer than k non-NaN values, is selected by k passes over it, with the same result.
+// drafter's candidates): each 4096-value chunk keeps the words from the bin of its own k-th largest up (an LDS
+// histogram of the order words' top 11 bits), and one workgroup per row ranks the kept words from the largest of those
+// bins up -- a few hundred, typically; a row with crowded bins, or with fewer than k non-NaN values, is selected by k
+// passes over it, with the same result.
 #include <cfloat>
 #include <climits>
 
@@ -202,10 +203,13 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 }
 
 // Writes pick j of a row: the element named by word w, or (no element left: fewer than k non-NaN values) index 0 and
-// x[0], as the k-pass selection reports it.
+// x[0], as the k-pass selection reports it. The value comes back from the word's key, which maps float bits one to
+// one except +0 and -0 (one key): only then, or with no element, is x read for the element's own bits.
 __device__ __forceinline__ void put_pick(const float* xr, float* values, int32_t* indices, int64_t at, uint64_t w) {
     const int32_t i = w == 0 ? 0 : word_index(w);
-    values[at] = xr[i];  // the element's own bits (-0 stays -0)
+    const uint32_t key = static_cast<uint32_t>(w >> 32);
+    const uint32_t bits = (key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key;
+    values[at] = w == 0 || bits == 0 ? xr[i] : __uint_as_float(bits);
     indices[at] = i;
 }
 
@@ -243,32 +247,39 @@ __global__ __launch_bounds__(kBlock) void topk_wave_rows(const float* __restrict
     }
 }
 
-// Wide rows: the k-th largest word's top 11 bits (its bin) from a histogram of the row, then every element of that
-// bin or above compacted as a candidate -- usually a few hundred -- and those ranked. Per row in scratch: the bins,
-// the candidate count, the candidates. A row whose candidates overflow (a crowded bin) or that holds fewer than k
-// non-NaN values is selected by k passes over it instead (topk_passes), with the same result.
-constexpr int kBins = 2048;
-constexpr int kCap = 4096;
-constexpr int kWideChunk = kBlock * 16;  // values per workgroup of the histogram and compaction passes
+// Wide rows: a workgroup per chunk of kWideChunk values computes a lower bound T on the chunk's k-th largest word and
+// writes every word >= T (the chunk's candidates) to its slot in scratch, with T and their count. T is the k-th
+// largest of the workgroup's per-thread maxima when there are at least k of those (k distinct words are >= it), else
+// the k-th largest of all the chunk's words; either is found by an LDS histogram over the 11 bits just below the
+// highest bit where the histogrammed words differ, so the words spread over the bins. The row's k-th largest word is
+// at least every chunk's, so every word of the row's top k is at least G = max T and sits among its chunk's
+// candidates. A workgroup per row gathers the candidates >= G into LDS and narrows them by more such histograms to the
+// words from the k-th largest's bin up, then ranks those. A row whose chunk overflows its slot or whose gathered
+// candidates overflow LDS (crowded values), or that holds fewer than k non-NaN values, is selected by k passes over
+// it instead (topk_passes), with the same result. Every scratch word read is written earlier in the same call, so
+// scratch needs no clearing.
+constexpr int kBins = 2048;  // 11 bits
+constexpr int kCap = 4096;   // candidates gathered in LDS
+constexpr int kWideChunk = kBlock * 16;
 constexpr int64_t kWideMaxK = 1024;
-constexpr size_t kRowScratch = (kBins + 64) * 4 + kCap * 8;  // bins, count (+ padding to 256 bytes), candidates
+constexpr uint32_t kRankMax = 128;  // ranked directly; more are narrowed, or bitonic-sorted at the last bit
+constexpr int kGatherUnroll = 8;    // chunks a wave reads at once
 
-struct WideRow {
-    uint32_t* bins;
-    uint32_t* count;
-    uint64_t* cand;
+// Candidate slot per chunk: room for 4k words (at least 256, at most the chunk).
+__host__ __device__ constexpr int64_t chunk_cap(int64_t k) {
+    return k * 4 < 256 ? 256 : (k * 4 > kWideChunk ? kWideChunk : k * 4);
+}
+int64_t wide_chunks(int64_t width) { return (width + kWideChunk - 1) / kWideChunk; }
+// Per row: a header {T, count} (16 bytes) per chunk, then the chunks' candidate slots.
+constexpr size_t kHeaderBytes = 16;
+__host__ __device__ constexpr size_t wide_row_bytes(int64_t chunks, int64_t k) {
+    return static_cast<size_t>(chunks) * (kHeaderBytes + static_cast<size_t>(chunk_cap(k)) * 8);
+}
+struct ChunkHeader {
+    uint64_t bound;   // candidates are the words >= bound
+    uint32_t count;   // candidates, stored or not
+    uint32_t top;     // the chunk's largest value key (0: no non-NaN value)
 };
-__device__ __forceinline__ WideRow wide_row(void* scratch, int64_t row) {
-    char* base = static_cast<char*>(scratch) + row * kRowScratch;
-    return {reinterpret_cast<uint32_t*>(base), reinterpret_cast<uint32_t*>(base) + kBins,
-            reinterpret_cast<uint64_t*>(base + (kBins + 64) * 4)};
-}
-
-__global__ __launch_bounds__(kBlock) void topk_wide_clear(void* scratch) {
-    const WideRow r = wide_row(scratch, blockIdx.x);
-    for (int b = threadIdx.x; b < kBins; b += kBlock) r.bins[b] = 0;
-    if (threadIdx.x == 0) *r.count = 0;
-}
 
 // The element words of this workgroup's chunk, 16 a thread (four 4-value groups kBlock apart: each load instruction
 // covers consecutive values).
@@ -288,76 +299,235 @@ __device__ __forceinline__ void chunk_words(const float* xr, int64_t width, int6
     }
 }
 
-__global__ __launch_bounds__(kBlock) void topk_wide_hist(const float* __restrict__ x, int64_t width, bool vec,
-                                                         void* scratch) {
-    __shared__ uint32_t bins[kBins];
-    for (int b = threadIdx.x; b < kBins; b += kBlock) bins[b] = 0;
-    __syncthreads();
-    const int64_t row = blockIdx.y;
-    uint64_t w[16];
-    chunk_words(x + row * width, width, static_cast<int64_t>(blockIdx.x) * kWideChunk, vec, w);
+// Inclusive prefix sum over the block's threads (in thread order); every thread gets its own.
+__device__ __forceinline__ uint32_t block_inclusive_scan(uint32_t v) {
+    __shared__ uint32_t wsum[kBlock / 64];
+    const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int e = 0; e < 16; ++e)
-        if (w[e] != 0) atomicAdd(&bins[word_bin(w[e])], 1u);
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = __shfl_up(v, off, 64);
+        v += lane >= off ? o : 0u;
+    }
+    if (lane == 63) wsum[threadIdx.x >> 6] = v;
     __syncthreads();
-    const WideRow r = wide_row(scratch, row);
-    for (int b = threadIdx.x; b < kBins; b += kBlock)
-        if (bins[b] != 0) atomicAdd(&r.bins[b], bins[b]);
+    for (int q = 0; q < static_cast<int>(threadIdx.x >> 6); ++q) v += wsum[q];
+    __syncthreads();
+    return v;
 }
 
-// The bin of the k-th largest word: the largest b whose bins b .. top hold at least k elements (0 when the row holds
-// fewer than k: then everything is a candidate, and the final pass sees too few or too many).
-__device__ uint32_t threshold_bin(const uint32_t* gbins, int64_t k) {
+// The largest and smallest of the block's words v that are nonzero (hi = 0 when there are none); every thread gets
+// them.
+__device__ __forceinline__ void block_range(uint64_t hi_v, uint64_t lo_v, uint64_t& hi, uint64_t& lo) {
+    __shared__ uint64_t his[kBlock / 64], los[kBlock / 64];
+    hi_v = wave_max_u64(hi_v);
+    lo_v = ~wave_max_u64(~lo_v);
+    if ((threadIdx.x & 63) == 0) {
+        his[threadIdx.x >> 6] = hi_v;
+        los[threadIdx.x >> 6] = lo_v;
+    }
+    __syncthreads();
+    hi = his[0];
+    lo = los[0];
+    for (int q = 1; q < kBlock / 64; ++q) {
+        hi = his[q] > hi ? his[q] : hi;
+        lo = los[q] < lo ? los[q] : lo;
+    }
+    __syncthreads();
+}
+
+// The bin of the k-th largest word counted in `bins`, or -1 when they hold fewer than k; *above gets the count of
+// words in the bins above it.
+__device__ int threshold_bin(const uint32_t* bins, int64_t k, uint32_t* above) {
     constexpr int PER = kBins / kBlock;  // bins a thread, counted from the top
-    __shared__ uint32_t part[kBlock];
-    __shared__ uint32_t found;
+    __shared__ int found;
+    __shared__ uint32_t found_above;
     const int t = threadIdx.x;
     uint32_t c[PER];
     uint32_t sum = 0;
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
-        c[q] = gbins[kBins - 1 - (t * PER + q)];
+        c[q] = bins[kBins - 1 - (t * PER + q)];
         sum += c[q];
     }
-    part[t] = sum;
-    if (t == 0) found = 0;
-    __syncthreads();
-    // Exclusive prefix over the threads (a few thousand at most: serial over a wave, then per thread)
-    uint64_t before = 0;
-    for (int u = 0; u < t; ++u) before += part[u];
-    if (before < static_cast<uint64_t>(k) && before + sum >= static_cast<uint64_t>(k)) {
+    if (t == 0) {
+        found = -1;
+        found_above = 0;
+    }
+    const uint32_t incl = block_inclusive_scan(sum);  // its barriers also order `found`
+    const uint64_t before = incl - sum;
+    if (before < static_cast<uint64_t>(k) && incl >= static_cast<uint64_t>(k)) {
         uint64_t acc = before;
+#pragma unroll
         for (int q = 0; q < PER; ++q) {
-            acc += c[q];
-            if (acc >= static_cast<uint64_t>(k)) {
-                found = static_cast<uint32_t>(kBins - 1 - (t * PER + q));
-                break;
+            if (acc < static_cast<uint64_t>(k) && acc + c[q] >= static_cast<uint64_t>(k)) {
+                found = kBins - 1 - (t * PER + q);
+                found_above = static_cast<uint32_t>(acc);
             }
+            acc += c[q];
         }
     }
     __syncthreads();
+    *above = found_above;
     return found;
 }
 
-__global__ __launch_bounds__(kBlock) void topk_wide_compact(const float* __restrict__ x, int64_t width, bool vec,
-                                                            int64_t k, void* scratch) {
+// The histogram window for words in [lo, hi] (hi != lo): they share every bit from `top` up; the window is the 11 (or
+// fewer) bits below it.
+struct Window {
+    int top, bottom;
+};
+__device__ __forceinline__ Window window_of(uint64_t hi, uint64_t lo) {
+    const int top = 64 - __builtin_clzll(hi ^ lo);
+    return {top, top > 11 ? top - 11 : 0};
+}
+__device__ __forceinline__ uint32_t window_bin(uint64_t w, Window win) {
+    return static_cast<uint32_t>(w >> win.bottom) & ((1u << (win.top - win.bottom)) - 1u);
+}
+// The smallest word with the shared bits of `like` from win.top up and bin b in the window.
+__device__ __forceinline__ uint64_t window_floor(uint64_t like, Window win, uint32_t b) {
+    const uint64_t shared = win.top >= 64 ? 0 : (like >> win.top) << win.top;
+    return shared | (static_cast<uint64_t>(b) << win.bottom);
+}
+
+// Largest / smallest u32 over the wave; every lane gets it.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, static_cast<uint32_t>(dpp_i<dpp::kQuadXor1>(static_cast<int>(v))));
+    v = max(v, static_cast<uint32_t>(dpp_i<dpp::kQuadXor2>(static_cast<int>(v))));
+    v = max(v, static_cast<uint32_t>(dpp_i<dpp::kRowHalfMirror>(static_cast<int>(v))));
+    v = max(v, static_cast<uint32_t>(dpp_i<dpp::kRowMirror>(static_cast<int>(v))));
+    v = max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), 16, 64)));
+    return max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), 32, 64)));
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) { return ~wave_max_u32(~v); }
+
+// 32-bit windows over value keys (the high half of a word): the bits below the highest where hi and lo differ.
+__device__ __forceinline__ Window window_of32(uint32_t hi, uint32_t lo) {
+    const int top = 32 - __builtin_clz(hi ^ lo);
+    return {top, top > 11 ? top - 11 : 0};
+}
+__device__ __forceinline__ uint32_t window_bin32(uint32_t key, Window win) {
+    return (key >> win.bottom) & ((1u << (win.top - win.bottom)) - 1u);
+}
+
+// Each lane's exclusive prefix of c (0..31) over the wave, and the wave's total, from c's bit planes.
+__device__ __forceinline__ uint32_t wave_exclusive_small(uint32_t c, uint32_t& total) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t below = (uint64_t{1} << lane) - 1;
+    uint32_t before = 0;
+    total = 0;
+#pragma unroll
+    for (int bit = 0; bit < 5; ++bit) {
+        const uint64_t plane = __ballot((c >> bit) & 1u);
+        before += static_cast<uint32_t>(__popcll(plane & below)) << bit;
+        total += static_cast<uint32_t>(__popcll(plane)) << bit;
+    }
+    return before;
+}
+
+// grid (chunks, rows): the chunk's bound, count and candidates. The bound is a value key (the high half of a word):
+// every word with a key at or above it is a candidate.
+__global__ __launch_bounds__(kBlock) void topk_wide_chunks(const float* __restrict__ x, int64_t width, bool vec,
+                                                           int64_t k, void* scratch) {
+    __shared__ uint32_t bins[kBins];
+    __shared__ uint32_t wave_nz[kBlock / 64], wave_hi[kBlock / 64], wave_lo_max[kBlock / 64],
+        wave_lo_all[kBlock / 64];
+    __shared__ uint32_t n;
+    for (int b = threadIdx.x; b < kBins; b += kBlock) bins[b] = 0;
+    if (threadIdx.x == 0) n = 0;
     const int64_t row = blockIdx.y;
-    const WideRow r = wide_row(scratch, row);
-    const uint32_t bin = threshold_bin(r.bins, k);
+    const int64_t chunks = gridDim.x;
+    const int64_t cap = chunk_cap(k);
+    const int wave = threadIdx.x >> 6;
     uint64_t w[16];
     chunk_words(x + row * width, width, static_cast<int64_t>(blockIdx.x) * kWideChunk, vec, w);
-    const int lane = threadIdx.x & 63;
+    uint32_t m = 0, lo_all = ~0u;  // value keys: the thread's largest, the smallest of its non-NaN ones
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-        const bool keep = w[e] != 0 && word_bin(w[e]) >= bin;
-        const uint64_t mask = __ballot(keep);
-        if (mask == 0) continue;
-        uint32_t base = 0;
-        if (lane == __builtin_ctzll(mask)) base = atomicAdd(r.count, static_cast<uint32_t>(__popcll(mask)));
-        base = __shfl(base, __builtin_ctzll(mask), 64);
-        const uint32_t slot = base + static_cast<uint32_t>(__popcll(mask & ((uint64_t{1} << lane) - 1)));
-        if (keep && slot < kCap) r.cand[slot] = w[e];
+        const uint32_t key = static_cast<uint32_t>(w[e] >> 32);
+        m = key > m ? key : m;
+        lo_all = key != 0 && key < lo_all ? key : lo_all;
     }
+    {
+        const uint32_t nz = static_cast<uint32_t>(__popcll(__ballot(m != 0)));
+        const uint32_t hi = wave_max_u32(m);
+        const uint32_t lo_max = wave_min_u32(m != 0 ? m : ~0u);
+        const uint32_t lo_a = wave_min_u32(lo_all);
+        if ((threadIdx.x & 63) == 0) {
+            wave_nz[wave] = nz;
+            wave_hi[wave] = hi;
+            wave_lo_max[wave] = lo_max;
+            wave_lo_all[wave] = lo_a;
+        }
+    }
+    __syncthreads();
+    uint32_t nz = 0, hi = 0, lo_max = ~0u, lo_a = ~0u;
+#pragma unroll
+    for (int q = 0; q < kBlock / 64; ++q) {
+        nz += wave_nz[q];
+        hi = max(hi, wave_hi[q]);
+        lo_max = min(lo_max, wave_lo_max[q]);
+        lo_a = min(lo_a, wave_lo_all[q]);
+    }
+    // The k-th largest per-thread maximum bounds the chunk's k-th largest when there are k maxima; else all words.
+    const bool by_max = k <= kBlock && nz >= static_cast<uint64_t>(k);  // uniform
+    const uint32_t lo = by_max ? lo_max : lo_a;
+    // With one distinct key, every histogrammed word has it: the k maxima, or all the non-NaN words.
+    uint32_t bound = hi != 0 && hi == lo ? hi : 0;  // 0: keep every non-NaN word
+    if (hi != 0 && hi != lo) {  // uniform
+        const Window win = window_of32(hi, lo);
+        if (by_max) {
+            if (m != 0) atomicAdd(&bins[window_bin32(m, win)], 1u);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const uint32_t key = static_cast<uint32_t>(w[e] >> 32);
+                if (key != 0) atomicAdd(&bins[window_bin32(key, win)], 1u);
+            }
+        }
+        __syncthreads();
+        uint32_t above;
+        const int b = threshold_bin(bins, k, &above);
+        if (b >= 0) bound = ((win.top >= 32 ? 0u : (hi >> win.top) << win.top)) | (static_cast<uint32_t>(b) << win.bottom);
+    }
+    uint32_t mine = 0;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) mine += w[e] != 0 && static_cast<uint32_t>(w[e] >> 32) >= bound ? 1u : 0u;
+    uint32_t wave_total;
+    const uint32_t before = wave_exclusive_small(mine, wave_total);
+    uint32_t base_at = 0;
+    if ((threadIdx.x & 63) == 0 && wave_total != 0) base_at = atomicAdd(&n, wave_total);
+    base_at = static_cast<uint32_t>(__shfl(static_cast<int>(base_at), 0, 64));
+    char* base = static_cast<char*>(scratch) + row * wide_row_bytes(chunks, k);
+    uint64_t* cand = reinterpret_cast<uint64_t*>(base + chunks * kHeaderBytes) + blockIdx.x * cap;
+    uint32_t at = base_at + before;
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+        if (w[e] != 0 && static_cast<uint32_t>(w[e] >> 32) >= bound) {
+            if (at < cap) cand[at] = w[e];
+            ++at;
+        }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        ChunkHeader h;
+        h.bound = static_cast<uint64_t>(bound) << 32;
+        h.count = n;
+        h.top = hi;
+        reinterpret_cast<ChunkHeader*>(base)[blockIdx.x] = h;
+    }
+}
+
+// Appends the words with keep set to out[..cap) at the LDS counter n (one atomic per wave); n counts every kept word,
+// stored or not.
+__device__ __forceinline__ void append_kept(bool keep, uint64_t w, uint32_t* n, uint64_t* out, uint32_t cap) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t mask = __ballot(keep);
+    if (mask == 0) return;
+    const int leader = __builtin_ctzll(mask);
+    uint32_t base = 0;
+    if (lane == leader) base = atomicAdd(n, static_cast<uint32_t>(__popcll(mask)));
+    base = __shfl(base, leader, 64);
+    const uint32_t slot = base + static_cast<uint32_t>(__popcll(mask & ((uint64_t{1} << lane) - 1)));
+    if (keep && slot < cap) out[slot] = w;
 }
 
 // The k best of a row by k passes over it: pick j is the best element strictly after pick j - 1.
@@ -381,51 +551,276 @@ __device__ void topk_passes(const float* xr, float* values, int32_t* indices, in
     }
 }
 
-// One workgroup per row: the candidates ranked (each one's rank = how many candidates beat it) or, past 512 of
-// them, bitonic-sorted in LDS; the fallback rows by passes.
+// One workgroup per row; see the wide-row outline above. The candidates >= G end up in registers, kPerThread a
+// thread: copied from their chunks' slots at prefix offsets when they all fit, else gathered from G up by a wave per
+// chunk through LDS. The first narrowing level histograms their value keys over [G, the largest chunk top].
+constexpr int kFlatChunks = kBins;  // chunk prefix sums held in LDS (rows up to 8M values)
+constexpr int kPerThread = kCap / kBlock;
+
 __global__ __launch_bounds__(kBlock) void topk_wide_finish(const float* __restrict__ x, float* __restrict__ values,
                                                            int32_t* __restrict__ indices, int64_t width, int64_t k,
-                                                           void* scratch) {
-    __shared__ uint64_t cand[kCap];
+                                                           int64_t chunks, const void* scratch) {
+    __shared__ uint64_t kept[kWideMaxK];
+    __shared__ uint64_t staging[kCap];
+    __shared__ uint32_t prefix[kFlatChunks];
+    __shared__ uint32_t bins[kBins];
+    __shared__ uint32_t rank_of[kRankMax];
+    __shared__ uint32_t n, nk;
+    __shared__ uint64_t red_bound[kBlock / 64];
+    __shared__ uint32_t red_over[kBlock / 64], red_top[kBlock / 64], red_total[2];
     const int64_t row = blockIdx.x;
     const float* xr = x + row * width;
-    const WideRow r = wide_row(scratch, row);
-    const uint32_t n = *r.count;
-    if (n > static_cast<uint32_t>(kCap) || n < static_cast<uint64_t>(k)) {
+    const int64_t cap = chunk_cap(k);
+    const char* base = static_cast<const char*>(scratch) + row * wide_row_bytes(chunks, k);
+    const ChunkHeader* hdr = reinterpret_cast<const ChunkHeader*>(base);
+    const uint64_t* slots = reinterpret_cast<const uint64_t*>(base + chunks * kHeaderBytes);
+    const bool flat = chunks <= kFlatChunks;
+    // Headers: G, the largest top, overflow, and (flat) each thread's run of kFlatChunks / kBlock chunks' counts.
+    constexpr int PER = kFlatChunks / kBlock;
+    uint64_t g = 0;
+    uint32_t over = 0, sum = 0, top = 0;
+    uint32_t cnt[PER];
+    for (int b = threadIdx.x; b < kBins; b += kBlock) bins[b] = 0;
+    if (flat) {
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const int64_t c = static_cast<int64_t>(threadIdx.x) * PER + q;
+            const ChunkHeader h = c < chunks ? hdr[c] : ChunkHeader{0, 0, 0};
+            g = h.bound > g ? h.bound : g;
+            top = h.top > top ? h.top : top;
+            over |= h.count > static_cast<uint32_t>(cap) ? 1u : 0u;
+            cnt[q] = h.count;
+            sum += h.count;
+        }
+    } else {
+        for (int64_t c = threadIdx.x; c < chunks; c += kBlock) {
+            const ChunkHeader h = hdr[c];
+            g = h.bound > g ? h.bound : g;
+            top = h.top > top ? h.top : top;
+            over |= h.count > static_cast<uint32_t>(cap) ? 1u : 0u;
+        }
+    }
+    const uint32_t incl = block_inclusive_scan(sum);
+    if (flat) {
+        uint32_t at = incl - sum;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            prefix[threadIdx.x * PER + q] = at;  // exclusive prefix of chunk threadIdx.x * PER + q
+            at += cnt[q];
+        }
+    }
+    g = wave_max_u64(g);
+    top = wave_max_u32(top);
+    for (int off = 1; off < 64; off <<= 1) over |= __shfl_xor(over, off, 64);
+    if ((threadIdx.x & 63) == 0) {
+        red_bound[threadIdx.x >> 6] = g;
+        red_over[threadIdx.x >> 6] = over;
+        red_top[threadIdx.x >> 6] = top;
+    }
+    if (threadIdx.x == kBlock - 1) red_total[0] = incl;
+    if (threadIdx.x == 0) {
+        n = 0;
+        nk = 0;
+    }
+    __syncthreads();
+    for (int q = 0; q < kBlock / 64; ++q) {
+        g = red_bound[q] > g ? red_bound[q] : g;
+        top = red_top[q] > top ? red_top[q] : top;
+        over |= red_over[q];
+    }
+    if (over != 0) {  // uniform: a chunk lost candidates
         topk_passes(xr, values, indices, row, width, k);
         return;
     }
-    for (uint32_t i = threadIdx.x; i < n; i += kBlock) cand[i] = r.cand[i];
-    __syncthreads();
-    if (n <= 512) {
-        for (uint32_t i = threadIdx.x; i < n; i += kBlock) {
-            const uint64_t w = cand[i];
-            uint32_t rank = 0;
-            for (uint32_t j = 0; j < n; ++j) rank += cand[j] > w ? 1u : 0u;
-            if (rank < k) put_pick(xr, values, indices, row * k + rank, w);
+    const uint32_t g_key = static_cast<uint32_t>(g >> 32);
+    // Level 0 window over value keys in [G, top] (none when they are one key).
+    const bool level0 = top > g_key;
+    const Window win0 = level0 ? window_of32(top, g_key) : Window{0, 0};
+    uint64_t c[kPerThread];  // flat index threadIdx.x + kBlock q; 0 = none
+    uint32_t total;
+    if (flat && red_total[0] <= static_cast<uint32_t>(kCap)) {
+        total = red_total[0];
+        // Candidate i lives in the chunk whose prefix is the last <= i: one branch-free binary search per candidate,
+        // all of a thread's searches stepping together.
+        uint32_t at[kPerThread];
+#pragma unroll
+        for (int q = 0; q < kPerThread; ++q) at[q] = 0;
+        // prefix[c] for c >= chunks holds the total, above every i: a probe past the last chunk (clamped into the
+        // array) is never taken, and the reads need no guard, so they overlap.
+        const uint32_t nchunks = static_cast<uint32_t>(chunks);
+        for (uint32_t step = nchunks > 1 ? 1u << (31 - __builtin_clz(nchunks - 1)) : 0u; step != 0; step >>= 1) {
+#pragma unroll
+            for (int q = 0; q < kPerThread; ++q) {
+                const uint32_t i = threadIdx.x + kBlock * q;
+                const uint32_t next = at[q] + step;
+                at[q] = prefix[min(next, static_cast<uint32_t>(kFlatChunks - 1))] <= i ? next : at[q];
+            }
         }
+#pragma unroll
+        for (int q = 0; q < kPerThread; ++q) {
+            const uint32_t i = threadIdx.x + kBlock * q;
+            c[q] = i < total ? slots[static_cast<int64_t>(at[q]) * cap + (i - prefix[at[q]])] : 0;
+        }
+#pragma unroll
+        for (int q = 0; q < kPerThread; ++q) c[q] = c[q] >= g ? c[q] : 0;
+    } else {
+        // A wave takes kGatherUnroll chunks at once, its lanes over their candidates, keeping those >= G.
+        const int lane = threadIdx.x & 63;
+        for (int64_t c0 = static_cast<int64_t>(threadIdx.x >> 6) * kGatherUnroll; c0 < chunks;
+             c0 += kGatherUnroll * (kBlock / 64)) {
+            uint32_t cn[kGatherUnroll];
+            uint32_t most = 0;
+#pragma unroll
+            for (int u = 0; u < kGatherUnroll; ++u) {
+                cn[u] = c0 + u < chunks ? hdr[c0 + u].count : 0u;
+                most = cn[u] > most ? cn[u] : most;
+            }
+            for (uint32_t j0 = 0; j0 < most; j0 += 64) {
+                const uint32_t j = j0 + lane;
+                uint64_t w[kGatherUnroll];
+#pragma unroll
+                for (int u = 0; u < kGatherUnroll; ++u) w[u] = j < cn[u] ? slots[(c0 + u) * cap + j] : 0;
+#pragma unroll
+                for (int u = 0; u < kGatherUnroll; ++u)
+                    append_kept(w[u] != 0 && w[u] >= g, w[u], &n, staging, kCap);
+            }
+        }
+        __syncthreads();
+        total = n;
+        if (total > static_cast<uint32_t>(kCap)) {
+            topk_passes(xr, values, indices, row, width, k);
+            return;
+        }
+#pragma unroll
+        for (int q = 0; q < kPerThread; ++q) {
+            const uint32_t i = threadIdx.x + kBlock * q;
+            c[q] = i < total ? staging[i] : 0;
+        }
+    }
+    // Narrow: every word >= floor is a candidate of the top k, `left` of the top k are in [floor, ceil] (the words
+    // still being split) and the rest above ceil; `count` words are >= floor (an over-estimate until a level ran).
+    uint64_t floor = g, ceil = ~uint64_t{0};
+    uint32_t left = static_cast<uint32_t>(k), count = total;
+    bool too_few = false;
+    if (level0) {
+#pragma unroll
+        for (int q = 0; q < kPerThread; ++q)
+            if (c[q] != 0) atomicAdd(&bins[window_bin32(static_cast<uint32_t>(c[q] >> 32), win0)], 1u);
+        __syncthreads();
+        uint32_t above;
+        const int b = threshold_bin(bins, left, &above);
+        if (b < 0) {
+            too_few = true;
+        } else {
+            const uint32_t shared = win0.top >= 32 ? 0u : (top >> win0.top) << win0.top;
+            const uint32_t fk = shared | (static_cast<uint32_t>(b) << win0.bottom);
+            const uint32_t ck = fk | ((1u << win0.bottom) - 1u);
+            count = static_cast<uint32_t>(k) - left + above + bins[b];
+            left -= above;
+            floor = static_cast<uint64_t>(fk) << 32;
+            ceil = (static_cast<uint64_t>(ck) << 32) | 0xFFFFFFFFull;
+        }
+        __syncthreads();  // bins read before they are cleared again
+    }
+    while (!too_few && count > kRankMax) {
+        uint64_t hi = 0, lo = ~uint64_t{0};
+        uint32_t inside = 0;
+#pragma unroll
+        for (int q = 0; q < kPerThread; ++q) {
+            const bool in = c[q] != 0 && c[q] >= floor && c[q] <= ceil;
+            hi = in && c[q] > hi ? c[q] : hi;
+            lo = in && c[q] < lo ? c[q] : lo;
+            inside += in ? 1u : 0u;
+        }
+        const uint32_t in_all = block_inclusive_scan(inside);
+        if (threadIdx.x == kBlock - 1) red_total[1] = in_all;
+        block_range(hi, lo, hi, lo);  // its barrier publishes red_total[1]
+        if (red_total[1] < left) {  // fewer than k non-NaN values in the row
+            too_few = true;
+            break;
+        }
+        if (hi == lo) {  // one word left to split: it is the k-th
+            floor = hi;
+            count = static_cast<uint32_t>(k);
+            break;
+        }
+        const Window win = window_of(hi, lo);
+        for (int b = threadIdx.x; b < kBins; b += kBlock) bins[b] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < kPerThread; ++q)
+            if (c[q] != 0 && c[q] >= lo && c[q] <= hi) atomicAdd(&bins[window_bin(c[q], win)], 1u);
+        __syncthreads();
+        uint32_t above;
+        const int b = threshold_bin(bins, left, &above);  // found: `left` words lie in [lo, hi]
+        count = static_cast<uint32_t>(k) - left + above + bins[b];
+        left -= above;
+        floor = window_floor(hi, win, static_cast<uint32_t>(b));
+        ceil = floor | ((uint64_t{1} << win.bottom) - 1);
+        __syncthreads();  // bins read before the next level clears them
+    }
+    if (!too_few) {
+        if (threadIdx.x < kRankMax) rank_of[threadIdx.x] = 0;
+        uint32_t mine = 0;
+#pragma unroll
+        for (int q = 0; q < kPerThread; ++q) mine += c[q] != 0 && c[q] >= floor ? 1u : 0u;
+        uint32_t wave_total;
+        const uint32_t before = wave_exclusive_small(mine, wave_total);
+        uint32_t at = 0;
+        if ((threadIdx.x & 63) == 0 && wave_total != 0) at = atomicAdd(&nk, wave_total);
+        at = static_cast<uint32_t>(__shfl(static_cast<int>(at), 0, 64)) + before;
+#pragma unroll
+        for (int q = 0; q < kPerThread; ++q)
+            if (c[q] != 0 && c[q] >= floor) {
+                if (at < kWideMaxK) kept[at] = c[q];
+                ++at;
+            }
+        __syncthreads();
+        too_few = nk < static_cast<uint32_t>(k);  // uniform
+    }
+    if (too_few) {
+        topk_passes(xr, values, indices, row, width, k);
         return;
     }
-    uint32_t size = 1;
-    while (size < n) size <<= 1;
-    for (uint32_t i = n + threadIdx.x; i < size; i += kBlock) cand[i] = 0;
-    __syncthreads();
-    for (uint32_t len = 2; len <= size; len <<= 1) {
-        for (uint32_t stride = len / 2; stride > 0; stride >>= 1) {
-            for (uint32_t i = threadIdx.x; i < size / 2; i += kBlock) {
-                const uint32_t lo = (i / stride) * 2 * stride + (i % stride);
-                const uint32_t hi = lo + stride;
-                const bool descending = (lo & len) == 0;  // the final order is descending
-                const uint64_t a = cand[lo], b = cand[hi];
-                if ((a < b) == descending) {
-                    cand[lo] = b;
-                    cand[hi] = a;
+    // The kept words: count <= kRankMax of them, ranked below, or (k > kRankMax) exactly k, sorted.
+    const uint32_t m = nk;
+    if (m > kRankMax) {
+        uint32_t size = 1;
+        while (size < m) size <<= 1;
+        for (uint32_t i = m + threadIdx.x; i < size; i += kBlock) kept[i] = 0;
+        __syncthreads();
+        for (uint32_t len = 2; len <= size; len <<= 1) {
+            for (uint32_t stride = len / 2; stride > 0; stride >>= 1) {
+                for (uint32_t i = threadIdx.x; i < size / 2; i += kBlock) {
+                    const uint32_t lo = (i / stride) * 2 * stride + (i % stride);
+                    const uint32_t hi = lo + stride;
+                    const bool descending = (lo & len) == 0;  // the final order is descending
+                    const uint64_t a = kept[lo], b = kept[hi];
+                    if ((a < b) == descending) {
+                        kept[lo] = b;
+                        kept[hi] = a;
+                    }
                 }
+                __syncthreads();
             }
-            __syncthreads();
         }
+        for (int64_t j = threadIdx.x; j < k; j += kBlock) put_pick(xr, values, indices, row * k + j, kept[j]);
+        return;
     }
-    for (int64_t j = threadIdx.x; j < k; j += kBlock) put_pick(xr, values, indices, row * k + j, cand[j]);
+    // Rank: the waves split the comparisons of each kept word.
+    const int lane = threadIdx.x & 63;
+    const uint32_t part = threadIdx.x >> 6;
+    const uint32_t j_begin = m * part / (kBlock / 64), j_end = m * (part + 1) / (kBlock / 64);
+    for (uint32_t i = lane; i < m; i += 64) {
+        const uint64_t w = kept[i];
+        uint32_t r = 0;
+#pragma unroll 8
+        for (uint32_t j = j_begin; j < j_end; ++j) r += kept[j] > w ? 1u : 0u;
+        if (r != 0) atomicAdd(&rank_of[i], r);
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < m; i += kBlock)
+        if (rank_of[i] < k) put_pick(xr, values, indices, row * k + rank_of[i], kept[i]);
 }
 
 // k passes by a workgroup per row (the widest k).
@@ -449,7 +844,7 @@ extern "C" {
 
 size_t xs_hip_topk_scratch(int64_t rows, int64_t width, int64_t k) {
     if (rows <= 0 || width <= 0) return 0;
-    if (wide_path(width, k)) return static_cast<size_t>(rows) * kRowScratch;
+    if (wide_path(width, k)) return static_cast<size_t>(rows) * wide_row_bytes(wide_chunks(width), k);
     if (k != 1) return 0;
     const int64_t chunks = argmax_chunks_of(width);
     if (chunks <= 1) return 0;
@@ -509,11 +904,11 @@ int xs_hip_topk(void* stream, const float* x, float* values, int32_t* indices, i
         return fail(XS_HIP_EINVAL, "xs_hip_topk: top-" + std::to_string(k) + " of rows of " + std::to_string(width) +
                                        " needs xs_hip_topk_scratch bytes of 8-byte aligned scratch");
     const bool vec = width % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
-    const dim3 grid(static_cast<unsigned>((width + kWideChunk - 1) / kWideChunk), static_cast<unsigned>(rows));
-    topk_wide_clear<<<static_cast<unsigned>(rows), kBlock, 0, s>>>(scratch);
-    topk_wide_hist<<<grid, kBlock, 0, s>>>(x, width, vec, scratch);
-    topk_wide_compact<<<grid, kBlock, 0, s>>>(x, width, vec, k, scratch);
-    topk_wide_finish<<<static_cast<unsigned>(rows), kBlock, 0, s>>>(x, values, indices, width, k, scratch);
+    const int64_t chunks = wide_chunks(width);
+    if (chunks > INT32_MAX) return fail(XS_HIP_EUNSUPPORTED, "xs_hip_topk: row too wide");
+    topk_wide_chunks<<<dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(rows)), kBlock, 0, s>>>(x, width, vec,
+                                                                                                        k, scratch);
+    topk_wide_finish<<<static_cast<unsigned>(rows), kBlock, 0, s>>>(x, values, indices, width, k, chunks, scratch);
     return check_launch("xs_hip_topk");
 }
 
