@@ -185,7 +185,7 @@ def op_rmsnorm():
         # the updated residual goes back into r, as a decoder layer keeps it
         X.call("xs_hip_add_rms_norm", stream, vp(x), vp(r), vp(w), None, vp(r), X.F32, vp(y), rows, width,
                C.c_float(1e-6))
-    return Op("rmsnorm_residual", W.ALGO_BYTES["rmsnorm_residual"], 4 * rows * width * 4, mk, go, 1, "rms_norm_vec")
+    return Op("rmsnorm_residual", W.ALGO_BYTES["rmsnorm_residual"], 4 * rows * width * 4, mk, go, 1, "row_norm_vec")
 
 
 def op_row_norms(kind):
@@ -295,7 +295,7 @@ def op_topk(name):
         X.call("xs_hip_topk", stream, vp(x), vp(v), vp(i), rows, width, k, C.c_void_p(sc.ptr if nscratch else 0))
     nbytes = rows * width * 4 + rows * k * 8
     wide = nscratch > 0  # clear, histogram, compact, finish; else a wave per row
-    return Op(name, nbytes, nbytes, mk, go, 4 if wide else 1, "topk_wide_compact" if wide else "topk_wave_rows")
+    return Op(name, nbytes, nbytes, mk, go, 2 if wide else 1, "topk_wide_chunks" if wide else "topk_wave_rows")
 
 
 def op_rope(separate=False):
@@ -326,8 +326,8 @@ def op_rope(separate=False):
         X.call("xs_hip_rope", stream, X.F16, vp(k), X.I32, vp(p), vp(f), X.F16, vp(yk), tokens, kh, dim, 0, 1, None)
     if separate:
         return Op("rope_qk_separate", W.ALGO_BYTES["rope_qk"], 2 * (q0.nbytes + k0.nbytes), mk, go_separate, 2,
-                  "rope_kernel")
-    return Op("rope_qk", W.ALGO_BYTES["rope_qk"], 2 * (q0.nbytes + k0.nbytes), mk, go, 1, "rope_kernel")
+                  "rope_rows_kernel")
+    return Op("rope_qk", W.ALGO_BYTES["rope_qk"], 2 * (q0.nbytes + k0.nbytes), mk, go, 1, "rope_rows_kernel")
 
 
 def _kv_inputs():
