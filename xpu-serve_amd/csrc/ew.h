@@ -174,9 +174,12 @@ __device__ __forceinline__ void store8(typename T::storage* p, const float* f) {
     }
 }
 
+// Threads of a vector-path workgroup.
+constexpr int kVecBlock = 64;
+
 // Vector path: cols % 8 == 0, every pointer 16-byte aligned, every nonzero row stride a multiple of 8.
 template <typename TX, typename TY, int OP, int ACT, int U>
-__global__ __launch_bounds__(kBlock) void ew2d_vec(Ew2D e, uint32_t units, FastDiv32 chunks_per_row, uint32_t cpr) {
+__global__ __launch_bounds__(kVecBlock) void ew2d_vec(Ew2D e, uint32_t units, FastDiv32 chunks_per_row, uint32_t cpr) {
     using SX = typename TX::storage;
     using SY = typename TY::storage;
     constexpr bool RB = reads_b(OP), RC = reads_c(OP);
@@ -185,9 +188,9 @@ __global__ __launch_bounds__(kBlock) void ew2d_vec(Ew2D e, uint32_t units, FastD
     const SX* b = static_cast<const SX*>(e.b);
     const SX* c = static_cast<const SX*>(e.c);
     SY* y = static_cast<SY*>(e.y);
-    constexpr uint32_t stride = kBlock;
+    constexpr uint32_t stride = kVecBlock;
     {
-        const uint32_t u0 = blockIdx.x * (kBlock * U) + threadIdx.x;
+        const uint32_t u0 = blockIdx.x * (kVecBlock * U) + threadIdx.x;
         float fa[U][8], fb[U][8], fc[U][8];
         int64_t row[U], col[U];
 #pragma unroll
@@ -274,9 +277,9 @@ int launch(hipStream_t s, const Ew2D& e, const char* what) {
     const int64_t cpr = e.cols / 8;
     const int64_t units = e.rows * cpr;
     if (vec && units < (int64_t{1} << 31)) {
-        constexpr int U = 2;
-        const unsigned grid = static_cast<unsigned>((units + kBlock * U - 1) / (kBlock * U));
-        ew2d_vec<TX, TY, OP, ACT, U><<<grid, kBlock, 0, s>>>(e, static_cast<uint32_t>(units),
+        constexpr int U = 1;
+        const unsigned grid = static_cast<unsigned>((units + kVecBlock * U - 1) / (kVecBlock * U));
+        ew2d_vec<TX, TY, OP, ACT, U><<<grid, kVecBlock, 0, s>>>(e, static_cast<uint32_t>(units),
                                                             FastDiv32(static_cast<uint32_t>(cpr)),
                                                             static_cast<uint32_t>(cpr));
     } else {

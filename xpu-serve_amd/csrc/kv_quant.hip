@@ -48,13 +48,16 @@ __device__ __forceinline__ uint32_t pack_low_bytes(uint32_t a, uint32_t b, uint3
     return ab | cd;
 }
 
+// Threads of a quantize workgroup.
+constexpr int kQBlock = 256;
+
 template <typename T, int L, int VPL, int U>
-__global__ __launch_bounds__(kBlock) void quantize_i8_vec(const typename T::storage* __restrict__ x,
+__global__ __launch_bounds__(kQBlock) void quantize_i8_vec(const typename T::storage* __restrict__ x,
                                                           int8_t* __restrict__ codes, float* __restrict__ scales,
                                                           int64_t rows, int64_t width) {
     constexpr int VEC = vec_elems<T>();
     constexpr int RPW = 64 / L;  // rows per wave
-    constexpr int WAVES = kBlock / 64;
+    constexpr int WAVES = kQBlock / 64;
     const int lane = threadIdx.x & 63;
     const int sub = lane / L;
     const int l = lane % L;
@@ -123,15 +126,18 @@ __global__ __launch_bounds__(kBlock) void quantize_i8_any(const typename T::stor
     }
 }
 
+// Threads of a dequantize workgroup.
+constexpr int kDeqBlock = 64;
+
 // out = fl32(code * scale[row]) for units of 8 codes.
 template <typename Y, int U>
-__global__ __launch_bounds__(kBlock) void dequantize_i8_vec(const uint64_t* __restrict__ codes,
+__global__ __launch_bounds__(kDeqBlock) void dequantize_i8_vec(const uint64_t* __restrict__ codes,
                                                             const float* __restrict__ scales,
                                                             typename Y::storage* __restrict__ out, uint32_t units,
                                                             FastDiv32 units_per_row) {
-    constexpr uint32_t stride = kBlock;
+    constexpr uint32_t stride = kDeqBlock;
     {
-        const uint32_t v0 = blockIdx.x * (kBlock * U) + threadIdx.x;
+        const uint32_t v0 = blockIdx.x * (kDeqBlock * U) + threadIdx.x;
         uint64_t raw[U];
         float scale[U];
 #pragma unroll
@@ -184,9 +190,9 @@ int launch_quantize(hipStream_t s, const void* x, int8_t* codes, float* scales, 
     const auto* xs = static_cast<const S*>(x);
     constexpr int U = 2;
     auto go = [&](auto kernel, int lanes) {
-        const int64_t rows_per_tile = (kBlock / 64) * (64 / lanes) * U;
+        const int64_t rows_per_tile = (kQBlock / 64) * (64 / lanes) * U;
         const unsigned grid = static_cast<unsigned>((rows + rows_per_tile - 1) / rows_per_tile);
-        kernel<<<grid, kBlock, 0, s>>>(xs, codes, scales, rows, width);
+        kernel<<<grid, kQBlock, 0, s>>>(xs, codes, scales, rows, width);
         return check_launch("xs_hip_quantize_kv");
     };
     if (vec_ok) {
@@ -212,10 +218,11 @@ int launch_dequantize(hipStream_t s, const int8_t* codes, const float* scales, v
     using S = typename Y::storage;
     const int64_t n = rows * width;
     auto* o = static_cast<S*>(out);
-    if (width % 8 == 0 && reinterpret_cast<uintptr_t>(codes) % 8 == 0 && aligned16(out) && n / 8 < (int64_t{1} << 32)) {
+    if (width % 8 == 0 && reinterpret_cast<uintptr_t>(codes) % 8 == 0 && aligned16(out) && n / 8 < (int64_t{1} << 31)) {
+        // (below 2^31 units no lane index wraps in 32 bits)
         const uint32_t units = static_cast<uint32_t>(n / 8);
-        constexpr int U = 2;
-        dequantize_i8_vec<Y, U><<<(units + kBlock * U - 1) / (kBlock * U), kBlock, 0, s>>>(
+        constexpr int U = 1;
+        dequantize_i8_vec<Y, U><<<(units + kDeqBlock * U - 1) / (kDeqBlock * U), kDeqBlock, 0, s>>>(
             reinterpret_cast<const uint64_t*>(codes), scales, o, units, FastDiv32(static_cast<uint32_t>(width / 8)));
     } else {
         dequantize_i8_any<Y><<<grid_for(n, kBlock * 4), kBlock, 0, s>>>(codes, scales, o, n, width);

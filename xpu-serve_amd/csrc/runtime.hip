@@ -58,9 +58,13 @@ int device_cus() {
 
 namespace {
 
-// y = x in 16-byte vectors, one per lane: a tile of kBlock vectors per workgroup, as many workgroups as tiles.
-__global__ __launch_bounds__(kBlock) void copy_kernel(const u32x4* __restrict__ x, u32x4* __restrict__ y, int64_t n) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+// Threads of a copy workgroup.
+constexpr int kCopyBlock = 64;
+
+// y = x in 16-byte vectors, one per lane: a tile of kCopyBlock vectors per workgroup, as many workgroups as tiles.
+__global__ __launch_bounds__(kCopyBlock) void copy_kernel(const u32x4* __restrict__ x, u32x4* __restrict__ y,
+                                                          int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kCopyBlock + threadIdx.x;
     if (i < n) st128_nt(y + i, ld128_nt(x + i));
 }
 
@@ -296,8 +300,8 @@ int xs_hip_copy(void* stream, const void* x, void* y, size_t bytes) {
         return fail(XS_HIP_EINVAL, "xs_hip_copy: needs non-null 16-byte aligned buffers and a multiple of 16 bytes, got " +
                                        std::to_string(bytes));
     const int64_t n = static_cast<int64_t>(bytes / 16);
-    if ((n + kBlock - 1) / kBlock > 0x7fffffffLL) return fail(XS_HIP_EUNSUPPORTED, "xs_hip_copy: too many bytes");
-    copy_kernel<<<static_cast<unsigned>((n + kBlock - 1) / kBlock), kBlock, 0, as_stream(stream)>>>(
+    if (n > 0xffffffffLL - kCopyBlock) return fail(XS_HIP_EUNSUPPORTED, "xs_hip_copy: too many bytes");
+    copy_kernel<<<static_cast<unsigned>((n + kCopyBlock - 1) / kCopyBlock), kCopyBlock, 0, as_stream(stream)>>>(
         static_cast<const u32x4*>(x), static_cast<u32x4*>(y), n);
     return check_launch("xs_hip_copy");
 }
