@@ -215,8 +215,12 @@ __global__ __launch_bounds__(kBlock) void turbo_quantize_kernel(const typename X
     }
 }
 
+// Threads of a decode workgroup, and the groups it takes.
+constexpr int kDecBlock = 512;
+constexpr int kDecGroupsPerBlock = kDecBlock / kLanes;
+
 template <int Bits, typename Y>
-__global__ __launch_bounds__(kBlock) void turbo_decode_kernel(const uint8_t* __restrict__ codes,
+__global__ __launch_bounds__(kDecBlock) void turbo_decode_kernel(const uint8_t* __restrict__ codes,
                                                               const uint16_t* __restrict__ norms,
                                                               typename Y::storage* __restrict__ out, int64_t groups) {
     constexpr int NC = 1 << Bits;
@@ -228,7 +232,7 @@ __global__ __launch_bounds__(kBlock) void turbo_decode_kernel(const uint8_t* __r
     }
     __syncthreads();
     const int lane = threadIdx.x % kLanes;
-    const int64_t g = static_cast<int64_t>(blockIdx.x) * kGroupsPerBlock + threadIdx.x / kLanes;
+    const int64_t g = static_cast<int64_t>(blockIdx.x) * kDecGroupsPerBlock + threadIdx.x / kLanes;
     if (g >= groups) return;
     const uint8_t* gc = codes + g * (kGroup * Bits / 8);
     uint32_t packed, high = 0;
@@ -280,8 +284,8 @@ __global__ __launch_bounds__(kBlock) void turbo_rotate_kernel(const float* __res
     st128(yl + 4, pack<F32>(v + 4));
 }
 
-unsigned blocks_for(int64_t groups, int rounds = 1) {
-    return static_cast<unsigned>((groups + kGroupsPerBlock * rounds - 1) / (kGroupsPerBlock * rounds));
+unsigned blocks_for(int64_t groups, int rounds = 1, int per_block = kGroupsPerBlock) {
+    return static_cast<unsigned>((groups + per_block * rounds - 1) / (per_block * rounds));
 }
 
 template <int Bits>
@@ -311,15 +315,15 @@ int decode_bits(hipStream_t s, const uint8_t* codes, const uint16_t* norms, xs_d
                 int64_t groups) {
     switch (out_dtype) {
         case XS_F32:
-            turbo_decode_kernel<Bits, F32><<<blocks_for(groups), kBlock, 0, s>>>(codes, norms, static_cast<float*>(out),
+            turbo_decode_kernel<Bits, F32><<<blocks_for(groups, 1, kDecGroupsPerBlock), kDecBlock, 0, s>>>(codes, norms, static_cast<float*>(out),
                                                                                  groups);
             break;
         case XS_F16:
-            turbo_decode_kernel<Bits, F16><<<blocks_for(groups), kBlock, 0, s>>>(codes, norms,
+            turbo_decode_kernel<Bits, F16><<<blocks_for(groups, 1, kDecGroupsPerBlock), kDecBlock, 0, s>>>(codes, norms,
                                                                                  static_cast<uint16_t*>(out), groups);
             break;
         case XS_BF16:
-            turbo_decode_kernel<Bits, BF16><<<blocks_for(groups), kBlock, 0, s>>>(codes, norms,
+            turbo_decode_kernel<Bits, BF16><<<blocks_for(groups, 1, kDecGroupsPerBlock), kDecBlock, 0, s>>>(codes, norms,
                                                                                   static_cast<uint16_t*>(out), groups);
             break;
         default:
@@ -335,7 +339,7 @@ int check_turbo(const char* op, int64_t rows, int64_t width, const void* a, cons
                                        std::to_string(rows) + " rows of " + std::to_string(width));
     if (rows > 0 && (a == nullptr || b == nullptr || c == nullptr))
         return fail(XS_HIP_EINVAL, std::string(op) + ": null buffer");
-    if (rows * (width / kGroup) > int64_t{0x7fffffff} * kGroupsPerBlock)
+    if (rows * (width / kGroup) > (int64_t{0xffffffff} - kBlock) / kLanes)  // a lane per 8 values, in 32 bits
         return fail(XS_HIP_EUNSUPPORTED, std::string(op) + ": too many groups");
     return XS_HIP_OK;
 }
