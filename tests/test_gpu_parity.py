@@ -306,7 +306,7 @@ def test_rms_norm_goldens(ora):
 
 
 @pytest.mark.parametrize("rows,width", [(1, 16), (5, 48), (7, 100), (3, 2560), (9, 4096), (2, 8192), (4, 32768),
-                                        (2, 40000), (33, 512)])
+                                        (2, 40000), (33, 512), (3, 1536), (5, 5120), (2, 7168)])
 @pytest.mark.parametrize("xdt,ydt", [(F32, F32), (BF16, BF16), (F16, F32), (F32, F16)])
 def test_rms_norm_shapes(ora, rows, width, xdt, ydt):
     rng = np.random.default_rng(rows * width)
@@ -747,7 +747,8 @@ def test_layer_norm_goldens_and_shapes(ora):
     rng = np.random.default_rng(41)
     for rows, width, xdt, ydt, weighted in [(64, 2560, F32, F32, True), (7, 1000, BF16, BF16, True),
                                             (33, 4096, F16, F16, False), (3, 70000, F32, F32, True),
-                                            (5, 333, F32, F32, True)]:
+                                            (5, 333, F32, F32, True), (4, 5120, BF16, BF16, True),
+                                            (3, 7168, F32, F16, True)]:
         x = ora.narrow((rng.standard_normal((rows, width)) * 2 + 1).astype(np.float32), xdt)
         w = rng.standard_normal(width).astype(np.float32) if weighted else None
         b = rng.standard_normal(width).astype(np.float32) if weighted else None
@@ -766,6 +767,10 @@ def test_l2_clip_and_reduce_sum(ora):
     x[::2] *= 0.001
     step("l2_clip [300, 2048]")
     assert_f32_close(X.l2_clip(dev(x), 1.0, 1e-6).numpy(), ora.l2_clip(x, 1.0, 1e-6), what="l2_clip big")
+    x = rng.standard_normal((17, 2560)).astype(np.float32)  # five waves a row, two vectors a lane
+    x[::3] *= 0.001
+    step("l2_clip [17, 2560]")
+    assert_f32_close(X.l2_clip(dev(x), 1.0, 1e-6).numpy(), ora.l2_clip(x, 1.0, 1e-6), what="l2_clip 2560")
     for a in range(3):
         step(f"reduce_sum goldens axis {a}")
         assert_f32_close(X.reduce_sum(dev(g["rs_x"]), a).numpy(), g[f"rs_axis{a}"], what=f"reduce_sum {a}")
