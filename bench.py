@@ -21,6 +21,7 @@ import ctypes as C
 import json
 import math
 import os
+import re
 import sys
 import time
 
@@ -35,7 +36,6 @@ import xs_hip as X  # noqa: E402
 PEAK_HBM_GBS = 8000.0
 METRIC = "achieved HBM GB/s (% of ~8 TB/s peak) and µs/call per op; host CPU baseline"
 ROTATE_BYTES = 1 << 30
-WARM_SECONDS = 0.3  # sustained replay of each op's graph before its timed windows
 
 
 def log(msg):
@@ -72,7 +72,7 @@ def _elapsed(start, end):
     return ms.value
 
 
-def time_op(op, steps, warmup, repeats, stream):
+def time_op(op, steps, warmup, repeats, stream, warm_seconds):
     """Median ms per call over `repeats` windows of `steps` calls, two ways: replaying one HIP graph that holds the
     `steps` calls (device time, no host launch cost between kernels), and launching them one by one from Python."""
     nsets = max(2, math.ceil(ROTATE_BYTES / op.footprint))
@@ -88,13 +88,13 @@ def time_op(op, steps, warmup, repeats, stream):
         op.launch(sets[i % nsets], stream)
     graph = C.c_void_p()
     X.call("xs_hip_stream_end_capture", stream, C.byref(graph))
-    # Warm the graph, then keep replaying it for WARM_SECONDS so the timed windows see the clocks of sustained
+    # Warm the graph, then keep replaying it for `warm_seconds` so the timed windows see the clocks of sustained
     # work rather than the ramp out of idle (the first windows otherwise read a few percent slow).
     t_warm = time.perf_counter()
     while True:
         X.call("xs_hip_graph_launch", graph, stream)
         X.call("xs_hip_stream_synchronize", stream)
-        if time.perf_counter() - t_warm >= WARM_SECONDS:
+        if time.perf_counter() - t_warm >= warm_seconds:
             break
     graph_ms = []
     for _ in range(repeats):
@@ -445,8 +445,9 @@ def op_attention_i8(inputs):
               2, "attention_i8_rows")
 
 
-def op_copy(n=256 << 20):
-    """Bytes per call n (default 256 MiB): the kernel the hardware byte counters are calibrated against."""
+def op_copy(n=256 << 20, name="copy"):
+    """Bytes per call n (default 256 MiB): the kernel the hardware byte counters are calibrated against, and, at
+    other sizes (`--only copy_10MiB` etc.), the ceiling a streaming op of that size can reach."""
     x0 = X.DeviceBuffer(n)
     X.call("xs_hip_memset", C.c_void_p(x0.ptr), 1, C.c_size_t(n), None)
 
@@ -458,7 +459,7 @@ def op_copy(n=256 << 20):
     def go(s, stream):
         x, y = s
         X.call("xs_hip_copy", stream, C.c_void_p(x.ptr), C.c_void_p(y.ptr), C.c_size_t(n))
-    return Op("copy", 2 * n, 2 * n, mk, go, 1, "copy_kernel")
+    return Op(name, 2 * n, 2 * n, mk, go, 1, "copy_kernel")
 
 
 OP_ORDER = ["swiglu_bias", "swiglu_bias_strided", "rmsnorm_residual", "softmax_masked", "argmax", "rope_qk",
@@ -470,6 +471,9 @@ OP_ORDER = ["swiglu_bias", "swiglu_bias_strided", "rmsnorm_residual", "softmax_m
 def build_ops(only):
     """Yields the ops one at a time, so only one op's buffers are alive at once."""
     names = OP_ORDER if only is None else [n for n in OP_ORDER + ["copy"] if n in only]
+    sized = {} if only is None else {n: m for n in sorted(only) if (m := re.fullmatch(r"copy_(\d+)(KiB|MiB)", n))}
+    for name, m in sized.items():
+        yield op_copy(int(m.group(1)) << (10 if m.group(2) == "KiB" else 20), name)
     kv = None
     for name in names:
         if name in ("kv_quantize", "kv_dequantize", "attention_i8_decode", "kv_turbo4_quantize",
@@ -550,9 +554,12 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--repeats", type=int, default=5)
-    ap.add_argument("--only", type=str, default=None, help="comma-separated op names (or 'copy')")
+    ap.add_argument("--only", type=str, default=None, help="comma-separated op names (or 'copy', 'copy_<n>KiB', 'copy_<n>MiB')")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--warm-seconds", type=float, default=0.3,
+                    help="sustained graph replay before each op's timed windows (0 under hardware-counter runs, "
+                         "where every dispatch is serialized)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": f"--gpus {args.gpus}: this path is built and measured on one GPU; the kernels "
@@ -568,7 +575,7 @@ def main():
     results = {}
     for op in build_ops(only):
         log(f"timing {op.name}")
-        results[op.name] = time_op(op, args.steps, args.warmup, args.repeats, stream)
+        results[op.name] = time_op(op, args.steps, args.warmup, args.repeats, stream, args.warm_seconds)
         log(f"  {op.name}: {results[op.name]['us_per_call']} us/call, {results[op.name]['gb_s']} GB/s")
     X.call("xs_hip_stream_destroy", stream)
 

@@ -257,8 +257,11 @@ struct RowArgs {
     FastDiv32 row_vecs_a, row_vecs_b;  // dividers by heads * R and heads2 * R (vectors per token of each tensor)
 };
 
+// Threads of a row-kernel workgroup (64 and 128 measured slower on MI355X at config 3's shape).
+constexpr int kRowBlock = 256;
+
 template <typename TX, typename TY, typename I, int R, int NV>
-__global__ __launch_bounds__(kBlock) void rope_rows_kernel(RowArgs a) {
+__global__ __launch_bounds__(kRowBlock) void rope_rows_kernel(RowArgs a) {
     using SX = typename TX::storage;
     using SY = typename TY::storage;
     constexpr int VEC = vec_elems<TX>();
@@ -283,13 +286,13 @@ __global__ __launch_bounds__(kBlock) void rope_rows_kernel(RowArgs a) {
     u32x4 raw[NV];
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-        const int j = min(t + k * kBlock, n - 1);
+        const int j = min(t + k * kRowBlock, n - 1);
         raw[k] = ld128_nt(j < na ? xa + static_cast<int64_t>(j) * VEC : xb + static_cast<int64_t>(j - na) * VEC);
     }
 
     // (cos, sin) of every (token, pair) of the tile, as the kernel above builds it.
     const int entries = tt_n * a.pairs;
-    for (int e = t; e < entries; e += kBlock) {
+    for (int e = t; e < entries; e += kRowBlock) {
         const int te = e / a.pairs;
         const int p = e - te * a.pairs;
         int64_t sec = 0;
@@ -309,7 +312,7 @@ __global__ __launch_bounds__(kBlock) void rope_rows_kernel(RowArgs a) {
     SY* yb = static_cast<SY*>(a.y2) + t0 * a.heads2 * R * VEC;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-        const int j = t + k * kBlock;
+        const int j = t + k * kRowBlock;
         if (j >= n) break;  // rows are whole, so a lane and its partner leave together
         const int tl = static_cast<int>(j < na ? a.row_vecs_a.div(static_cast<uint32_t>(j))
                                                : a.row_vecs_b.div(static_cast<uint32_t>(j - na)));
@@ -398,16 +401,16 @@ __global__ __launch_bounds__(kBlock) void rope_rows_kernel(RowArgs a) {
 
 // Vectors per thread the row kernel is instantiated for, and the tile it aims at (vectors per block).
 constexpr int kRowMaxNV = 8;
-constexpr int kRowTargetVectors = 6 * kBlock;
+constexpr int kRowTargetVectors = 2 * kRowBlock;  // one token of Q+K at config 3 (measured best against 6x)
 
 template <typename TX, typename TY, typename I, int R>
 int launch_rows_nv(hipStream_t s, const RowArgs& a, int nv, unsigned grid) {
     // Instantiated for an even count of vectors per thread (the last one idles when the tile needs an odd count).
     switch ((nv + 1) / 2) {
-        case 1: rope_rows_kernel<TX, TY, I, R, 2><<<grid, kBlock, 0, s>>>(a); break;
-        case 2: rope_rows_kernel<TX, TY, I, R, 4><<<grid, kBlock, 0, s>>>(a); break;
-        case 3: rope_rows_kernel<TX, TY, I, R, 6><<<grid, kBlock, 0, s>>>(a); break;
-        default: rope_rows_kernel<TX, TY, I, R, 8><<<grid, kBlock, 0, s>>>(a); break;
+        case 1: rope_rows_kernel<TX, TY, I, R, 2><<<grid, kRowBlock, 0, s>>>(a); break;
+        case 2: rope_rows_kernel<TX, TY, I, R, 4><<<grid, kRowBlock, 0, s>>>(a); break;
+        case 3: rope_rows_kernel<TX, TY, I, R, 6><<<grid, kRowBlock, 0, s>>>(a); break;
+        default: rope_rows_kernel<TX, TY, I, R, 8><<<grid, kRowBlock, 0, s>>>(a); break;
     }
     return check_launch("xs_hip_rope");
 }
@@ -421,14 +424,14 @@ int try_launch_rows(hipStream_t s, const RopeArgs& a) {
     if (r != 8 && r != 16 && r != 32) return -1;  // head dims 64 / 128 / 256 at 16 bits, 32 / 64 / 128 at 32 bits
     if (!aligned16(a.x) || !aligned16(a.y) || (a.heads2 > 0 && (!aligned16(a.x2) || !aligned16(a.y2)))) return -1;
     const int64_t per_token = (a.heads + a.heads2) * r;  // vectors
-    if (per_token > static_cast<int64_t>(kRowMaxNV) * kBlock) return -1;
+    if (per_token > static_cast<int64_t>(kRowMaxNV) * kRowBlock) return -1;
     int64_t tt = kRowTargetVectors / per_token;
     if (tt < 1) tt = 1;
     const int64_t pairs = a.dim / 2;
     if (tt * pairs > kMaxTableEntries) tt = kMaxTableEntries / pairs;
     if (tt < 1) return -1;
     if (tt > a.tokens) tt = a.tokens;
-    const int nv = static_cast<int>((tt * per_token + kBlock - 1) / kBlock);
+    const int nv = static_cast<int>((tt * per_token + kRowBlock - 1) / kRowBlock);
     RowArgs ra;
     ra.x = a.x;
     ra.y = a.y;
