@@ -215,8 +215,10 @@ __global__ __launch_bounds__(kBlock) void turbo_quantize_kernel(const typename X
     }
 }
 
-// Threads of a decode workgroup, and the groups it takes.
-constexpr int kDecBlock = 512;
+// Threads of a decode workgroup, the groups a 16-lane slice of it takes (kDecU, kDecGroupsPerBlock apart), and the
+// groups of a workgroup.
+constexpr int kDecBlock = 256;
+constexpr int kDecU = 2;
 constexpr int kDecGroupsPerBlock = kDecBlock / kLanes;
 
 template <int Bits, typename Y>
@@ -226,37 +228,52 @@ __global__ __launch_bounds__(kDecBlock) void turbo_decode_kernel(const uint8_t* 
     constexpr int NC = 1 << Bits;
     constexpr int NM = kMagnitudes<Bits>;
     __shared__ float centroid[NC];
+    const int lane = threadIdx.x % kLanes;
+    const int64_t g0 = static_cast<int64_t>(blockIdx.x) * kDecGroupsPerBlock * kDecU + threadIdx.x / kLanes;
+    // The groups' codes and norms are requested first, so their latency overlaps the codebook's staging.
+    uint32_t packed[kDecU], high[kDecU];
+    uint16_t norm_bits[kDecU];
+#pragma unroll
+    for (int u = 0; u < kDecU; ++u) {
+        const int64_t g = g0 + u * kDecGroupsPerBlock;
+        packed[u] = high[u] = 0;
+        norm_bits[u] = 0;
+        if (g < groups) {
+            const uint8_t* gc = codes + g * (kGroup * Bits / 8);
+            if constexpr (Bits == 4) {
+                packed[u] = reinterpret_cast<const uint32_t*>(gc)[lane];
+            } else {
+                packed[u] = reinterpret_cast<const uint16_t*>(gc)[lane];
+                if constexpr (Bits == 3) high[u] = gc[kGroup / 4 + lane];
+            }
+            norm_bits[u] = norms[g];
+        }
+    }
     if (threadIdx.x < NC) {
         const int c = static_cast<int>(threadIdx.x);
         centroid[c] = c >= NM ? Book<Bits>::mags[c - NM] : -Book<Bits>::mags[NM - 1 - c];
     }
     __syncthreads();
-    const int lane = threadIdx.x % kLanes;
-    const int64_t g = static_cast<int64_t>(blockIdx.x) * kDecGroupsPerBlock + threadIdx.x / kLanes;
-    if (g >= groups) return;
-    const uint8_t* gc = codes + g * (kGroup * Bits / 8);
-    uint32_t packed, high = 0;
-    if constexpr (Bits == 4) {
-        packed = reinterpret_cast<const uint32_t*>(gc)[lane];
-    } else {
-        packed = reinterpret_cast<const uint16_t*>(gc)[lane];
-        if constexpr (Bits == 3) high = gc[kGroup / 4 + lane];
-    }
-    const float norm = f16_to_f32(norms[g]);
-    float v[kLaneValues];
 #pragma unroll
-    for (int e = 0; e < kLaneValues; ++e) {
-        uint32_t code;
-        if constexpr (Bits == 4) code = (packed >> (4 * e)) & 15u;
-        else code = ((packed >> (2 * e)) & 3u) | (Bits == 3 ? ((high >> e) & 1u) << 2 : 0u);
-        v[e] = centroid[code] * norm;
-    }
-    typename Y::storage* o = out + g * kGroup + lane * kLaneValues;
-    if constexpr (sizeof(typename Y::storage) == 4) {
-        st128_nt(o, pack<Y>(v));
-        st128_nt(o + 4, pack<Y>(v + 4));
-    } else {
-        st128_nt(o, pack<Y>(v));
+    for (int u = 0; u < kDecU; ++u) {
+        const int64_t g = g0 + u * kDecGroupsPerBlock;
+        if (g >= groups) break;  // later u are later groups
+        const float norm = f16_to_f32(norm_bits[u]);
+        float v[kLaneValues];
+#pragma unroll
+        for (int e = 0; e < kLaneValues; ++e) {
+            uint32_t code;
+            if constexpr (Bits == 4) code = (packed[u] >> (4 * e)) & 15u;
+            else code = ((packed[u] >> (2 * e)) & 3u) | (Bits == 3 ? ((high[u] >> e) & 1u) << 2 : 0u);
+            v[e] = centroid[code] * norm;
+        }
+        typename Y::storage* o = out + g * kGroup + lane * kLaneValues;
+        if constexpr (sizeof(typename Y::storage) == 4) {
+            st128_nt(o, pack<Y>(v));
+            st128_nt(o + 4, pack<Y>(v + 4));
+        } else {
+            st128_nt(o, pack<Y>(v));
+        }
     }
 }
 
@@ -315,15 +332,15 @@ int decode_bits(hipStream_t s, const uint8_t* codes, const uint16_t* norms, xs_d
                 int64_t groups) {
     switch (out_dtype) {
         case XS_F32:
-            turbo_decode_kernel<Bits, F32><<<blocks_for(groups, 1, kDecGroupsPerBlock), kDecBlock, 0, s>>>(codes, norms, static_cast<float*>(out),
+            turbo_decode_kernel<Bits, F32><<<blocks_for(groups, kDecU, kDecGroupsPerBlock), kDecBlock, 0, s>>>(codes, norms, static_cast<float*>(out),
                                                                                  groups);
             break;
         case XS_F16:
-            turbo_decode_kernel<Bits, F16><<<blocks_for(groups, 1, kDecGroupsPerBlock), kDecBlock, 0, s>>>(codes, norms,
+            turbo_decode_kernel<Bits, F16><<<blocks_for(groups, kDecU, kDecGroupsPerBlock), kDecBlock, 0, s>>>(codes, norms,
                                                                                  static_cast<uint16_t*>(out), groups);
             break;
         case XS_BF16:
-            turbo_decode_kernel<Bits, BF16><<<blocks_for(groups, 1, kDecGroupsPerBlock), kDecBlock, 0, s>>>(codes, norms,
+            turbo_decode_kernel<Bits, BF16><<<blocks_for(groups, kDecU, kDecGroupsPerBlock), kDecBlock, 0, s>>>(codes, norms,
                                                                                   static_cast<uint16_t*>(out), groups);
             break;
         default:
