@@ -775,7 +775,7 @@ def test_l2_clip_and_reduce_sum(ora):
         step(f"reduce_sum goldens axis {a}")
         assert_f32_close(X.reduce_sum(dev(g["rs_x"]), a).numpy(), g[f"rs_axis{a}"], what=f"reduce_sum {a}")
     for shape, a in [((1000, 4096), 1), ((64, 3000, 7), 1), ((5, 200, 300), 0), ((2, 17), 1), ((1, 1, 5), 1),
-                     ((3, 0, 4), 1)]:
+                     ((3, 0, 4), 1), ((512, 2560), 0), ((3, 37, 100), 1), ((2, 9, 33), 1)]:
         t = (rng.standard_normal(shape) * 100).astype(np.float32)
         step(f"reduce_sum {shape} axis {a}")
         assert_f32_close(X.reduce_sum(dev(t), a).numpy(), ora.reduce_sum(t, a), what=f"reduce_sum {shape}")
