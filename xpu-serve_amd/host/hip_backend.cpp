@@ -1320,21 +1320,31 @@ HipSession::HipSession(std::span<const Graph* const> programs, const WeightStore
     int device = 0;
     if (!options_.device.empty()) {
         const std::string& d = options_.device;
-        XS_CHECK(d.rfind("GPU.", 0) == 0, "hip: device '", d, "' (expected GPU.<n>)");
-        device = std::stoi(d.substr(4));
+        const std::string n = d.rfind("GPU.", 0) == 0 ? d.substr(4) : std::string();
+        XS_CHECK(!n.empty() && n.size() < 6 && n.find_first_not_of("0123456789") == std::string::npos, "hip: device '",
+                 d, "' (expected GPU.<n>)");
+        device = std::stoi(n);
         XS_CHECK(device >= 0 && device < count, "hip: device '", d, "' (", count, " present)");
     }
     check(xs_hip_set_device(device), "set device");
     check(xs_hip_stream_create(&stream_), "stream");
-    for (KvState& k : kv_) {
-        const auto rows = static_cast<size_t>(k.cap * k.heads);
-        k.kc.grow(rows * static_cast<size_t>(k.dim));
-        k.vc.grow(rows * static_cast<size_t>(k.dim));
-        k.ks.grow(rows * 4);
-        k.vs.grow(rows * 4);
+    try {
+        for (KvState& k : kv_) {
+            const auto rows = static_cast<size_t>(k.cap * k.heads);
+            k.kc.grow(rows * static_cast<size_t>(k.dim));
+            k.vc.grow(rows * static_cast<size_t>(k.dim));
+            k.ks.grow(rows * 4);
+            k.vs.grow(rows * 4);
+        }
+        for (auto& p : programs_) p->upload();
+        check(xs_hip_stream_synchronize(stream_), "weight upload");
+    } catch (...) {
+        // The destructor does not run for a constructor that throws: wait for what was queued, then let the stream go.
+        xs_hip_stream_synchronize(stream_);
+        xs_hip_stream_destroy(stream_);
+        stream_ = nullptr;
+        throw;
     }
-    for (auto& p : programs_) p->upload();
-    check(xs_hip_stream_synchronize(stream_), "weight upload");
 }
 
 class HipBackend final : public Backend {
