@@ -195,6 +195,27 @@ def op_rmsnorm():
     return Op("rmsnorm_residual", W.ALGO_BYTES["rmsnorm_residual"], 4 * rows * width * 4, mk, go, 1, "row_norm_vec")
 
 
+def op_rmsnorm_separate():
+    """Config 0 in the reference's call pattern: the Add, then the RmsNorm of its sum (two launches; the same work
+    and algorithmic bytes as the fused call)."""
+    a = W.config0().arrays
+    rows, width = a["x"].shape
+    x0, r0, w0 = (X.DeviceTensor.from_numpy(a[k]) for k in ("x", "residual", "weight"))
+
+    def mk():
+        s = (dcopy(x0), dcopy(r0), dcopy(w0), X.DeviceTensor.empty(X.F32, (rows, width)))
+        for t in (s[0], s[1], s[3]):
+            need(t, rows * width * 4, "rmsnorm separate")
+        return s
+
+    def go(s, stream):
+        x, r, w, y = s
+        X.call("xs_hip_binary_same", stream, X.ADD, X.F32, vp(x), vp(r), X.F32, vp(r), rows * width)
+        X.call("xs_hip_rms_norm", stream, X.F32, vp(r), vp(w), None, X.F32, vp(y), rows, width, C.c_float(1e-6))
+    return Op("rmsnorm_residual_separate", W.ALGO_BYTES["rmsnorm_residual"], 4 * rows * width * 4, mk, go, 2,
+              "ew2d_vec")
+
+
 def op_row_norms(kind):
     """layer_norm, l2_clip or reduce_sum (over the rows or the columns) of config 0's x [512, 2560] f32."""
     a = W.config0().arrays
@@ -462,8 +483,8 @@ def op_copy(n=256 << 20, name="copy"):
     return Op(name, 2 * n, 2 * n, mk, go, 1, "copy_kernel")
 
 
-OP_ORDER = ["swiglu_bias", "swiglu_bias_strided", "rmsnorm_residual", "softmax_masked", "argmax", "rope_qk",
-            "rope_qk_separate", "kv_quantize", "kv_dequantize", "attention_i8_decode", "layer_norm", "l2_clip",
+OP_ORDER = ["swiglu_bias", "swiglu_bias_strided", "rmsnorm_residual", "rmsnorm_residual_separate", "softmax_masked",
+            "argmax", "rope_qk", "rope_qk_separate", "kv_quantize", "kv_dequantize", "attention_i8_decode", "layer_norm", "l2_clip",
             "reduce_sum_rows", "reduce_sum_cols", "unary_softcap", "kv_turbo4_quantize", "kv_turbo4_dequantize",
             "topk_shortlist", "topk_moe_router", "topk_draft_candidates"]
 
@@ -480,6 +501,7 @@ def build_ops(only):
                     "kv_turbo4_dequantize") and kv is None:
             kv = _kv_inputs()
         yield {"swiglu_bias": op_swiglu, "swiglu_bias_strided": op_swiglu_strided, "rmsnorm_residual": op_rmsnorm,
+               "rmsnorm_residual_separate": op_rmsnorm_separate,
                "softmax_masked": op_softmax, "argmax": op_argmax, "rope_qk": op_rope,
                "rope_qk_separate": lambda: op_rope(True), "copy": op_copy,
                "kv_quantize": lambda: op_kv_quantize(kv), "kv_dequantize": lambda: op_kv_dequantize(kv),
