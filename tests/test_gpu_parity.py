@@ -859,6 +859,27 @@ def test_attention_i8_decode_full_size(ora):
     assert_attention_close(y, ora.attention(q, k_rt, v_rt, 1.0 / math.sqrt(d)), "decode full size")
 
 
+def test_attention_i8_cache_beyond_2gib():
+    """A cache whose key and value codes each pass 2 GiB (2^24 + 37 keys x 128): the tiles' buffer extents are clamped
+    to 32 bits there. Every key row is the same, so every score is equal and the output is the plain mean of the value
+    rows, which cycle through seven patterns: a closed form over counts."""
+    n, d, hq = (1 << 24) + 37, 128, 2
+    rng = np.random.default_rng(71)
+    pats = rng.integers(-127, 128, size=(7, d)).astype(np.int8)
+    step(f"attention_i8 over {n} keys (codes past 2 GiB)")
+    kc = X.DeviceTensor.empty(X.I8, (n, d))
+    X.call("xs_hip_memset", C.c_void_p(kc.ptr), 3, C.c_size_t(kc.nbytes), None)
+    ks = dev(np.full(n, 0.02, np.float32))
+    vc = dev(np.tile(pats, ((n + 6) // 7, 1))[:n])
+    vs = dev(np.full(n, 0.25, np.float32))
+    q = rng.standard_normal((1, hq, d)).astype(np.float32)
+    y = X.attention_i8(dev(q), kc, ks, vc, vs, 1, 1.0 / math.sqrt(d)).numpy()
+    counts = np.array([(n - r + 6) // 7 for r in range(7)], np.float64)
+    want = (counts @ pats.astype(np.float64)) * np.float64(np.float32(0.25)) / n
+    for h in range(hq):
+        assert_attention_close(y[0, h], want.astype(np.float32), f"head {h} over {n} keys")
+
+
 # ---------------------------------------------------------------------------------------------------------------
 # TurboQuant KV formats
 
