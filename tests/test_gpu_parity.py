@@ -124,6 +124,35 @@ def test_kv_config4_full(ora):
         assert (np.abs(xf - bf) <= bound * (1 + 1e-6)).all()
 
 
+def test_kv_beyond_4gib(ora):
+    """Quantize and dequantize of 2^24 + 5 rows of 128 f16 (4 GiB in, 2 GiB of codes): 64-bit offsets throughout.
+    The rows repeat a block of 4099 distinct rows, so every output row is checked bit for bit against the oracle's
+    result for its block row."""
+    rows, width, distinct = (1 << 24) + 5, 128, 4099
+    rng = np.random.default_rng(72)
+    block = ora.narrow((rng.standard_normal((distinct, width)) * 3).astype(np.float32), F16)
+    block[5, 17] = np.float16(900.0)  # an outlier channel
+    block[6] = 0                      # a zero row
+    reps = (rows + distinct - 1) // distinct
+    step(f"kv quantize / dequantize [{rows}, {width}] f16 (past 4 GiB)")
+    x = dev(np.tile(block, (reps, 1))[:rows], F16)
+    codes, scales = X.quantize_kv(x)
+    del x
+    wc, ws = ora.quantize_kv(ora.widen(block, F16))
+    want_back = ora.narrow(ora.dequantize_kv(wc, ws), F16).view(np.uint16)
+    got_c, got_s = codes.numpy(), scales.numpy()
+    for r0 in range(0, rows, distinct * 512):  # compare a slab of whole blocks at a time
+        r1 = min(rows, r0 + distinct * 512)
+        n = r1 - r0
+        assert_exact(got_c[r0:r1], np.tile(wc, (512, 1))[:n], f"codes rows {r0}..{r1}")
+        assert_exact(got_s[r0:r1], np.tile(ws, 512)[:n], f"scales rows {r0}..{r1}")
+    del got_c
+    back = X.dequantize_kv(codes, scales, F16).numpy().view(np.uint16)
+    for r0 in range(0, rows, distinct * 512):
+        r1 = min(rows, r0 + distinct * 512)
+        assert_exact(back[r0:r1], np.tile(want_back, (512, 1))[:r1 - r0], f"dequant rows {r0}..{r1}")
+
+
 # ---------------------------------------------------------------------------------------------------------------
 # activation times gate (SwiGLU)
 
