@@ -186,6 +186,31 @@ def test_swiglu_shapes(ora, rows, cols):
     assert_ulp(y, ora.narrow(want, BF16), "bf16", what="swiglu")
 
 
+def test_swiglu_beyond_2g_elements(ora):
+    """The SwiGLU gate with bias over 2^31 + 3 * 8192 elements of bf16 (gate, up and out 4 GiB each). The rows repeat
+    a block of 61 distinct rows: the first block is checked against the oracle within one bf16 ulp, and every other
+    row must equal its block row's output bit for bit."""
+    rows, cols, distinct = (1 << 18) + 3, 8192, 61
+    rng = np.random.default_rng(73)
+    gate = ora.narrow(rng.standard_normal((distinct, cols)).astype(np.float32) * 2, BF16)
+    up = ora.narrow(rng.standard_normal((distinct, cols)).astype(np.float32), BF16)
+    bias = ora.narrow((0.02 * rng.standard_normal(cols)).astype(np.float32), BF16)
+    reps = (rows + distinct - 1) // distinct
+    step(f"swiglu bf16 [{rows}, {cols}] (past 2^31 elements)")
+    dg = dev(np.tile(gate, (reps, 1))[:rows], BF16)
+    du = dev(np.tile(up, (reps, 1))[:rows], BF16)
+    y = X.swiglu(dg, du, dev(bias, BF16), BF16)
+    del dg, du
+    out = y.numpy().view(np.uint16)
+    want = ora.act_bias_mul(SILU, ora.widen(gate, BF16), ora.widen(up, BF16), ora.widen(bias, BF16))
+    assert_ulp(out[:distinct], ora.narrow(want, BF16), "bf16", what="swiglu block")
+    first = out[:distinct]
+    slab = distinct * 256
+    for r0 in range(0, rows, slab):
+        r1 = min(rows, r0 + slab)
+        assert_exact(out[r0:r1], np.tile(first, (256, 1))[:r1 - r0], f"swiglu rows {r0}..{r1}")
+
+
 def test_unary_bias(ora):
     rng = np.random.default_rng(12)
     x = rng.standard_normal((9, 40)).astype(np.float32) * 3
