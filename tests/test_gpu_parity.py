@@ -664,6 +664,30 @@ def test_rope_config3_full(ora):
             assert np.allclose(n0, n1, rtol=5e-3, atol=1e-3)
 
 
+@pytest.mark.parametrize("xdt", [F32, F16])
+def test_rope_far_positions_and_planted_interleave(ora, xdt):
+    """Positions near 30,000 and up to 2^20 (device_ops.cpp:499-501 rotates at 30,000), theta 1e4 and 1e6, on both
+    RoPE kernels (head_dim 128: the row kernel; 96: the per-pair kernel); and the reference's planted-bug control
+    (device_ops.cpp:503-505): the interleaved (GPT-J) rotation must not match the device's output."""
+    rng = np.random.default_rng(74)
+    for theta, dim in ((1e4, 128), (1e6, 128), (1e4, 96)):
+        t, h = 37, 3
+        x = ora.narrow((rng.standard_normal((t, h, dim)) * 2).astype(np.float32), xdt)
+        pos = np.concatenate([np.arange(29990, 30010), rng.integers(0, 1 << 20, t - 20)]).astype(np.int32)
+        f = ora.rope_inv_freq(theta, dim, dim // 2, dim // 2)
+        step(f"rope far positions theta {theta:g} dim {dim} {DT[xdt]}")
+        y = X.rope(dev(x, xdt), dev(pos), dev(f), y_dtype=F32).numpy()
+        want = ora.rope(ora.widen(x, xdt), pos, f)
+        assert_f32_close(y, want, what=f"rope far positions theta {theta:g} dim {dim}")
+        xf = ora.widen(x, xdt).astype(np.float64)
+        ang = pos[:, None].astype(np.float64) * f[None, :].astype(np.float64)
+        c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+        wrong = xf.copy()
+        wrong[..., 0::2] = xf[..., 0::2] * c - xf[..., 1::2] * s
+        wrong[..., 1::2] = xf[..., 1::2] * c + xf[..., 0::2] * s
+        assert not np.allclose(y, wrong, rtol=1e-3, atol=1e-3), "the interleaved rotation matched"
+
+
 def test_rope_qk_fused(ora):
     """xs_hip_rope2 (Q and K in one launch) rotates each tensor exactly as xs_hip_rope does, at the config 3 shape,
     in place, and with partial rotary (pass-through channels)."""
