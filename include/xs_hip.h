@@ -256,6 +256,13 @@ int xs_hip_quantize_kv(void* stream, xs_kv_format format, xs_dtype x_dtype, cons
  * kv_turbo.cpp:86-91; xs_hip_kv_rotate rotates back); out 16-byte aligned. */
 int xs_hip_dequantize_kv(void* stream, xs_kv_format format, const void* codes, const void* scales, xs_dtype out_dtype,
                          void* out, int64_t rows, int64_t width);
+/* No counterpart in the reference: for callers that capture a step into a HIP graph and replay it while the cache
+ * grows. The XS_KV_I8 quantize of `rows` rows, written at rows row0[0] * rows_per_unit + r of a cache of
+ * `capacity_rows` rows (codes int8 [capacity_rows, width], scales f32 [capacity_rows]); row0 is a device int64 read
+ * when the kernel runs, so one captured launch appends wherever the cache ends at replay. A destination outside the
+ * cache writes nothing. */
+int xs_hip_quantize_kv_at(void* stream, xs_dtype x_dtype, const void* x, void* codes, void* scales, int64_t rows,
+                          int64_t width, const int64_t* row0, int64_t rows_per_unit, int64_t capacity_rows);
 
 /* y [rows, width] = x with each group of 128 values rotated as the TurboQuant formats rotate a row (inverse = 0), or
  * rotated back (inverse = 1); f32, 16-byte aligned, y may be x. Replaces sycl_be::kv_rotate (sycl_kernels.h:219-221);
@@ -281,6 +288,15 @@ int xs_hip_attention_i8(void* stream, const float* q, const void* k_codes, const
                         const void* v_scales, float* out, int64_t tokens, int64_t q_heads, int64_t kv_heads,
                         int64_t head_dim, int64_t kv_len, float scale, float softcap, int64_t window, int causal,
                         int64_t split, void* scratch);
+/* No counterpart in the reference: for callers that capture a step into a HIP graph and replay it while the cache
+ * grows. xs_hip_attention_i8 over a cache of kv_capacity keys of which kv_len[0] -- a device int64 read when the kernel
+ * runs, clamped to [0, kv_capacity] -- are held; the caller keeps kv_len[0] >= tokens. `split` is fixed at the launch
+ * (take xs_hip_attention_i8_split of the largest key count the replays will see); splits left without keys add
+ * nothing. */
+int xs_hip_attention_i8_at(void* stream, const float* q, const void* k_codes, const void* k_scales,
+                           const void* v_codes, const void* v_scales, float* out, int64_t tokens, int64_t q_heads,
+                           int64_t kv_heads, int64_t head_dim, int64_t kv_capacity, const int64_t* kv_len,
+                           float scale, float softcap, int64_t window, int causal, int64_t split, void* scratch);
 int64_t xs_hip_attention_i8_split(int64_t tokens, int64_t kv_heads, int64_t kv_len);
 size_t xs_hip_attention_i8_scratch(int64_t tokens, int64_t q_heads, int64_t head_dim, int64_t split);
 

@@ -958,6 +958,93 @@ def test_attention_i8_cache_beyond_2gib():
         assert_attention_close(y[0, h], want.astype(np.float32), f"head {h} over {n} keys")
 
 
+def _dev_i64(v):
+    return dev(np.array([v], np.int64))
+
+
+def test_quantize_kv_at_device_row(ora):
+    """xs_hip_quantize_kv_at: the rows land at row0[0] * unit of the cache, bit-exact with xs_hip_quantize_kv, and
+    nothing else changes; a destination outside the cache (past the end, or negative) writes nothing."""
+    rng = np.random.default_rng(75)
+    heads, d, cap_tokens, t = 4, 128, 40, 3
+    for xdt in (F32, F16):
+        x = ora.narrow(rng.standard_normal((t * heads, d)).astype(np.float32), xdt)
+        step(f"quantize_kv_at {DT[xdt]}")
+        wc, ws = X.quantize_kv(dev(x, xdt))
+        wc, ws = wc.numpy(), ws.numpy()
+        for tok0, lands in ((5, True), (cap_tokens - t, True), (cap_tokens - t + 1, False), (-1, False)):
+            codes = X.DeviceTensor.empty(X.I8, (cap_tokens * heads, d))
+            scales = X.DeviceTensor.empty(F32, (cap_tokens * heads,))
+            X.call("xs_hip_memset", C.c_void_p(codes.ptr), 0x5A, C.c_size_t(codes.nbytes), None)
+            X.call("xs_hip_memset", C.c_void_p(scales.ptr), 0x5A, C.c_size_t(scales.nbytes), None)
+            row0 = _dev_i64(tok0)
+            xd = dev(x, xdt)
+            X.call("xs_hip_quantize_kv_at", None, xdt, C.c_void_p(xd.ptr), C.c_void_p(codes.ptr),
+                   C.c_void_p(scales.ptr), t * heads, d, C.c_void_p(row0.ptr), heads, cap_tokens * heads)
+            gc, gs = codes.numpy(), scales.numpy()
+            want_c = np.full_like(gc, 0x5A)
+            want_s = np.full(gs.shape, np.frombuffer(b"\x5a" * 4, np.float32)[0], np.float32)
+            if lands:
+                want_c[tok0 * heads:(tok0 + t) * heads] = wc
+                want_s[tok0 * heads:(tok0 + t) * heads] = ws
+            assert_exact(gc, want_c, f"codes at token {tok0}")
+            assert_exact(gs.view(np.uint32), want_s.view(np.uint32), f"scales at token {tok0}")
+
+
+def test_attention_i8_at_device_length(ora):
+    """xs_hip_attention_i8_at reads the key count from device memory: with the same split it is bit-exact with
+    xs_hip_attention_i8 at that count; with the split chosen for the whole capacity (splits without keys) it agrees
+    within the attention bar; a count above the capacity is clamped to it."""
+    rng = np.random.default_rng(76)
+    hq, hkv, d, cap = 8, 2, 128, 600
+    k = rng.standard_normal((cap, hkv, d)).astype(np.float32)
+    v = rng.standard_normal((cap, hkv, d)).astype(np.float32)
+    kc, ks = cache_i8(k)
+    vc, vs = cache_i8(v)
+    scale = 1.0 / math.sqrt(d)
+    for t, n, window, causal in ((1, 257, 0, True), (3, 64, 0, True), (2, 300, 17, True), (1, 600, 0, False)):
+        q = dev(rng.standard_normal((t, hq, d)).astype(np.float32))
+        step(f"attention_i8_at T{t} n{n} w{window} causal{causal}")
+        for split in (X.lib().xs_hip_attention_i8_split(t, hkv, n), X.lib().xs_hip_attention_i8_split(t, hkv, cap)):
+            nbytes = int(X.lib().xs_hip_attention_i8_scratch(t, hq, d, split))
+            sc = X.DeviceBuffer(nbytes) if nbytes else None
+            outs = []
+            for at in (False, True):
+                out = X.DeviceTensor.empty(F32, (t, hq, d))
+                args = [C.c_void_p(q.ptr), C.c_void_p(kc.ptr), C.c_void_p(ks.ptr), C.c_void_p(vc.ptr),
+                        C.c_void_p(vs.ptr), C.c_void_p(out.ptr), t, hq, hkv, d]
+                tail = [C.c_float(scale), C.c_float(0.0), window, int(causal), split,
+                        C.c_void_p(sc.ptr) if sc else None]
+                if at:
+                    nd = _dev_i64(n)
+                    X.call("xs_hip_attention_i8_at", None, *args, cap, C.c_void_p(nd.ptr), *tail)
+                else:
+                    X.call("xs_hip_attention_i8", None, *args, n, *tail)
+                X.synchronize()
+                outs.append(out.numpy())
+            assert_exact(outs[1], outs[0], f"T{t} n{n} split {split}")
+        # the split of the whole capacity, against the oracle over the first n keys
+        want = ora.attention(q.numpy(), ora.dequantize_kv(kc.numpy(), ks.numpy()).reshape(k.shape)[:n],
+                             ora.dequantize_kv(vc.numpy(), vs.numpy()).reshape(v.shape)[:n], scale, 0.0, window,
+                             causal)
+        assert_attention_close(outs[1], want, f"T{t} n{n} at the capacity's split")
+    # a count above the capacity reads the capacity
+    q = dev(rng.standard_normal((1, hq, d)).astype(np.float32))
+    step("attention_i8_at clamped count")
+    split = X.lib().xs_hip_attention_i8_split(1, hkv, cap)
+    sc = X.DeviceBuffer(int(X.lib().xs_hip_attention_i8_scratch(1, hq, d, split)))
+    got = []
+    for n_dev in (cap, cap + 1000):
+        out = X.DeviceTensor.empty(F32, (1, hq, d))
+        nd = _dev_i64(n_dev)
+        X.call("xs_hip_attention_i8_at", None, C.c_void_p(q.ptr), C.c_void_p(kc.ptr), C.c_void_p(ks.ptr),
+               C.c_void_p(vc.ptr), C.c_void_p(vs.ptr), C.c_void_p(out.ptr), 1, hq, hkv, d, cap, C.c_void_p(nd.ptr),
+               C.c_float(scale), C.c_float(0.0), 0, 1, split, C.c_void_p(sc.ptr))
+        X.synchronize()
+        got.append(out.numpy())
+    assert_exact(got[1], got[0], "clamped to the capacity")
+
+
 # ---------------------------------------------------------------------------------------------------------------
 # TurboQuant KV formats
 

@@ -40,13 +40,24 @@ struct AttnArgs {
     float scale, softcap;
     int causal, split;
     int hg;  // KV heads a workgroup (8, 4, 2 or 1)
+    // Or the key count read from device memory when the kernel runs (a step replayed from a captured graph), clamped
+    // to [0, kv_len]: kv_len is then the cache's capacity.
+    const int64_t* kv_len_dev = nullptr;
 };
 
-// The key range [first, last] of query token t (cpu_ref::attention, ops.cpp:565-575 without blocks and anchors).
-__device__ __forceinline__ void key_range(const AttnArgs& a, int64_t t, int64_t& first, int64_t& last) {
-    const int64_t pos = a.kv_len - a.tokens + t;
+// The keys the cache holds for this launch.
+__device__ __forceinline__ int64_t keys_of(const AttnArgs& a) {
+    if (a.kv_len_dev == nullptr) return a.kv_len;
+    const int64_t n = a.kv_len_dev[0];
+    return n < 0 ? 0 : (n > a.kv_len ? a.kv_len : n);
+}
+
+// The key range [first, last] of query token t over n keys (cpu_ref::attention, ops.cpp:565-575 without blocks and
+// anchors).
+__device__ __forceinline__ void key_range(const AttnArgs& a, int64_t n, int64_t t, int64_t& first, int64_t& last) {
+    const int64_t pos = n - a.tokens + t;
     first = a.window > 0 ? (pos - a.window + 1 > 0 ? pos - a.window + 1 : 0) : 0;
-    last = a.causal ? pos : a.kv_len - 1;
+    last = a.causal ? pos : n - 1;
     if (a.window > 0 && pos + a.window - 1 < last) last = pos + a.window - 1;
 }
 
@@ -160,7 +171,7 @@ __global__ __launch_bounds__(64 * waves_for(G, D)) void attention_i8_rows(AttnAr
     float* const vscale = kscale + kTile;                    // [kTile]
 
     int64_t first, last;
-    key_range(a, t, first, last);
+    key_range(a, keys_of(a), t, first, last);
     const int64_t len = last >= first ? last - first + 1 : 0;
     const int64_t per = (len + a.split - 1) / a.split;
     const int64_t k0 = first + s * per;
@@ -631,11 +642,16 @@ size_t xs_hip_attention_i8_scratch(int64_t tokens, int64_t q_heads, int64_t head
     return static_cast<size_t>(tokens * q_heads * split * (head_dim + 2)) * sizeof(float);
 }
 
-int xs_hip_attention_i8(void* stream, const float* q, const void* k_codes, const void* k_scales, const void* v_codes,
-                        const void* v_scales, float* out, int64_t tokens, int64_t q_heads, int64_t kv_heads,
-                        int64_t head_dim, int64_t kv_len, float scale, float softcap, int64_t window, int causal,
-                        int64_t split, void* scratch) {
-    const char* what = "xs_hip_attention_i8";
+}  // extern "C"
+
+namespace {
+
+// Both entry points: kv_len keys, or (kv_len_dev set) a capacity of kv_len keys of which the kernel reads how many
+// the cache holds.
+int attention_i8(void* stream, const float* q, const void* k_codes, const void* k_scales, const void* v_codes,
+                 const void* v_scales, float* out, int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                 int64_t kv_len, const int64_t* kv_len_dev, float scale, float softcap, int64_t window, int causal,
+                 int64_t split, void* scratch, const char* what) {
     if (tokens < 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || kv_len < 0 || window < 0 || split < 1 ||
         q_heads % kv_heads != 0)
         return fail(XS_HIP_EINVAL, std::string(what) + ": q [" + std::to_string(tokens) + ", " +
@@ -665,7 +681,7 @@ int xs_hip_attention_i8(void* stream, const float* q, const void* k_codes, const
     AttnArgs a{q, static_cast<const int8_t*>(k_codes), static_cast<const float*>(k_scales),
                static_cast<const int8_t*>(v_codes), static_cast<const float*>(v_scales),
                out, split > 1 ? static_cast<float*>(scratch) : nullptr, tokens, q_heads, kv_heads, head_dim, kv_len,
-               window, scale, softcap, causal ? 1 : 0, static_cast<int>(split), 1};
+               window, scale, softcap, causal ? 1 : 0, static_cast<int>(split), 1, kv_len_dev};
     const hipStream_t s = as_stream(stream);
     int rc;
     switch (q_heads / kv_heads) {
@@ -684,7 +700,29 @@ int xs_hip_attention_i8(void* stream, const float* q, const void* k_codes, const
     if (rc != XS_HIP_OK || split == 1) return rc;
     attention_combine_rows<<<static_cast<unsigned>(tokens * q_heads * (head_dim / kCombineDims)), 256, 0, s>>>(
         static_cast<const float*>(scratch), out, static_cast<int>(split), head_dim, tokens * q_heads);
-    return check_launch("xs_hip_attention_i8 (combine)");
+    return check_launch(what);
+}
+
+}  // namespace
+
+extern "C" {
+
+int xs_hip_attention_i8(void* stream, const float* q, const void* k_codes, const void* k_scales, const void* v_codes,
+                        const void* v_scales, float* out, int64_t tokens, int64_t q_heads, int64_t kv_heads,
+                        int64_t head_dim, int64_t kv_len, float scale, float softcap, int64_t window, int causal,
+                        int64_t split, void* scratch) {
+    return attention_i8(stream, q, k_codes, k_scales, v_codes, v_scales, out, tokens, q_heads, kv_heads, head_dim,
+                        kv_len, nullptr, scale, softcap, window, causal, split, scratch, "xs_hip_attention_i8");
+}
+
+int xs_hip_attention_i8_at(void* stream, const float* q, const void* k_codes, const void* k_scales,
+                           const void* v_codes, const void* v_scales, float* out, int64_t tokens, int64_t q_heads,
+                           int64_t kv_heads, int64_t head_dim, int64_t kv_capacity, const int64_t* kv_len,
+                           float scale, float softcap, int64_t window, int causal, int64_t split, void* scratch) {
+    if (kv_len == nullptr || reinterpret_cast<uintptr_t>(kv_len) % 8 != 0)
+        return fail(XS_HIP_EINVAL, "xs_hip_attention_i8_at: kv_len must be an 8-byte aligned device int64");
+    return attention_i8(stream, q, k_codes, k_scales, v_codes, v_scales, out, tokens, q_heads, kv_heads, head_dim,
+                        kv_capacity, kv_len, scale, softcap, window, causal, split, scratch, "xs_hip_attention_i8_at");
 }
 
 }  // extern "C"

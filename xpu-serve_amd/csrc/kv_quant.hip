@@ -51,10 +51,29 @@ __device__ __forceinline__ uint32_t pack_low_bytes(uint32_t a, uint32_t b, uint3
 // Threads of a quantize workgroup.
 constexpr int kQBlock = 256;
 
+// Where a quantize writes: rows [0, rows) of codes / scales, or, with `row0` set, rows row0[0] * unit + r of a cache of
+// `cap` rows -- the destination read from device memory when the kernel runs (a step replayed from a captured graph
+// appends where the cache ends that step). A destination past the cache writes nothing.
+struct QuantDest {
+    const int64_t* row0 = nullptr;
+    int64_t unit = 0, cap = 0;
+};
+
+// The first destination row, or -1 when the destination lies outside the cache.
+__device__ __forceinline__ int64_t first_row(const QuantDest& d, int64_t rows) {
+    if (d.row0 == nullptr) return 0;
+    const int64_t off = d.row0[0] * d.unit;
+    return off < 0 || off > d.cap - rows ? -1 : off;
+}
+
 template <typename T, int L, int VPL, int U>
 __global__ __launch_bounds__(kQBlock) void quantize_i8_vec(const typename T::storage* __restrict__ x,
                                                           int8_t* __restrict__ codes, float* __restrict__ scales,
-                                                          int64_t rows, int64_t width) {
+                                                          int64_t rows, int64_t width, QuantDest dest) {
+    const int64_t off = first_row(dest, rows);
+    if (off < 0) return;
+    codes += off * width;
+    scales += off;
     constexpr int VEC = vec_elems<T>();
     constexpr int RPW = 64 / L;  // rows per wave
     constexpr int WAVES = kQBlock / 64;
@@ -111,7 +130,11 @@ __global__ __launch_bounds__(kQBlock) void quantize_i8_vec(const typename T::sto
 template <typename T>
 __global__ __launch_bounds__(kBlock) void quantize_i8_any(const typename T::storage* __restrict__ x,
                                                           int8_t* __restrict__ codes, float* __restrict__ scales,
-                                                          int64_t rows, int64_t width) {
+                                                          int64_t rows, int64_t width, QuantDest dest) {
+    const int64_t off = first_row(dest, rows);
+    if (off < 0) return;
+    codes += off * width;
+    scales += off;
     const int lane = threadIdx.x & 63;
     const int64_t waves = static_cast<int64_t>(gridDim.x) * (kBlock / 64);
     for (int64_t r = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6); r < rows; r += waves) {
@@ -181,7 +204,8 @@ __global__ __launch_bounds__(kBlock) void dequantize_i8_any(const int8_t* __rest
 }
 
 template <typename T>
-int launch_quantize(hipStream_t s, const void* x, int8_t* codes, float* scales, int64_t rows, int64_t width) {
+int launch_quantize(hipStream_t s, const void* x, int8_t* codes, float* scales, int64_t rows, int64_t width,
+                    const QuantDest& dest) {
     using S = typename T::storage;
     const int64_t row_bytes = width * static_cast<int64_t>(sizeof(S));
     const int64_t nvr = row_bytes / 16;  // 128-bit vectors per row
@@ -192,7 +216,7 @@ int launch_quantize(hipStream_t s, const void* x, int8_t* codes, float* scales, 
     auto go = [&](auto kernel, int lanes) {
         const int64_t rows_per_tile = (kQBlock / 64) * (64 / lanes) * U;
         const unsigned grid = static_cast<unsigned>((rows + rows_per_tile - 1) / rows_per_tile);
-        kernel<<<grid, kQBlock, 0, s>>>(xs, codes, scales, rows, width);
+        kernel<<<grid, kQBlock, 0, s>>>(xs, codes, scales, rows, width, dest);
         return check_launch("xs_hip_quantize_kv");
     };
     if (vec_ok) {
@@ -208,7 +232,7 @@ int launch_quantize(hipStream_t s, const void* x, int8_t* codes, float* scales, 
         }
     }
     const unsigned grid = grid_for(rows, kBlock / 64);
-    quantize_i8_any<T><<<grid, kBlock, 0, s>>>(xs, codes, scales, rows, width);
+    quantize_i8_any<T><<<grid, kBlock, 0, s>>>(xs, codes, scales, rows, width, dest);
     return check_launch("xs_hip_quantize_kv");
 }
 
@@ -241,6 +265,19 @@ int check_kv_format(xs_kv_format format, const char* op) {
     return fail(XS_HIP_EINVAL, std::string(op) + ": unknown KV format " + std::to_string(static_cast<int>(format)));
 }
 
+int quantize_i8(void* stream, xs_dtype x_dtype, const void* x, void* codes, void* scales, int64_t rows, int64_t width,
+                const QuantDest& dest, const char* what) {
+    auto* c = static_cast<int8_t*>(codes);
+    auto* sc = static_cast<float*>(scales);
+    switch (x_dtype) {
+        case XS_F32: return launch_quantize<F32>(as_stream(stream), x, c, sc, rows, width, dest);
+        case XS_F16: return launch_quantize<F16>(as_stream(stream), x, c, sc, rows, width, dest);
+        case XS_BF16: return launch_quantize<BF16>(as_stream(stream), x, c, sc, rows, width, dest);
+        default:
+            return fail(XS_HIP_EINVAL, std::string(what) + ": x must be f32, f16 or bf16, got " + dtype_name(x_dtype));
+    }
+}
+
 }  // namespace
 }  // namespace xs_hip
 
@@ -262,16 +299,23 @@ int xs_hip_quantize_kv(void* stream, xs_kv_format format, xs_dtype x_dtype, cons
         return fail(XS_HIP_EINVAL, "xs_hip_quantize_kv: null buffer");
     if (reinterpret_cast<uintptr_t>(scales) % 4 != 0)
         return fail(XS_HIP_EINVAL, "xs_hip_quantize_kv: scales must be 4-byte aligned f32");
-    auto* c = static_cast<int8_t*>(codes);
-    auto* sc = static_cast<float*>(scales);
-    switch (x_dtype) {
-        case XS_F32: return launch_quantize<F32>(as_stream(stream), x, c, sc, rows, width);
-        case XS_F16: return launch_quantize<F16>(as_stream(stream), x, c, sc, rows, width);
-        case XS_BF16: return launch_quantize<BF16>(as_stream(stream), x, c, sc, rows, width);
-        default:
-            return fail(XS_HIP_EINVAL, std::string("xs_hip_quantize_kv: x must be f32, f16 or bf16, got ") +
-                                           dtype_name(x_dtype));
-    }
+    return quantize_i8(stream, x_dtype, x, codes, scales, rows, width, QuantDest{}, "xs_hip_quantize_kv");
+}
+
+int xs_hip_quantize_kv_at(void* stream, xs_dtype x_dtype, const void* x, void* codes, void* scales, int64_t rows,
+                          int64_t width, const int64_t* row0, int64_t rows_per_unit, int64_t capacity_rows) {
+    const char* what = "xs_hip_quantize_kv_at";
+    if (rows < 0 || width <= 0 || rows_per_unit < 0 || capacity_rows < 0)
+        return fail(XS_HIP_EINVAL, std::string(what) + ": rows " + std::to_string(rows) + " of width " +
+                                       std::to_string(width) + ", " + std::to_string(rows_per_unit) +
+                                       " rows a unit, capacity " + std::to_string(capacity_rows));
+    if (rows == 0) return XS_HIP_OK;
+    if (x == nullptr || codes == nullptr || scales == nullptr || row0 == nullptr)
+        return fail(XS_HIP_EINVAL, std::string(what) + ": null buffer");
+    if (reinterpret_cast<uintptr_t>(scales) % 4 != 0 || reinterpret_cast<uintptr_t>(row0) % 8 != 0)
+        return fail(XS_HIP_EINVAL, std::string(what) + ": scales must be 4-byte and row0 8-byte aligned");
+    return quantize_i8(stream, x_dtype, x, codes, scales, rows, width, QuantDest{row0, rows_per_unit, capacity_rows},
+                       what);
 }
 
 int xs_hip_dequantize_kv(void* stream, xs_kv_format format, const void* codes, const void* scales, xs_dtype out_dtype,

@@ -104,10 +104,13 @@ _SIGS = {
     "xs_hip_rope2": [_P, _INT, _P, _P, _I64, _P, _P, _I64, _INT, _P, _P, _INT, _I64, _I64, _I64, _I64, _P],
     "xs_hip_quantize_kv": [_P, _INT, _INT, _P, _P, _P, _I64, _I64],
     "xs_hip_dequantize_kv": [_P, _INT, _P, _P, _INT, _P, _I64, _I64],
+    "xs_hip_quantize_kv_at": [_P, _INT, _P, _P, _P, _I64, _I64, _P, _I64, _I64],
     "xs_hip_copy": [_P, _P, _P, C.c_size_t],
     "xs_hip_copy_rows": [_P, _P, _I64, _P, _I64, _I64, _I64],
     "xs_hip_kv_rotate": [_P, _P, _P, _I64, _I64, _INT],
     "xs_hip_attention_i8": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _F, _I64, _INT, _I64, _P],
+    "xs_hip_attention_i8_at": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _F, _F, _I64, _INT, _I64,
+                               _P],
     "xs_hip_attention_i8_split": [_I64, _I64, _I64],
     "xs_hip_attention_i8_scratch": [_I64, _I64, _I64, _I64],
 }
