@@ -233,6 +233,36 @@ void* xss_compile(int nprog, void* const* graphs, void* store, int precision, in
     }
 }
 
+// xss_compile with backend options: "key=value" pairs separated by ';' (SessionOptions::extra).
+void* xss_compile_opts(int nprog, void* const* graphs, void* store, int precision, int64_t max_context, int kv_k,
+                       int kv_v, const char* device, const char* extra) {
+    try {
+        auto box = std::make_unique<SessionBox>();
+        box->backend = make_backend("hip");
+        SessionOptions o;
+        o.precision = static_cast<DType>(precision);
+        o.max_context = max_context;
+        o.kv.k = static_cast<quant::KvFormat>(kv_k);
+        o.kv.v = static_cast<quant::KvFormat>(kv_v);
+        o.device = device != nullptr ? device : "";
+        std::string rest = extra != nullptr ? extra : "";
+        while (!rest.empty()) {
+            const size_t end = rest.find(';');
+            const std::string kv = rest.substr(0, end);
+            rest = end == std::string::npos ? "" : rest.substr(end + 1);
+            const size_t eq = kv.find('=');
+            if (!kv.empty()) o.extra[kv.substr(0, eq)] = eq == std::string::npos ? "" : kv.substr(eq + 1);
+        }
+        std::vector<const Graph*> progs;
+        for (int i = 0; i < nprog; ++i) progs.push_back(static_cast<const Graph*>(graphs[i]));
+        box->session = box->backend->compile(progs, static_cast<Store*>(store)->views, o);
+        return box.release();
+    } catch (const std::exception& e) {
+        g_error = e.what();
+        return nullptr;
+    }
+}
+
 void xss_free(void* s) { delete static_cast<SessionBox*>(s); }
 
 int xss_run(void* s, int64_t program, int n_in, const char* const* names, const int* dtypes, const int* ranks,

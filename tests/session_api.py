@@ -63,6 +63,7 @@ def lib():
         "xsw_new": ([], P), "xsw_free": ([P], None),
         "xsw_add": ([P, C.c_char_p, C.c_int, C.c_int, dims, P], C.c_int),
         "xss_compile": ([C.c_int, C.POINTER(P), P, C.c_int, I64_, C.c_int, C.c_int, C.c_char_p], P),
+        "xss_compile_opts": ([C.c_int, C.POINTER(P), P, C.c_int, I64_, C.c_int, C.c_int, C.c_char_p, C.c_char_p], P),
         "xss_free": ([P], None),
         "xss_run": ([P, I64_, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_int), C.POINTER(C.c_int), dims,
                      C.POINTER(P), C.c_int, C.POINTER(C.c_char_p)], C.c_int),
@@ -212,13 +213,17 @@ class Graph:
 class Session:
     """Backend("hip").compile(programs, weights, options)."""
 
-    def __init__(self, graphs, weights=None, max_context=4096, kv=(KV_I8, KV_I8), precision=F32, device=""):
+    def __init__(self, graphs, weights=None, max_context=4096, kv=(KV_I8, KV_I8), precision=F32, device="",
+                 options=None):
+        """options: backend options (SessionOptions::extra), e.g. {"graphs": "0"}."""
         if not isinstance(graphs, (list, tuple)):
             graphs = [graphs]
         self.weights = weights if weights is not None else Weights()
         self.graphs = list(graphs)
         arr = (C.c_void_p * len(graphs))(*[g.h for g in graphs])
-        h = lib().xss_compile(len(graphs), arr, self.weights.h, precision, max_context, kv[0], kv[1], device.encode())
+        extra = ";".join(f"{k}={v}" for k, v in (options or {}).items())
+        h = lib().xss_compile_opts(len(graphs), arr, self.weights.h, precision, max_context, kv[0], kv[1],
+                                   device.encode(), extra.encode())
         if not h:
             raise BackendError(_err())
         self.h = h

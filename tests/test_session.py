@@ -142,6 +142,15 @@ def test_graph_validation():
     _refusal(S.Graph(), "no outputs")
 
 
+def test_graphs_option_values():
+    g = S.Graph()
+    g.output("y", g.silu(g.input("x", S.F32, [S.T, 4])))
+    with pytest.raises(S.BackendError, match="graphs=2"):
+        S.Session(g, options={"graphs": "2"})
+    with pytest.raises(S.BackendError, match="unknown backend option 'fast'"):
+        S.Session(g, options={"fast": "1"})
+
+
 @pytest.mark.skipif(_gpu(), reason="checks the message of a machine without a GPU")
 def test_needs_a_device():
     g = S.Graph()
@@ -384,6 +393,104 @@ def test_kv_decode_steps(ora, hq, hkv, d, window, softcap):
     cache.truncate(0)
     assert s.num_cached() == 0
     one(4)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("graphs", ["1", "0"])
+def test_kv_decode_many_steps(ora, graphs):
+    """Forty decode steps after a prefill, through key counts 9 .. 49 (length buckets 16, 32 and 64), with the
+    repeated steps replayed from captured graphs (graphs=1) or launched one by one (graphs=0); then a truncate, more
+    steps, a reset and a fresh prefill. Every step against cpu-ref's cache on the oracle."""
+    hq, hkv, d = 8, 2, 128
+    rng = np.random.default_rng(91)
+    prefill, reader = _kv_programs(hq, hkv, d)
+    step(f"session kv {40} steps graphs={graphs}")
+    s = S.Session([prefill, reader], max_context=64, options={"graphs": graphs})
+    cache = _Cache(ora, hkv, d)
+    scale = 1 / math.sqrt(d)
+
+    def one(tokens, program=0):
+        q = rng.standard_normal((tokens, hq, d)).astype(np.float32)
+        inputs = {"q": (q, S.F32)}
+        if program == 0:
+            k = rng.standard_normal((tokens, hkv, d)).astype(np.float32)
+            v = rng.standard_normal((tokens, hkv, d)).astype(np.float32)
+            inputs.update({"k": (k, S.F32), "v": (v, S.F32)})
+            cache.append(k, v)
+        o = s.run(inputs, program=program)["o"]
+        want = ora.attention(q, cache.k, cache.v, scale, 0.0, 0, True)
+        attention_close(o, want, f"graphs={graphs} program {program}, {tokens} tokens at L {len(cache.k)}")
+
+    one(8)
+    for i in range(40):
+        one(1)
+        if i % 9 == 4:
+            one(1, program=1)  # a reader program replayed at the same key count
+    assert s.num_cached() == 48
+    s.truncate(20)
+    cache.truncate(20)
+    for _ in range(5):
+        one(1)
+    one(3)
+    s.reset()
+    cache.truncate(0)
+    one(5)
+    for _ in range(4):
+        one(1)
+    assert s.num_cached() == 9
+
+
+def _decoder_steps(graphs, layers, steps, hq=16, hkv=4, d=128):
+    """A decoder-shaped step graph -- per layer the residual add and RMSNorm, the Q and K RoPE pair, the int8 KV
+    append, attention and the gated multiply -- run for a prefill and `steps` decode steps; returns the outputs of every
+    step and the mean wall time of a decode step (Session::run, inputs up and outputs down included)."""
+    import time
+    hid = hq * d
+    rng = np.random.default_rng(92)
+    w = S.Weights()
+    w.add("norm", (1 + 0.1 * rng.standard_normal(hid)).astype(np.float32))
+    w.add("inv", (1.0 / (1e6 ** (np.arange(0, d, 2) / d))).astype(np.float32))
+    g = S.Graph()
+    x = g.input("x", S.F32, [S.T, hid])
+    r = g.input("r", S.F32, [S.T, hid])
+    pos = g.input("pos", S.I64, [S.T])
+    nw, fi = g.weight(w, "norm"), g.weight(w, "inv")
+    for layer in range(layers):
+        h = g.add(x, r)
+        n = g.rms_norm(h, nw)
+        qr = g.rope(g.reshape(n, [S.T, hq, d]), pos, fi)
+        k = g.reshape(g.slice(n, 1, 0, hkv * d), [S.T, hkv, d])
+        ka, va = g.kv_cache(g.kv_slot(hkv, d, 0, label=f"l{layer}"), g.rope(k, pos, fi), k)
+        x = g.mul(g.silu(g.reshape(g.attention(qr, ka, va, 1 / math.sqrt(d)), [S.T, hid])), n)
+        r = h
+    g.output("x", x)
+    s = S.Session(g, w, max_context=1024, options={"graphs": graphs})
+    feed = np.random.default_rng(93)
+
+    def run(t, p0):
+        return s.run({"x": (feed.standard_normal((t, hid)).astype(np.float32), S.F32),
+                      "r": (feed.standard_normal((t, hid)).astype(np.float32), S.F32),
+                      "pos": (np.arange(p0, p0 + t).astype(np.int64), S.I64)})["x"]
+
+    outs = [run(64, 0)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        outs.append(run(1, 64 + i))
+    return outs, (time.perf_counter() - t0) / steps
+
+
+@pytest.mark.gpu
+def test_decoder_steps_replayed_match_eager():
+    """The decoder-shaped graph (8 layers, about 60 launches a step) with graphs on and off: every step's output
+    agrees (the replayed attention splits its keys as for its length bucket, the eager one as for the exact count),
+    and the wall time per decode step of each mode is printed."""
+    step("decoder steps graphs on / off")
+    on, t_on = _decoder_steps("1", 8, 120)
+    off, t_off = _decoder_steps("0", 8, 120)
+    for i, (a, b) in enumerate(zip(on, off)):
+        attention_close(a, b, f"decode step {i}", atol=1e-4, rtol=1e-3)
+    print(f"[session] 8-layer decode step: {t_on * 1e6:.1f} us with graph replay, {t_off * 1e6:.1f} us launched "
+          f"one by one", flush=True)
 
 
 @pytest.mark.gpu

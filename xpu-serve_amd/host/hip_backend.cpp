@@ -93,14 +93,15 @@ public:
     ~DeviceMemory() {
         if (p_ != nullptr) xs_hip_free(p_);
     }
-    // At least `bytes`; the contents are not kept when it grows.
-    void grow(size_t bytes) {
-        if (bytes <= n_) return;
+    // At least `bytes`; the contents are not kept when it grows. True when the memory moved.
+    bool grow(size_t bytes) {
+        if (bytes <= n_) return false;
         if (p_ != nullptr) check(xs_hip_free(p_), "free");
         p_ = nullptr;
         n_ = 0;
         check(xs_hip_malloc(&p_, std::max<size_t>(bytes, 256)), "malloc");
         n_ = std::max<size_t>(bytes, 256);
+        return true;
     }
     char* get() const { return static_cast<char*>(p_); }
     size_t size() const { return n_; }
@@ -204,6 +205,9 @@ class HipSession;
 class Program {
 public:
     Program(const Graph& g, HipSession& s, size_t index);  // plans; touches no device
+    ~Program();
+    Program(const Program&) = delete;
+    Program& operator=(const Program&) = delete;
     void upload();                                          // weights and constants to the device
 
     void run(const TensorMap& inputs, TensorMap& outputs, std::span<const std::string> only);
@@ -221,13 +225,24 @@ private:
         std::vector<int32_t> scratch;           // per node: its scratch block, or -1
         std::vector<size_t> scratch_bytes;
         size_t arena_bytes = 0;
+        // Captured steps by key-count bucket (see Program::run): the executable graph, the arena generation its
+        // addresses belong to, and how often the bucket has run.
+        struct Captured {
+            void* exec = nullptr;
+            uint64_t arena_gen = 0;
+            int runs = 0;
+        };
+        std::map<int, Captured> graphs;
     };
 
     const std::vector<char>& live_for(std::span<const std::string> only);
     RunPlan& plan_for(int64_t T, std::span<const std::string> only);
     Dims resolve(const Dims& d, int64_t T, int64_t L) const;
     bool needs_f32(size_t node, size_t operand) const;
-    void launch(size_t i, const RunPlan& p, int64_t T, int64_t L);
+    // replay_cap > 0: the launch goes into a captured graph, the KV append and attention read the step record
+    // (first row, key count) from device memory, and the attention's split is the one of replay_cap keys.
+    void launch(size_t i, const RunPlan& p, int64_t T, int64_t L, int64_t replay_cap = 0);
+    void launch_all(RunPlan& p, int64_t T, int64_t L);
     char* ptr(const RunPlan& p, Value v) const;
     const char* ptr_f32(const RunPlan& p, Value v) const;
     DType dtype(Value v) const { return dt_[static_cast<size_t>(v.node)][static_cast<size_t>(v.index)]; }
@@ -275,6 +290,20 @@ public:
     // Device copies of leaves: weights by name ("w:<name>", shared by the programs), constants by program and node.
     std::map<std::string, Leaf>& leaves() { return leaves_; }
     DeviceMemory& arena() { return arena_; }
+    // Grows the arena; when it moves, every captured step (which holds its addresses) is stale.
+    void grow_arena(size_t bytes) {
+        if (arena_.grow(bytes)) ++arena_gen_;
+    }
+    uint64_t arena_gen() const { return arena_gen_; }
+    // HIP-graph replay of repeated steps: the "graphs" backend option ("1", the default, or "0").
+    bool graphs() const { return graphs_; }
+    // The step record a replayed step reads from device memory: [first token the step appends, keys held].
+    const int64_t* step_record() const { return reinterpret_cast<const int64_t*>(step_.get()); }
+    void set_step(int64_t first, int64_t keys) {
+        step_host_[0] = first;
+        step_host_[1] = keys;
+        check(xs_hip_memcpy_h2d(step_.get(), step_host_, sizeof(step_host_), stream_), "step record");
+    }
 
     int slot_for(const graph::KvSlot& s) {
         for (size_t i = 0; i < kv_.size(); ++i) {
@@ -300,6 +329,10 @@ private:
     std::vector<KvState> kv_;
     std::map<std::string, Leaf> leaves_;
     DeviceMemory arena_;
+    uint64_t arena_gen_ = 0;
+    bool graphs_ = true;
+    DeviceMemory step_;
+    int64_t step_host_[2] = {0, 0};  // read by the copy queued in set_step until the step's end
     std::vector<std::unique_ptr<Program>> programs_;
 };
 
@@ -978,7 +1011,7 @@ const char* Program::ptr_f32(const RunPlan& p, Value v) const {
 // ---------------------------------------------------------------------------------------------------------------
 // Launches.
 
-void Program::launch(size_t i, const RunPlan& p, int64_t T, int64_t L) {
+void Program::launch(size_t i, const RunPlan& p, int64_t T, int64_t L, int64_t replay_cap) {
     const Node& nd = g_.nodes()[i];
     const NodePlan& np = plan_[i];
     void* const st = s_.stream();
@@ -1173,10 +1206,17 @@ void Program::launch(size_t i, const RunPlan& p, int64_t T, int64_t L) {
             const int64_t first = L - T;  // rows [L - T, L) of the slot
             for (int which = 0; which < 2; ++which) {
                 const Value x = np.reads[static_cast<size_t>(which)];
-                char* codes = (which == 0 ? kv.kc : kv.vc).get() + first * kv.heads * kv.dim;
-                char* scales = (which == 0 ? kv.ks : kv.vs).get() + first * kv.heads * 4;
-                check(xs_hip_quantize_kv(st, XS_KV_I8, abi(dtype(x)), ptr(p, x), codes, scales, T * kv.heads, kv.dim),
-                      "KvCache");
+                char* codes = (which == 0 ? kv.kc : kv.vc).get();
+                char* scales = (which == 0 ? kv.ks : kv.vs).get();
+                if (replay_cap > 0) {  // the first token read from the step record at replay
+                    check(xs_hip_quantize_kv_at(st, abi(dtype(x)), ptr(p, x), codes, scales, T * kv.heads, kv.dim,
+                                                s_.step_record(), kv.heads, kv.cap * kv.heads),
+                          "KvCache");
+                } else {
+                    check(xs_hip_quantize_kv(st, XS_KV_I8, abi(dtype(x)), ptr(p, x), codes + first * kv.heads * kv.dim,
+                                             scales + first * kv.heads * 4, T * kv.heads, kv.dim),
+                          "KvCache");
+                }
             }
             return;
         }
@@ -1186,14 +1226,20 @@ void Program::launch(size_t i, const RunPlan& p, int64_t T, int64_t L) {
             const Loc& kl = p.locs[static_cast<size_t>(np.reads[1].node)][0];
             KvState& kv = s_.kv()[static_cast<size_t>(kl.id)];
             const Dims& qs = in_shape(q);
-            const int64_t split = xs_hip_attention_i8_split(qs[0], kv.heads, L);
-            check(xs_hip_attention_i8(st, f32(0), kv.kc.get(), kv.ks.get(), kv.vc.get(), kv.vs.get(),
-                                      reinterpret_cast<float*>(ptr(p, Value{static_cast<int32_t>(i), 0})), qs[0], qs[1],
-                                      kv.heads, qs[2], L, a.scale, a.softcap, a.sliding_window, a.causal ? 1 : 0,
-                                      split,
-                                      split > 1 ? s_.arena().get() + p.block_offset[static_cast<size_t>(p.scratch[i])]
-                                                : nullptr),
-                  what);
+            const int64_t split = xs_hip_attention_i8_split(qs[0], kv.heads, replay_cap > 0 ? replay_cap : L);
+            auto* out_p = reinterpret_cast<float*>(ptr(p, Value{static_cast<int32_t>(i), 0}));
+            char* scratch = split > 1 ? s_.arena().get() + p.block_offset[static_cast<size_t>(p.scratch[i])] : nullptr;
+            if (replay_cap > 0) {  // the key count read from the step record at replay
+                check(xs_hip_attention_i8_at(st, f32(0), kv.kc.get(), kv.ks.get(), kv.vc.get(), kv.vs.get(), out_p,
+                                             qs[0], qs[1], kv.heads, qs[2], kv.cap, s_.step_record() + 1, a.scale,
+                                             a.softcap, a.sliding_window, a.causal ? 1 : 0, split, scratch),
+                      what);
+            } else {
+                check(xs_hip_attention_i8(st, f32(0), kv.kc.get(), kv.ks.get(), kv.vc.get(), kv.vs.get(), out_p, qs[0],
+                                          qs[1], kv.heads, qs[2], L, a.scale, a.softcap, a.sliding_window,
+                                          a.causal ? 1 : 0, split, scratch),
+                      what);
+            }
             return;
         }
         case Op::SliceCopy: {
@@ -1257,7 +1303,7 @@ void Program::run(const TensorMap& inputs, TensorMap& outputs, std::span<const s
         }
     }
     RunPlan& p = plan_for(T, only);
-    s_.arena().grow(p.arena_bytes);
+    s_.grow_arena(p.arena_bytes);
     // Inputs.
     for (const Value& v : g_.inputs()) {
         const auto i = static_cast<size_t>(v.node);
@@ -1265,9 +1311,7 @@ void Program::run(const TensorMap& inputs, TensorMap& outputs, std::span<const s
         const HostTensor& t = inputs.at(std::get<graph::InputAttrs>(nodes[i].attrs).name);
         if (t.nbytes() > 0) check(xs_hip_memcpy_h2d(ptr(p, v), t.raw(), t.nbytes(), s_.stream()), "input upload");
     }
-    for (size_t i = 0; i < nodes.size(); ++i) {
-        if (p.live[i] && plan_[i].op != Op::None) launch(i, p, T, L);
-    }
+    launch_all(p, T, L);
     // Outputs: f32 for floats (16-bit values widened on the device), integers as they are.
     TensorMap result;
     for (const auto& o : g_.outputs()) {
@@ -1293,6 +1337,59 @@ void Program::run(const TensorMap& inputs, TensorMap& outputs, std::span<const s
     for (auto& [name, t] : result) outputs[name] = std::move(t);
 }
 
+// The step's launches. With graphs on, a (plan, key-count bucket) that runs a second time is captured into a HIP
+// graph, and later runs replay it: the bucket is the smallest power of two >= L (capped at the slots' capacity), the
+// attention takes that bucket's split, and the KV append and attention read where to append and how many keys there
+// are from the step record uploaded before the replay. A one-off step (a prefill of a new length) runs eagerly.
+void Program::launch_all(RunPlan& p, int64_t T, int64_t L) {
+    const auto each = [&](int64_t replay_cap) {
+        for (size_t i = 0; i < g_.nodes().size(); ++i) {
+            if (p.live[i] && plan_[i].op != Op::None) launch(i, p, T, L, replay_cap);
+        }
+    };
+    // Graphs off, or a reading step with fewer keys than queries (whose refusal comes from the launch): eagerly.
+    if (!s_.graphs() || (!appends_ && L < T)) return each(0);
+    int64_t cap = 0;  // the bucket's key count (0 without KV slots)
+    if (!slot_of_.empty()) {
+        cap = 1;
+        while (cap < L) cap *= 2;
+        for (const int slot : slot_of_) cap = std::min(cap, s_.kv()[static_cast<size_t>(slot)].cap);
+        cap = std::max<int64_t>(cap, 1);
+    }
+    RunPlan::Captured& g = p.graphs[static_cast<int>(cap)];
+    if (g.exec != nullptr && g.arena_gen != s_.arena_gen()) {  // the arena moved under it
+        check(xs_hip_graph_destroy(g.exec), "graph");
+        g = RunPlan::Captured{};
+    }
+    s_.set_step(L - T, L);
+    if (g.exec == nullptr && ++g.runs >= 2) {
+        check(xs_hip_stream_begin_capture(s_.stream()), "capture");
+        try {
+            each(std::max<int64_t>(cap, 1));
+        } catch (...) {
+            void* discard = nullptr;
+            xs_hip_stream_end_capture(s_.stream(), &discard);
+            if (discard != nullptr) xs_hip_graph_destroy(discard);
+            throw;
+        }
+        check(xs_hip_stream_end_capture(s_.stream(), &g.exec), "capture");
+        g.arena_gen = s_.arena_gen();
+    }
+    if (g.exec != nullptr) {
+        check(xs_hip_graph_launch(g.exec, s_.stream()), "graph replay");
+    } else {
+        each(0);
+    }
+}
+
+Program::~Program() {
+    for (auto& [key, plan] : plans_) {
+        for (auto& [cap, g] : plan.graphs) {
+            if (g.exec != nullptr) xs_hip_graph_destroy(g.exec);
+        }
+    }
+}
+
 int64_t Program::cached() const {
     if (slot_of_.empty() || !appends_) return 0;
     return s_.kv()[static_cast<size_t>(slot_of_[0])].len;
@@ -1311,7 +1408,11 @@ HipSession::HipSession(std::span<const Graph* const> programs, const WeightStore
     XS_CHECK(!programs.empty(), "hip: nothing to compile");
     XS_CHECK(options_.max_context > 0, "hip: max_context ", options_.max_context);
     XS_CHECK(options_.rewind_tokens >= 0, "hip: rewind_tokens ", options_.rewind_tokens);
-    for (const auto& [key, value] : options_.extra) fail("hip: unknown backend option '", key, "'");
+    for (const auto& [key, value] : options_.extra) {
+        XS_CHECK(key == "graphs", "hip: unknown backend option '", key, "' (known: graphs)");
+        XS_CHECK(value == "0" || value == "1", "hip: backend option graphs=", value, " (expected 0 or 1)");
+        graphs_ = value == "1";
+    }
     // Plan every program first: what this backend cannot run is refused before any device work.
     for (size_t i = 0; i < programs.size(); ++i) programs_.push_back(std::make_unique<Program>(*programs[i], *this, i));
     int count = 0;
@@ -1336,6 +1437,7 @@ HipSession::HipSession(std::span<const Graph* const> programs, const WeightStore
             k.ks.grow(rows * 4);
             k.vs.grow(rows * 4);
         }
+        step_.grow(sizeof(step_host_));
         for (auto& p : programs_) p->upload();
         check(xs_hip_stream_synchronize(stream_), "weight upload");
     } catch (...) {
