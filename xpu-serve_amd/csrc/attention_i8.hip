@@ -627,11 +627,16 @@ extern "C" {
 
 int64_t xs_hip_attention_i8_split(int64_t tokens, int64_t kv_heads, int64_t kv_len) {
     if (tokens <= 0 || kv_heads <= 0 || kv_len <= 0) return 1;
-    // A workgroup (of eight waves) for every CU, each wave with at least two tiles of keys.
+    // Up to a workgroup for every CU, and as many as one tile of keys each: a split's workgroups all take their first
+    // tile at once, and a decode step waits on the slowest. A cache of at most two tiles a wave stays in one
+    // workgroup, where the combine launch would cost more than the split saves. Measured on MI355X, one query token,
+    // head_dim 128: with 16 query and 4 KV heads, 1024 keys 10.2 us (4 splits, two tiles a wave: 13.0), 4096 keys
+    // 10.8 us (16 splits: 14.3), 256 keys 9.9 us unsplit or split alike, 128 keys 8.0 us unsplit (9.8 split); with 32
+    // and 8, 256 keys 9.9 us split in four (12.9 unsplit), 4096 keys 11.5 us (32 splits: 13.4).
     const int hg = heads_per_group(kv_heads, kMaxWaves);
     const int64_t groups = tokens * (kv_heads / hg);
     int64_t split = (static_cast<int64_t>(device_cus()) + groups - 1) / groups;
-    const int64_t by_len = kv_len / (2 * kTile * (kMaxWaves / hg));
+    const int64_t by_len = kv_len <= 2 * kTile * (kMaxWaves / hg) ? 1 : kv_len / kTile;
     if (split > by_len) split = by_len;
     if (split > kMaxSplit) split = kMaxSplit;
     return split < 1 ? 1 : split;
