@@ -106,6 +106,12 @@ int xs_hip_memset(void* ptr, int value, size_t bytes, void* stream);
 int xs_hip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream); /* synchronous w.r.t. the host */
 int xs_hip_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream); /* synchronous w.r.t. the host */
 int xs_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream); /* asynchronous */
+/* Asynchronous host copies, for host memory from xs_hip_host_alloc (page-locked): the host memory must stay as it is
+ * until the stream has finished the copy. */
+int xs_hip_memcpy_h2d_async(void* dst, const void* src, size_t bytes, void* stream);
+int xs_hip_memcpy_d2h_async(void* dst, const void* src, size_t bytes, void* stream);
+int xs_hip_host_alloc(void** ptr, size_t bytes);
+int xs_hip_host_free(void* ptr);
 int xs_hip_stream_create(void** stream);
 int xs_hip_stream_destroy(void* stream);
 int xs_hip_stream_synchronize(void* stream);

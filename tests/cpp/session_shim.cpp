@@ -5,6 +5,8 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <algorithm>
+#include <chrono>
 #include <string>
 #include <vector>
 
@@ -278,6 +280,29 @@ int xss_run(void* s, int64_t program, int n_in, const char* const* names, const 
         std::vector<std::string> o(only, only + n_only);
         b.outputs.clear();
         b.session->run(static_cast<size_t>(program), in, b.outputs, o);
+        return int64_t{0};
+    }));
+}
+
+// Runs `program` `iters` times on the same inputs and stores the mean wall time of one Session::run in *us_per_run:
+// the backend's step cost (inputs up, launches or a graph replay, outputs down, the wait) timed from C++.
+int xss_time_runs(void* s, int64_t program, int n_in, const char* const* names, const int* dtypes, const int* ranks,
+                  const int64_t* all_dims, const void* const* datas, int iters, double* us_per_run) {
+    return static_cast<int>(guard([&] {
+        SessionBox& b = *static_cast<SessionBox*>(s);
+        TensorMap in;
+        const int64_t* d = all_dims;
+        for (int i = 0; i < n_in; ++i) {
+            in[names[i]] = HostTensor::borrow(static_cast<DType>(dtypes[i]), dims(ranks[i], d), const_cast<void*>(datas[i]));
+            d += ranks[i];
+        }
+        const auto t0 = std::chrono::steady_clock::now();
+        for (int k = 0; k < iters; ++k) {
+            b.outputs.clear();
+            b.session->run(static_cast<size_t>(program), in, b.outputs, {});
+        }
+        const std::chrono::duration<double, std::micro> dt = std::chrono::steady_clock::now() - t0;
+        *us_per_run = dt.count() / std::max(iters, 1);
         return int64_t{0};
     }));
 }

@@ -65,6 +65,8 @@ def lib():
         "xss_compile": ([C.c_int, C.POINTER(P), P, C.c_int, I64_, C.c_int, C.c_int, C.c_char_p], P),
         "xss_compile_opts": ([C.c_int, C.POINTER(P), P, C.c_int, I64_, C.c_int, C.c_int, C.c_char_p, C.c_char_p], P),
         "xss_free": ([P], None),
+        "xss_time_runs": ([P, I64_, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_int), C.POINTER(C.c_int), dims,
+                           C.POINTER(P), C.c_int, C.POINTER(C.c_double)], C.c_int),
         "xss_run": ([P, I64_, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_int), C.POINTER(C.c_int), dims,
                      C.POINTER(P), C.c_int, C.POINTER(C.c_char_p)], C.c_int),
         "xss_output": ([P, C.c_char_p, C.POINTER(C.c_int), C.POINTER(C.c_int), dims, C.POINTER(P)], C.c_int),
@@ -231,6 +233,26 @@ class Session:
     def __del__(self):
         if getattr(self, "h", None):
             lib().xss_free(self.h)
+
+    def time_runs(self, inputs, iters, program=0):
+        """Mean wall time in microseconds of one Session::run of `program` on these inputs, timed in C++."""
+        names, dtypes, ranks, dims, datas, keep = [], [], [], [], [], []
+        for name, (arr, dtype) in inputs.items():
+            a = np.ascontiguousarray(arr, NP[dtype])
+            keep.append(a)
+            names.append(name.encode())
+            dtypes.append(dtype)
+            ranks.append(a.ndim)
+            dims.extend(a.shape)
+            datas.append(a.ctypes.data_as(C.c_void_p))
+        n = len(names)
+        us = C.c_double()
+        rc = lib().xss_time_runs(self.h, program, n, (C.c_char_p * n)(*names), (C.c_int * n)(*dtypes),
+                                 (C.c_int * n)(*ranks), (C.c_int64 * len(dims))(*dims), (C.c_void_p * n)(*datas), iters,
+                                 C.byref(us))
+        if rc != 0:
+            raise BackendError(_err())
+        return us.value
 
     def run(self, inputs, program=0, only=()):
         """inputs: {name: (array, dtype)}; returns {name: array} of the outputs run (f32 for floats)."""

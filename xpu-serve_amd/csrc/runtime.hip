@@ -187,6 +187,23 @@ int xs_hip_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream) {
     return check_hip(hipStreamSynchronize(as_stream(stream)), "memcpy d2h sync");
 }
 
+int xs_hip_memcpy_h2d_async(void* dst, const void* src, size_t bytes, void* stream) {
+    return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, as_stream(stream)), "memcpy h2d");
+}
+
+int xs_hip_memcpy_d2h_async(void* dst, const void* src, size_t bytes, void* stream) {
+    return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, as_stream(stream)), "memcpy d2h");
+}
+
+int xs_hip_host_alloc(void** ptr, size_t bytes) {
+    if (ptr == nullptr) return fail(XS_HIP_EINVAL, "xs_hip_host_alloc: null output");
+    *ptr = nullptr;
+    if (bytes == 0) return XS_HIP_OK;
+    return check_hip(hipHostMalloc(ptr, bytes, hipHostMallocDefault), "hipHostMalloc");
+}
+
+int xs_hip_host_free(void* ptr) { return ptr == nullptr ? XS_HIP_OK : check_hip(hipHostFree(ptr), "hipHostFree"); }
+
 int xs_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
     return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream)), "memcpy d2d");
 }

@@ -111,6 +111,31 @@ private:
     size_t n_ = 0;
 };
 
+// Page-locked host memory owned by the session: the staging of a step's host copies, which then run asynchronously.
+class PinnedMemory {
+public:
+    PinnedMemory() = default;
+    PinnedMemory(const PinnedMemory&) = delete;
+    PinnedMemory& operator=(const PinnedMemory&) = delete;
+    ~PinnedMemory() {
+        if (p_ != nullptr) xs_hip_host_free(p_);
+    }
+    // At least `bytes`; the contents are not kept when it grows (only between steps, when no copy is pending).
+    void grow(size_t bytes) {
+        if (bytes <= n_) return;
+        if (p_ != nullptr) check(xs_hip_host_free(p_), "free");
+        p_ = nullptr;
+        n_ = 0;
+        check(xs_hip_host_alloc(&p_, bytes), "host alloc");
+        n_ = bytes;
+    }
+    char* get() const { return static_cast<char*>(p_); }
+
+private:
+    void* p_ = nullptr;
+    size_t n_ = 0;
+};
+
 // f32 from IEEE binary16 / bfloat16 bits, exactly (the widening of the reference's util/half.h).
 float widen(DType t, uint16_t h) {
     uint32_t bits;
@@ -297,12 +322,19 @@ public:
     uint64_t arena_gen() const { return arena_gen_; }
     // HIP-graph replay of repeated steps: the "graphs" backend option ("1", the default, or "0").
     bool graphs() const { return graphs_; }
-    // The step record a replayed step reads from device memory: [first token the step appends, keys held].
+    // The step record a replayed step reads from device memory: [first token the step appends, keys held]. Its host
+    // copy is the first 16 bytes of the staging.
     const int64_t* step_record() const { return reinterpret_cast<const int64_t*>(step_.get()); }
     void set_step(int64_t first, int64_t keys) {
-        step_host_[0] = first;
-        step_host_[1] = keys;
-        check(xs_hip_memcpy_h2d(step_.get(), step_host_, sizeof(step_host_), stream_), "step record");
+        auto* h = reinterpret_cast<int64_t*>(staging_.get());
+        h[0] = first;
+        h[1] = keys;
+        check(xs_hip_memcpy_h2d_async(step_.get(), h, 2 * sizeof(int64_t), stream_), "step record");
+    }
+    // The step's host staging: the step record, then the inputs and outputs (256-byte aligned pieces).
+    char* staging(size_t bytes) {
+        staging_.grow(std::max<size_t>(bytes, 256));
+        return staging_.get();
     }
 
     int slot_for(const graph::KvSlot& s) {
@@ -332,7 +364,7 @@ private:
     uint64_t arena_gen_ = 0;
     bool graphs_ = true;
     DeviceMemory step_;
-    int64_t step_host_[2] = {0, 0};  // read by the copy queued in set_step until the step's end
+    PinnedMemory staging_;
     std::vector<std::unique_ptr<Program>> programs_;
 };
 
@@ -1304,16 +1336,36 @@ void Program::run(const TensorMap& inputs, TensorMap& outputs, std::span<const s
     }
     RunPlan& p = plan_for(T, only);
     s_.grow_arena(p.arena_bytes);
+    // The host side goes through page-locked staging, so every copy is asynchronous and the step waits once: the step
+    // record, then the inputs, then the outputs.
+    size_t stage_bytes = 256;
+    for (const Value& v : g_.inputs()) {
+        const auto i = static_cast<size_t>(v.node);
+        if (p.live[i]) stage_bytes += align_up(inputs.at(std::get<graph::InputAttrs>(nodes[i].attrs).name).nbytes());
+    }
+    for (const auto& o : g_.outputs()) {
+        if (!only.empty() && std::find(only.begin(), only.end(), o.name) == only.end()) continue;
+        const DType d = dtype(o.value);
+        const Dims& shape = p.shapes[static_cast<size_t>(o.value.node)][static_cast<size_t>(o.value.index)];
+        stage_bytes += align_up(static_cast<size_t>(numel(shape)) * dtype_size(is_float(d) ? DType::F32 : d));
+    }
+    char* const stage = s_.staging(stage_bytes);
+    size_t at = 256;
     // Inputs.
     for (const Value& v : g_.inputs()) {
         const auto i = static_cast<size_t>(v.node);
         if (!p.live[i]) continue;
         const HostTensor& t = inputs.at(std::get<graph::InputAttrs>(nodes[i].attrs).name);
-        if (t.nbytes() > 0) check(xs_hip_memcpy_h2d(ptr(p, v), t.raw(), t.nbytes(), s_.stream()), "input upload");
+        if (t.nbytes() > 0) {
+            std::memcpy(stage + at, t.raw(), t.nbytes());
+            check(xs_hip_memcpy_h2d_async(ptr(p, v), stage + at, t.nbytes(), s_.stream()), "input upload");
+            at += align_up(t.nbytes());
+        }
     }
     launch_all(p, T, L);
     // Outputs: f32 for floats (16-bit values widened on the device), integers as they are.
     TensorMap result;
+    std::vector<std::pair<std::string, size_t>> staged;  // output, its place in the staging
     for (const auto& o : g_.outputs()) {
         if (!only.empty() && std::find(only.begin(), only.end(), o.name) == only.end()) continue;
         const DType d = dtype(o.value);
@@ -1327,10 +1379,18 @@ void Program::run(const TensorMap& inputs, TensorMap& outputs, std::span<const s
             check(xs_hip_convert(s_.stream(), abi(d), src, XS_F32, dst, numel(shape)), "output");
             src = dst;
         }
-        if (t.nbytes() > 0) check(xs_hip_memcpy_d2h(t.raw(), src, t.nbytes(), s_.stream()), "output download");
+        if (t.nbytes() > 0) {
+            check(xs_hip_memcpy_d2h_async(stage + at, src, t.nbytes(), s_.stream()), "output download");
+            staged.emplace_back(o.name, at);
+            at += align_up(t.nbytes());
+        }
         result[o.name] = std::move(t);
     }
     check(xs_hip_stream_synchronize(s_.stream()), "step");
+    for (const auto& [name, off] : staged) {
+        HostTensor& t = result.at(name);
+        std::memcpy(t.raw(), stage + off, t.nbytes());
+    }
     if (appends_) {
         for (const int slot : slot_of_) s_.kv()[static_cast<size_t>(slot)].len = L;
     }
@@ -1437,7 +1497,8 @@ HipSession::HipSession(std::span<const Graph* const> programs, const WeightStore
             k.ks.grow(rows * 4);
             k.vs.grow(rows * 4);
         }
-        step_.grow(sizeof(step_host_));
+        step_.grow(2 * sizeof(int64_t));
+        staging(256);
         for (auto& p : programs_) p->upload();
         check(xs_hip_stream_synchronize(stream_), "weight upload");
     } catch (...) {

@@ -68,6 +68,10 @@ _SIGS = {
     "xs_hip_memcpy_h2d": [_P, _P, C.c_size_t, _P],
     "xs_hip_memcpy_d2h": [_P, _P, C.c_size_t, _P],
     "xs_hip_memcpy_d2d": [_P, _P, C.c_size_t, _P],
+    "xs_hip_memcpy_h2d_async": [_P, _P, C.c_size_t, _P],
+    "xs_hip_memcpy_d2h_async": [_P, _P, C.c_size_t, _P],
+    "xs_hip_host_alloc": [C.POINTER(_P), C.c_size_t],
+    "xs_hip_host_free": [_P],
     "xs_hip_stream_create": [C.POINTER(_P)],
     "xs_hip_stream_destroy": [_P],
     "xs_hip_stream_synchronize": [_P],
