@@ -66,14 +66,16 @@ __device__ __forceinline__ int64_t first_row(const QuantDest& d, int64_t rows) {
     return off < 0 || off > d.cap - rows ? -1 : off;
 }
 
-template <typename T, int L, int VPL, int U>
+template <typename T, int L, int VPL, int U, bool DEST>
 __global__ __launch_bounds__(kQBlock) void quantize_i8_vec(const typename T::storage* __restrict__ x,
                                                           int8_t* __restrict__ codes, float* __restrict__ scales,
                                                           int64_t rows, int64_t width, QuantDest dest) {
-    const int64_t off = first_row(dest, rows);
-    if (off < 0) return;
-    codes += off * width;
-    scales += off;
+    if constexpr (DEST) {
+        const int64_t off = first_row(dest, rows);
+        if (off < 0) return;
+        codes += off * width;
+        scales += off;
+    }
     constexpr int VEC = vec_elems<T>();
     constexpr int RPW = 64 / L;  // rows per wave
     constexpr int WAVES = kQBlock / 64;
@@ -213,21 +215,22 @@ int launch_quantize(hipStream_t s, const void* x, int8_t* codes, float* scales, 
                         (nvr & (nvr - 1)) == 0 && nvr >= 1 && nvr <= 64;
     const auto* xs = static_cast<const S*>(x);
     constexpr int U = 2;
-    auto go = [&](auto kernel, int lanes) {
+    auto go = [&](auto kernel, auto kernel_dest, int lanes) {
         const int64_t rows_per_tile = (kQBlock / 64) * (64 / lanes) * U;
         const unsigned grid = static_cast<unsigned>((rows + rows_per_tile - 1) / rows_per_tile);
-        kernel<<<grid, kQBlock, 0, s>>>(xs, codes, scales, rows, width, dest);
+        if (dest.row0 != nullptr) kernel_dest<<<grid, kQBlock, 0, s>>>(xs, codes, scales, rows, width, dest);
+        else kernel<<<grid, kQBlock, 0, s>>>(xs, codes, scales, rows, width, dest);
         return check_launch("xs_hip_quantize_kv");
     };
     if (vec_ok) {
         switch (nvr) {
-            case 1: return go(quantize_i8_vec<T, 1, 1, U>, 1);
-            case 2: return go(quantize_i8_vec<T, 2, 1, U>, 2);
-            case 4: return go(quantize_i8_vec<T, 4, 1, U>, 4);
-            case 8: return go(quantize_i8_vec<T, 8, 1, U>, 8);
-            case 16: return go(quantize_i8_vec<T, 16, 1, U>, 16);
-            case 32: return go(quantize_i8_vec<T, 16, 2, U>, 16);
-            case 64: return go(quantize_i8_vec<T, 16, 4, U>, 16);
+            case 1: return go(quantize_i8_vec<T, 1, 1, U, false>, quantize_i8_vec<T, 1, 1, U, true>, 1);
+            case 2: return go(quantize_i8_vec<T, 2, 1, U, false>, quantize_i8_vec<T, 2, 1, U, true>, 2);
+            case 4: return go(quantize_i8_vec<T, 4, 1, U, false>, quantize_i8_vec<T, 4, 1, U, true>, 4);
+            case 8: return go(quantize_i8_vec<T, 8, 1, U, false>, quantize_i8_vec<T, 8, 1, U, true>, 8);
+            case 16: return go(quantize_i8_vec<T, 16, 1, U, false>, quantize_i8_vec<T, 16, 1, U, true>, 16);
+            case 32: return go(quantize_i8_vec<T, 16, 2, U, false>, quantize_i8_vec<T, 16, 2, U, true>, 16);
+            case 64: return go(quantize_i8_vec<T, 16, 4, U, false>, quantize_i8_vec<T, 16, 4, U, true>, 16);
             default: break;
         }
     }
