@@ -269,6 +269,13 @@ int xs_hip_dequantize_kv(void* stream, xs_kv_format format, const void* codes, c
  * cache writes nothing. */
 int xs_hip_quantize_kv_at(void* stream, xs_dtype x_dtype, const void* x, void* codes, void* scales, int64_t rows,
                           int64_t width, const int64_t* row0, int64_t rows_per_unit, int64_t capacity_rows);
+/* No counterpart in the reference (it appends keys and values by two launches): the XS_KV_I8 quantize of a step's
+ * keys k and values v, both [rows, width] of x_dtype, in one launch, into their own caches -- at rows [0, rows) of
+ * k_codes / k_scales and v_codes / v_scales with row0 NULL, or at the device-held row as xs_hip_quantize_kv_at. The
+ * bits are xs_hip_quantize_kv's for each. */
+int xs_hip_quantize_kv_pair(void* stream, xs_dtype x_dtype, const void* k, const void* v, void* k_codes, void* k_scales,
+                            void* v_codes, void* v_scales, int64_t rows, int64_t width, const int64_t* row0,
+                            int64_t rows_per_unit, int64_t capacity_rows);
 
 /* y [rows, width] = x with each group of 128 values rotated as the TurboQuant formats rotate a row (inverse = 0), or
  * rotated back (inverse = 1); f32, 16-byte aligned, y may be x. Replaces sycl_be::kv_rotate (sycl_kernels.h:219-221);

@@ -991,6 +991,38 @@ def test_quantize_kv_at_device_row(ora):
             assert_exact(gs.view(np.uint32), want_s.view(np.uint32), f"scales at token {tok0}")
 
 
+@pytest.mark.parametrize("xdt,width", [(F32, 128), (F16, 128), (BF16, 64), (F32, 100)])
+def test_quantize_kv_pair(ora, xdt, width):
+    """xs_hip_quantize_kv_pair: keys and values in one launch, each bit-exact with xs_hip_quantize_kv, at the buffers'
+    starts (row0 NULL) or at a device-held row of their caches; width 100 takes the scalar path (two launches)."""
+    rng = np.random.default_rng(77)
+    heads, t, cap_tokens = 2, 5, 16
+    k = ora.narrow(rng.standard_normal((t * heads, width)).astype(np.float32), xdt)
+    v = ora.narrow((rng.standard_normal((t * heads, width)) * 4).astype(np.float32), xdt)
+    step(f"quantize_kv_pair {DT[xdt]} width {width}")
+    want = [tuple(a.numpy() for a in X.quantize_kv(dev(x, xdt))) for x in (k, v)]
+    dk, dv = dev(k, xdt), dev(v, xdt)
+    for tok0 in (None, 7):
+        bufs = []
+        for _ in range(2):
+            c = X.DeviceTensor.empty(X.I8, (cap_tokens * heads, width))
+            sc = X.DeviceTensor.empty(F32, (cap_tokens * heads,))
+            X.call("xs_hip_memset", C.c_void_p(c.ptr), 0, C.c_size_t(c.nbytes), None)
+            X.call("xs_hip_memset", C.c_void_p(sc.ptr), 0, C.c_size_t(sc.nbytes), None)
+            bufs.append((c, sc))
+        row0 = _dev_i64(tok0) if tok0 is not None else None
+        X.call("xs_hip_quantize_kv_pair", None, xdt, C.c_void_p(dk.ptr), C.c_void_p(dv.ptr),
+               C.c_void_p(bufs[0][0].ptr), C.c_void_p(bufs[0][1].ptr), C.c_void_p(bufs[1][0].ptr),
+               C.c_void_p(bufs[1][1].ptr), t * heads, width, C.c_void_p(row0.ptr) if row0 else None, heads,
+               cap_tokens * heads)
+        r0 = (tok0 or 0) * heads
+        for (c, sc), (wc, ws), name in zip(bufs, want, ("keys", "values")):
+            gc, gs = c.numpy(), sc.numpy()
+            assert_exact(gc[r0:r0 + t * heads], wc, f"{name} codes at {tok0}")
+            assert_exact(gs[r0:r0 + t * heads], ws, f"{name} scales at {tok0}")
+            assert not gc[:r0].any() and not gc[r0 + t * heads:].any(), f"{name}: rows outside written"
+
+
 def test_attention_i8_at_device_length(ora):
     """xs_hip_attention_i8_at reads the key count from device memory: with the same split it is bit-exact with
     xs_hip_attention_i8 at that count; with the split chosen for the whole capacity (splits without keys) it agrees

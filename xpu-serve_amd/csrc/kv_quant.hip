@@ -66,11 +66,32 @@ __device__ __forceinline__ int64_t first_row(const QuantDest& d, int64_t rows) {
     return off < 0 || off > d.cap - rows ? -1 : off;
 }
 
-template <typename T, int L, int VPL, int U, bool DEST>
+// A second tensor quantized by the same launch (a step's values beside its keys): workgroups from `first_block` on
+// take it, at the same rows of its own cache.
+struct QuantSecond {
+    const void* x = nullptr;
+    int8_t* codes = nullptr;
+    float* scales = nullptr;
+    unsigned first_block = 0;
+};
+
+// MODE 0: one tensor; 1: one tensor at a device-resident destination; 2: two tensors, the destination as in 1 or,
+// with no row0, at their buffers' starts.
+template <typename T, int L, int VPL, int U, int MODE>
 __global__ __launch_bounds__(kQBlock) void quantize_i8_vec(const typename T::storage* __restrict__ x,
                                                           int8_t* __restrict__ codes, float* __restrict__ scales,
-                                                          int64_t rows, int64_t width, QuantDest dest) {
-    if constexpr (DEST) {
+                                                          int64_t rows, int64_t width, QuantDest dest,
+                                                          QuantSecond second) {
+    unsigned block = blockIdx.x;
+    if constexpr (MODE == 2) {
+        if (block >= second.first_block) {
+            x = static_cast<const typename T::storage*>(second.x);
+            codes = second.codes;
+            scales = second.scales;
+            block -= second.first_block;
+        }
+    }
+    if constexpr (MODE != 0) {
         const int64_t off = first_row(dest, rows);
         if (off < 0) return;
         codes += off * width;
@@ -85,7 +106,7 @@ __global__ __launch_bounds__(kQBlock) void quantize_i8_vec(const typename T::sto
     // The block's tile: U * WAVES * RPW contiguous rows; wave w takes rows (u * WAVES + w) * RPW + sub.
     constexpr int64_t stride = WAVES * RPW;
     {
-        const int64_t base = static_cast<int64_t>(blockIdx.x) * (U * WAVES * RPW) + (threadIdx.x >> 6) * RPW + sub;
+        const int64_t base = static_cast<int64_t>(block) * (U * WAVES * RPW) + (threadIdx.x >> 6) * RPW + sub;
         u32x4 raw[U][VPL];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -207,35 +228,60 @@ __global__ __launch_bounds__(kBlock) void dequantize_i8_any(const int8_t* __rest
 
 template <typename T>
 int launch_quantize(hipStream_t s, const void* x, int8_t* codes, float* scales, int64_t rows, int64_t width,
-                    const QuantDest& dest) {
+                    const QuantDest& dest, QuantSecond second = QuantSecond{}) {
     using S = typename T::storage;
     const int64_t row_bytes = width * static_cast<int64_t>(sizeof(S));
     const int64_t nvr = row_bytes / 16;  // 128-bit vectors per row
+    const bool pair = second.x != nullptr;
     const bool vec_ok = row_bytes % 16 == 0 && aligned16(x) && (reinterpret_cast<uintptr_t>(codes) % 8 == 0) &&
-                        (nvr & (nvr - 1)) == 0 && nvr >= 1 && nvr <= 64;
+                        (nvr & (nvr - 1)) == 0 && nvr >= 1 && nvr <= 64 &&
+                        (!pair || (aligned16(second.x) && reinterpret_cast<uintptr_t>(second.codes) % 8 == 0));
     const auto* xs = static_cast<const S*>(x);
     constexpr int U = 2;
-    auto go = [&](auto kernel, auto kernel_dest, int lanes) {
+    auto go = [&](auto kernel, auto kernel_dest, auto kernel_pair, int lanes) {
         const int64_t rows_per_tile = (kQBlock / 64) * (64 / lanes) * U;
         const unsigned grid = static_cast<unsigned>((rows + rows_per_tile - 1) / rows_per_tile);
-        if (dest.row0 != nullptr) kernel_dest<<<grid, kQBlock, 0, s>>>(xs, codes, scales, rows, width, dest);
-        else kernel<<<grid, kQBlock, 0, s>>>(xs, codes, scales, rows, width, dest);
+        if (pair) {
+            second.first_block = grid;
+            kernel_pair<<<2 * grid, kQBlock, 0, s>>>(xs, codes, scales, rows, width, dest, second);
+        } else if (dest.row0 != nullptr) {
+            kernel_dest<<<grid, kQBlock, 0, s>>>(xs, codes, scales, rows, width, dest, second);
+        } else {
+            kernel<<<grid, kQBlock, 0, s>>>(xs, codes, scales, rows, width, dest, second);
+        }
         return check_launch("xs_hip_quantize_kv");
     };
     if (vec_ok) {
         switch (nvr) {
-            case 1: return go(quantize_i8_vec<T, 1, 1, U, false>, quantize_i8_vec<T, 1, 1, U, true>, 1);
-            case 2: return go(quantize_i8_vec<T, 2, 1, U, false>, quantize_i8_vec<T, 2, 1, U, true>, 2);
-            case 4: return go(quantize_i8_vec<T, 4, 1, U, false>, quantize_i8_vec<T, 4, 1, U, true>, 4);
-            case 8: return go(quantize_i8_vec<T, 8, 1, U, false>, quantize_i8_vec<T, 8, 1, U, true>, 8);
-            case 16: return go(quantize_i8_vec<T, 16, 1, U, false>, quantize_i8_vec<T, 16, 1, U, true>, 16);
-            case 32: return go(quantize_i8_vec<T, 16, 2, U, false>, quantize_i8_vec<T, 16, 2, U, true>, 16);
-            case 64: return go(quantize_i8_vec<T, 16, 4, U, false>, quantize_i8_vec<T, 16, 4, U, true>, 16);
+            case 1:
+                return go(quantize_i8_vec<T, 1, 1, U, 0>, quantize_i8_vec<T, 1, 1, U, 1>,
+                          quantize_i8_vec<T, 1, 1, U, 2>, 1);
+            case 2:
+                return go(quantize_i8_vec<T, 2, 1, U, 0>, quantize_i8_vec<T, 2, 1, U, 1>,
+                          quantize_i8_vec<T, 2, 1, U, 2>, 2);
+            case 4:
+                return go(quantize_i8_vec<T, 4, 1, U, 0>, quantize_i8_vec<T, 4, 1, U, 1>,
+                          quantize_i8_vec<T, 4, 1, U, 2>, 4);
+            case 8:
+                return go(quantize_i8_vec<T, 8, 1, U, 0>, quantize_i8_vec<T, 8, 1, U, 1>,
+                          quantize_i8_vec<T, 8, 1, U, 2>, 8);
+            case 16:
+                return go(quantize_i8_vec<T, 16, 1, U, 0>, quantize_i8_vec<T, 16, 1, U, 1>,
+                          quantize_i8_vec<T, 16, 1, U, 2>, 16);
+            case 32:
+                return go(quantize_i8_vec<T, 16, 2, U, 0>, quantize_i8_vec<T, 16, 2, U, 1>,
+                          quantize_i8_vec<T, 16, 2, U, 2>, 16);
+            case 64:
+                return go(quantize_i8_vec<T, 16, 4, U, 0>, quantize_i8_vec<T, 16, 4, U, 1>,
+                          quantize_i8_vec<T, 16, 4, U, 2>, 16);
             default: break;
         }
     }
     const unsigned grid = grid_for(rows, kBlock / 64);
     quantize_i8_any<T><<<grid, kBlock, 0, s>>>(xs, codes, scales, rows, width, dest);
+    if (pair)  // the second tensor by a second launch on this path
+        quantize_i8_any<T><<<grid, kBlock, 0, s>>>(static_cast<const S*>(second.x), second.codes, second.scales, rows,
+                                                   width, dest);
     return check_launch("xs_hip_quantize_kv");
 }
 
@@ -269,13 +315,13 @@ int check_kv_format(xs_kv_format format, const char* op) {
 }
 
 int quantize_i8(void* stream, xs_dtype x_dtype, const void* x, void* codes, void* scales, int64_t rows, int64_t width,
-                const QuantDest& dest, const char* what) {
+                const QuantDest& dest, const char* what, const QuantSecond& second = QuantSecond{}) {
     auto* c = static_cast<int8_t*>(codes);
     auto* sc = static_cast<float*>(scales);
     switch (x_dtype) {
-        case XS_F32: return launch_quantize<F32>(as_stream(stream), x, c, sc, rows, width, dest);
-        case XS_F16: return launch_quantize<F16>(as_stream(stream), x, c, sc, rows, width, dest);
-        case XS_BF16: return launch_quantize<BF16>(as_stream(stream), x, c, sc, rows, width, dest);
+        case XS_F32: return launch_quantize<F32>(as_stream(stream), x, c, sc, rows, width, dest, second);
+        case XS_F16: return launch_quantize<F16>(as_stream(stream), x, c, sc, rows, width, dest, second);
+        case XS_BF16: return launch_quantize<BF16>(as_stream(stream), x, c, sc, rows, width, dest, second);
         default:
             return fail(XS_HIP_EINVAL, std::string(what) + ": x must be f32, f16 or bf16, got " + dtype_name(x_dtype));
     }
@@ -303,6 +349,26 @@ int xs_hip_quantize_kv(void* stream, xs_kv_format format, xs_dtype x_dtype, cons
     if (reinterpret_cast<uintptr_t>(scales) % 4 != 0)
         return fail(XS_HIP_EINVAL, "xs_hip_quantize_kv: scales must be 4-byte aligned f32");
     return quantize_i8(stream, x_dtype, x, codes, scales, rows, width, QuantDest{}, "xs_hip_quantize_kv");
+}
+
+int xs_hip_quantize_kv_pair(void* stream, xs_dtype x_dtype, const void* k, const void* v, void* k_codes, void* k_scales,
+                            void* v_codes, void* v_scales, int64_t rows, int64_t width, const int64_t* row0,
+                            int64_t rows_per_unit, int64_t capacity_rows) {
+    const char* what = "xs_hip_quantize_kv_pair";
+    if (rows < 0 || width <= 0 || (row0 != nullptr && (rows_per_unit < 0 || capacity_rows < 0)))
+        return fail(XS_HIP_EINVAL, std::string(what) + ": rows " + std::to_string(rows) + " of width " +
+                                       std::to_string(width) + ", " + std::to_string(rows_per_unit) +
+                                       " rows a unit, capacity " + std::to_string(capacity_rows));
+    if (rows == 0) return XS_HIP_OK;
+    if (k == nullptr || v == nullptr || k_codes == nullptr || k_scales == nullptr || v_codes == nullptr ||
+        v_scales == nullptr)
+        return fail(XS_HIP_EINVAL, std::string(what) + ": null buffer");
+    if (reinterpret_cast<uintptr_t>(k_scales) % 4 != 0 || reinterpret_cast<uintptr_t>(v_scales) % 4 != 0 ||
+        reinterpret_cast<uintptr_t>(row0) % 8 != 0)
+        return fail(XS_HIP_EINVAL, std::string(what) + ": scales must be 4-byte and row0 8-byte aligned");
+    const QuantDest dest = row0 != nullptr ? QuantDest{row0, rows_per_unit, capacity_rows} : QuantDest{};
+    return quantize_i8(stream, x_dtype, k, k_codes, k_scales, rows, width, dest, what,
+                       QuantSecond{v, static_cast<int8_t*>(v_codes), static_cast<float*>(v_scales), 0});
 }
 
 int xs_hip_quantize_kv_at(void* stream, xs_dtype x_dtype, const void* x, void* codes, void* scales, int64_t rows,

@@ -1236,6 +1236,17 @@ void Program::launch(size_t i, const RunPlan& p, int64_t T, int64_t L, int64_t r
             const int slot = slot_of_[static_cast<size_t>(std::get<graph::KvCacheAttrs>(nd.attrs).slot)];
             KvState& kv = s_.kv()[static_cast<size_t>(slot)];
             const int64_t first = L - T;  // rows [L - T, L) of the slot
+            const Value k = np.reads[0], v = np.reads[1];
+            if (dtype(k) == dtype(v)) {  // keys and values in one launch
+                const bool at = replay_cap > 0;  // the first token read from the step record at replay
+                const int64_t skip = at ? 0 : first * kv.heads;
+                check(xs_hip_quantize_kv_pair(st, abi(dtype(k)), ptr(p, k), ptr(p, v), kv.kc.get() + skip * kv.dim,
+                                              kv.ks.get() + skip * 4, kv.vc.get() + skip * kv.dim,
+                                              kv.vs.get() + skip * 4, T * kv.heads, kv.dim,
+                                              at ? s_.step_record() : nullptr, kv.heads, kv.cap * kv.heads),
+                      "KvCache");
+                return;
+            }
             for (int which = 0; which < 2; ++which) {
                 const Value x = np.reads[static_cast<size_t>(which)];
                 char* codes = (which == 0 ? kv.kc : kv.vc).get();
