@@ -12,7 +12,11 @@
 //  - run: resolves T from the inputs (and L from the slots), plans the step's activations into one device arena by
 //    liveness (cached per T and `only` set), uploads the inputs, launches the steps in graph order on the session's
 //    stream, and copies the requested outputs back as f32 (integer outputs in their dtype). Slots advance only after
-//    every launch went in, so a refused step leaves the state as it was.
+//    every launch went in, so a refused step leaves the state as it was. Host copies go through page-locked staging,
+//    asynchronously, and the step waits once. A step that repeats (same plan, same power-of-two bucket of L) is
+//    captured into a HIP graph and replayed (the "graphs" backend option, on by default): where the KV append writes
+//    and how many keys the attention reads come from a device-resident step record, so one capture serves every L of
+//    its bucket (Program::launch_all).
 //
 // Fusions (static, per program), each one launch for what the graph spells as several nodes; a node is folded into
 // its consumer only when that consumer is its sole reader and it is not a graph output:
@@ -25,7 +29,8 @@
 //  - LayerNorm(Add(x, c)), c a row vector: the norm with a shift (sycl_backend.cpp:1100-1118);
 //  - RmsNorm(Add(x, r) [, w]): one pass that writes the sum (the updated residual stream, still read by later nodes)
 //    and the norm (no reference counterpart: the reference launches the add and the norm);
-//  - two Ropes of the same positions and frequencies (a step's Q and K): one launch (no reference counterpart).
+//  - two Ropes of the same positions and frequencies (a step's Q and K): one launch (no reference counterpart);
+//  - a KvCache's keys and values, of one dtype: one quantize launch (no reference counterpart).
 // Reshape is a view; Slice is a view when it keeps whole leading rows or only an act-bias-mul reads it, else a copy.
 //
 // What it refuses: MatMul and the other ops with no kernel here (the GEMM path is outside this library), float KV
