@@ -176,24 +176,24 @@ constexpr int64_t kChunk = kBlock * kChunkVpt * 4;  // keys per chunk: 1024
 constexpr int64_t kMaxRows = 65535;
 constexpr int kMaxChunks = 64;                      // the second launch combines a row's partials in one wave
 
-// Max over the block; every thread gets it.
+// Max over the block; every thread gets it. `lds` is written once per launch (each reduction has its own array), so
+// no barrier follows the reads.
 __device__ __forceinline__ float block_max(float v, float* lds) {
     v = group_reduce<64, OpMax>(v);
     if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
     __syncthreads();
     float m = lds[0];
     for (int i = 1; i < kBlock / 64; ++i) m = fmaxf(m, lds[i]);
-    __syncthreads();
     return m;
 }
 
+// Sum over the block, as block_max.
 __device__ __forceinline__ double block_sum(double v, double* lds) {
     v = group_sum_f64<64>(v);
     if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
     __syncthreads();
     double s = 0.0;
     for (int i = 0; i < kBlock / 64; ++i) s += lds[i];
-    __syncthreads();
     return s;
 }
 
