@@ -68,7 +68,7 @@ __device__ __forceinline__ void wave_best(float& v, int32_t& i) {
     }
 }
 
-// Best over the block (kBlock threads); every thread gets it.
+// Best over the block (kBlock threads); every thread gets it. Once per launch: no barrier follows the reads.
 __device__ __forceinline__ void block_best(float& v, int32_t& i) {
     __shared__ float sv[kBlock / 64];
     __shared__ int32_t si[kBlock / 64];
@@ -85,7 +85,6 @@ __device__ __forceinline__ void block_best(float& v, int32_t& i) {
             v = sv[w];
             i = si[w];
         }
-    __syncthreads();
 }
 
 // grid (chunks, rows). A row of one chunk writes its result; otherwise partials [rows][chunks] (packed value, index).
@@ -137,7 +136,8 @@ __global__ __launch_bounds__(kBlock) void argmax_chunks(const float* __restrict_
     }
 }
 
-// grid (rows): the best of a row's partials.
+// grid (rows): the best of a row's partials (a partial a thread: one round of loads; a single wave looping over
+// them measured 0.3 us slower).
 __global__ __launch_bounds__(kBlock) void argmax_final(const float* __restrict__ x, float* __restrict__ values,
                                                        int32_t* __restrict__ indices, int64_t width, int chunks,
                                                        const uint64_t* __restrict__ partials) {
