@@ -41,14 +41,15 @@ struct NormArgs {
 // Threads of a workgroup of LPR lanes a row: kBlock when LPR divides it (several rows a workgroup), else one row.
 constexpr int norm_block(int lpr) { return lpr < kBlock && kBlock % lpr == 0 ? kBlock : lpr; }
 
-// Sum over the LPR lanes of a row (f64): shuffles inside a wave, one LDS stage across the row's waves.
-template <int LPR, int BLOCK>
+// Sum over the LPR lanes of a row (f64): shuffles inside a wave, one LDS stage across the row's waves. REUSE: `partial`
+// held an earlier sum of this launch, whose reads must finish first.
+template <int LPR, int BLOCK, bool REUSE = false>
 __device__ __forceinline__ double row_sum(double v, double* partial) {
     constexpr int WAVES_PER_ROW = LPR > 64 ? LPR / 64 : 1;
     v = group_sum_f64<(LPR < 64 ? LPR : 64)>(v);
     if constexpr (WAVES_PER_ROW > 1) {
         const int wave = threadIdx.x >> 6;
-        __syncthreads();  // a previous use of `partial` is finished
+        if constexpr (REUSE) __syncthreads();
         if ((threadIdx.x & 63) == 0) partial[wave] = v;
         __syncthreads();
         const int first = (wave / WAVES_PER_ROW) * WAVES_PER_ROW;
@@ -132,7 +133,7 @@ __global__ __launch_bounds__(norm_block(LPR)) void row_norm_vec(NormArgs p) {
                 }
             }
         }
-        dev = row_sum<LPR, BLOCK>(dev, partial);
+        dev = row_sum<LPR, BLOCK, true>(dev, partial);
         scale = 1.0 / sqrt(dev / width + static_cast<double>(p.eps));
     } else if constexpr (MODE == kL2Clip) {
         const double f = static_cast<double>(p.threshold) / (sqrt(sum) + static_cast<double>(p.eps));
@@ -215,7 +216,7 @@ __global__ __launch_bounds__(kBlock) void row_norm_any(NormArgs p) {
             const double d = static_cast<double>(value(i)) - mean;
             dev += d * d;
         }
-        dev = row_sum<kBlock, kBlock>(dev, partial);
+        dev = row_sum<kBlock, kBlock, true>(dev, partial);
         scale = 1.0 / sqrt(dev / width + static_cast<double>(p.eps));
     } else if constexpr (MODE == kL2Clip) {
         const double f = static_cast<double>(p.threshold) / (sqrt(sum) + static_cast<double>(p.eps));
