@@ -585,7 +585,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": f"--gpus {args.gpus}: this path is built and measured on one GPU; the kernels "
-                                   "shard by rows with no exchange (see DESIGN.md), and no multi-GPU figure is "
+                                   "shard by rows with no exchange, and no multi-GPU figure is "
                                    "produced"}))
         sys.exit(2)
     only = None if args.only is None else set(args.only.split(","))

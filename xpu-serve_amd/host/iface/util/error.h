@@ -2,7 +2,7 @@
 
 // The interface surface the HIP backend is written against, restated from the reference (src/util/error.h:10-35):
 // one exception type, a variadic message builder, and the check macro. In the reference tree the backend includes
-// the reference's own header of this name instead (INTEGRATION.md).
+// the reference's own header of this name instead.
 
 #include <sstream>
 #include <stdexcept>
