@@ -16,9 +16,14 @@
 namespace xs_hip {
 namespace {
 
-__global__ __launch_bounds__(kBlock) void reduce_rows(const float* x, float* y, int64_t rows, int64_t dim, bool vec) {
+// Threads of a row-sum workgroup: one wave, one row (512 rows of 2560: 3.82 us against 3.93 with four rows a
+// workgroup).
+constexpr int kRowsBlock = 64;
+
+__global__ __launch_bounds__(kRowsBlock) void reduce_rows(const float* x, float* y, int64_t rows, int64_t dim,
+                                                          bool vec) {
     const int lane = threadIdx.x & 63;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kRowsBlock / 64) + (threadIdx.x >> 6);
     if (row >= rows) return;  // whole waves leave together; no workgroup barrier follows
     const float* xr = x + row * dim;
     double sum = 0.0;
@@ -104,8 +109,8 @@ int xs_hip_reduce_sum(void* stream, const float* x, float* y, int64_t outer, int
     const hipStream_t s = as_stream(stream);
     if (inner == 1) {
         const bool vec = dim % 4 == 0 && aligned16(x);
-        const int64_t blocks = (outer + kBlock / 64 - 1) / (kBlock / 64);
-        reduce_rows<<<static_cast<unsigned>(blocks), kBlock, 0, s>>>(x, y, outer, dim, vec);
+        const int64_t blocks = (outer + kRowsBlock / 64 - 1) / (kRowsBlock / 64);
+        reduce_rows<<<static_cast<unsigned>(blocks), kRowsBlock, 0, s>>>(x, y, outer, dim, vec);
     } else {
         // Few column tiles get sixteen waves each (more of `dim` in flight) and, below one tile a CU, tiles of one
         // 128-byte line; many get four waves over 64 columns.
