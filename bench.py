@@ -279,10 +279,32 @@ def op_softmax():
         x, y = s
         X.call("xs_hip_softmax_masked", stream, vp(x), vp(y), heads, keys, keys, C.c_float(scale), None, valid,
                C.c_void_p(sp))
-    return Op("softmax_masked", W.ALGO_BYTES["softmax_masked"], 2 * heads * keys * 4, mk, go, 2, "softmax_partials")
+    return Op("softmax_masked", W.ALGO_BYTES["softmax_masked"], 2 * heads * keys * 4, mk, go, 1, "softmax_split")
 
 
 def op_argmax():
+    """Config 2b through xs_hip_argmax: one launch, its zero-filled scratch shared by the calls (one stream, in
+    order; each call leaves it zero-filled)."""
+    c = W.config2b()
+    width = c.arrays["logits"].shape[1]
+    x0 = X.DeviceTensor.from_numpy(c.arrays["logits"])
+    scratch = X.Scratch()
+    sp = scratch.ptr(X.lib().xs_hip_argmax_scratch(1, width))
+
+    def mk():
+        s = (dcopy(x0), X.DeviceTensor.empty(X.F32, (1,)), X.DeviceTensor.empty(X.I32, (1,)))
+        need(s[0], width * 4, "argmax")
+        return s
+
+    def go(s, stream):
+        x, v, i = s
+        X.call("xs_hip_argmax", stream, vp(x), vp(v), vp(i), 1, width, C.c_void_p(sp))
+    return Op("argmax", W.ALGO_BYTES["argmax"], width * 4, mk, go, 1, "argmax_split")
+
+
+def op_argmax_topk():
+    """Config 2b through xs_hip_topk with k = 1 (the reference's call, sycl_be::topk): two launches through a
+    scratch of any contents."""
     c = W.config2b()
     width = c.arrays["logits"].shape[1]
     x0 = X.DeviceTensor.from_numpy(c.arrays["logits"])
@@ -297,7 +319,7 @@ def op_argmax():
     def go(s, stream):
         x, v, i, sc = s
         X.call("xs_hip_topk", stream, vp(x), vp(v), vp(i), 1, width, 1, C.c_void_p(sc.ptr))
-    return Op("argmax", W.ALGO_BYTES["argmax"], width * 4, mk, go, 2, "argmax_chunks")
+    return Op("argmax_topk_k1", W.ALGO_BYTES["argmax"], width * 4, mk, go, 2, "argmax_chunks")
 
 
 # Top-k shapes of the reference's callers (models/common/blocks.cpp:29-52, models/drafters/dflash.cpp:362): a
@@ -484,7 +506,7 @@ def op_copy(n=256 << 20, name="copy"):
 
 
 OP_ORDER = ["swiglu_bias", "swiglu_bias_strided", "rmsnorm_residual", "rmsnorm_residual_separate", "softmax_masked",
-            "argmax", "rope_qk", "rope_qk_separate", "kv_quantize", "kv_dequantize", "attention_i8_decode", "layer_norm", "l2_clip",
+            "argmax", "argmax_topk_k1", "rope_qk", "rope_qk_separate", "kv_quantize", "kv_dequantize", "attention_i8_decode", "layer_norm", "l2_clip",
             "reduce_sum_rows", "reduce_sum_cols", "unary_softcap", "kv_turbo4_quantize", "kv_turbo4_dequantize",
             "topk_shortlist", "topk_moe_router", "topk_draft_candidates"]
 
@@ -502,7 +524,8 @@ def build_ops(only):
             kv = _kv_inputs()
         yield {"swiglu_bias": op_swiglu, "swiglu_bias_strided": op_swiglu_strided, "rmsnorm_residual": op_rmsnorm,
                "rmsnorm_residual_separate": op_rmsnorm_separate,
-               "softmax_masked": op_softmax, "argmax": op_argmax, "rope_qk": op_rope,
+               "softmax_masked": op_softmax, "argmax": op_argmax,
+               "argmax_topk_k1": op_argmax_topk, "rope_qk": op_rope,
                "rope_qk_separate": lambda: op_rope(True), "copy": op_copy,
                "kv_quantize": lambda: op_kv_quantize(kv), "kv_dequantize": lambda: op_kv_dequantize(kv),
                "attention_i8_decode": lambda: op_attention_i8(kv), "unary_softcap": op_unary_softcap,

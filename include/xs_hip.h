@@ -205,14 +205,19 @@ int xs_hip_softmax(void* stream, const float* x, float* y, int64_t rows, int64_t
 /* The masked attention-score form: per row r, s = fl32(x * scale) for keys c < valid_len[r] (or `valid_len_all` when
  * valid_len is NULL) and -inf beyond, then softmax; masked keys come out exactly 0. x/y rows `row_stride` apart.
  * Equals cpu-ref's Scale (ops.cpp:209-211), Add of a 0/-inf mask, Softmax (ops.cpp:644-661).
- * With `scratch` (xs_hip_softmax_scratch bytes, 16-byte aligned, any contents), a few wide rows are split over several
- * workgroups in two launches that pass each chunk's (max, sum) through it; with NULL each row is one workgroup.
- * Concurrent calls must not share one scratch. */
+ * With `scratch` (xs_hip_softmax_scratch bytes, 16-byte aligned), a few wide rows are split over several workgroups of
+ * one launch that pass each chunk's (max, sum) through it; with NULL each row is one workgroup. The scratch must be
+ * zero-filled before its first use; every call leaves it ready for the next, so one buffer (of the largest size
+ * asked for) serves any sequence of calls of any shapes on one stream. Concurrent calls must not share one scratch. */
 int xs_hip_softmax_masked(void* stream, const float* x, float* y, int64_t rows, int64_t width, int64_t row_stride,
                           float scale, const int64_t* valid_len, int64_t valid_len_all, void* scratch);
 /* Bytes of scratch xs_hip_softmax_masked can use for rows of `width` (0: it would not split them). No reference
  * counterpart (cpu-ref's softmax needs none). */
 size_t xs_hip_softmax_scratch(int64_t rows, int64_t width);
+/* Polls a workgroup of a split launch (xs_hip_softmax_masked) makes for its row's other chunks before it computes the
+ * row's partials alone (same result, slower); 0 takes that path at once. A testing hook with no reference
+ * counterpart: the fallback keeps every launch finite when the chip cannot hold a split launch's workgroups at once. */
+void xs_hip_set_spin_limit(int polls);
 /* Bytes of scratch xs_hip_topk needs (0: none, NULL allowed). Replaces sycl_be::topk_scratch (sycl_kernels.h:61). */
 size_t xs_hip_topk_scratch(int64_t rows, int64_t width, int64_t k);
 /* The k largest per row of x [rows, width] f32: values f32 and indices i32 [rows, k], largest first, equal values keep
@@ -223,6 +228,17 @@ size_t xs_hip_topk_scratch(int64_t rows, int64_t width, int64_t k);
  * (sycl_kernels.h:62-63). */
 int xs_hip_topk(void* stream, const float* x, float* values, int32_t* indices, int64_t rows, int64_t width, int64_t k,
                 void* scratch);
+/* Bytes of zero-filled scratch xs_hip_argmax needs (0: none, NULL allowed). No reference counterpart. */
+size_t xs_hip_argmax_scratch(int64_t rows, int64_t width);
+/* Argmax per row of x [rows, width] f32 in one launch: values f32 [rows] the row's maximum, indices i32 [rows] its
+ * lowest index among exact ties; NaN is never picked, and a row of nothing but NaN reports index 0 and x[0] -- the
+ * results of xs_hip_topk with k = 1 (cpu_ref::topk, ops.cpp:663-684; blocks::argmax_rows, blocks.cpp:36-38). An
+ * extension of this device: the reference's argmax is sycl_be::topk with k = 1 (sycl_kernels.h:62-63), two launches
+ * through its scratch. `scratch` (xs_hip_argmax_scratch bytes, 8-byte aligned) must be zero-filled before its first
+ * use; every call leaves it zero-filled again, so one buffer (of the largest size asked for) serves any sequence of
+ * calls of any shapes on one stream. Concurrent calls must not share one scratch. */
+int xs_hip_argmax(void* stream, const float* x, float* values, int32_t* indices, int64_t rows, int64_t width,
+                  void* scratch);
 
 /* ---- RoPE ---------------------------------------------------------------------------------------------------- */
 

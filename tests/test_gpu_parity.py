@@ -447,6 +447,54 @@ def test_softmax_split_edges(ora):
     assert_f32_close(one, got, what="split vs unsplit")
 
 
+def _scratch_bytes(scratch, n):
+    buf = np.empty(n, np.uint8)
+    X.call("xs_hip_memcpy_d2h", C.c_void_p(buf.ctypes.data), C.c_void_p(scratch.buf.ptr), C.c_size_t(n), None)
+    return buf
+
+
+SPLIT_ROW_WORDS = 264  # 64-bit words of the split softmax's scratch a row owns: ticket counter, then two banks
+
+
+def _tickets_idle(scratch, rows):
+    """After a call every row's ticket count is back to 0 (the generation has moved on)."""
+    words = _scratch_bytes(scratch, rows * SPLIT_ROW_WORDS * 8).view(np.uint64).reshape(rows, SPLIT_ROW_WORDS)
+    return not (words[:, 0] & np.uint64(0xFFFFFFFF)).any()
+
+
+def test_softmax_split_one_launch_scratch(ora):
+    """One zero-filled scratch serves single-launch split calls of different shapes in a row (each row's words sit at
+    a fixed place; the banks alternate by generation), every row's ticket count returns to 0 after each call; and the
+    bounded wait's fallback (every workgroup computing its row's partials alone, forced here with a spin limit of 0)
+    gives the same bits as the published partials."""
+    rng = np.random.default_rng(23)
+    scratch = X.Scratch()
+    shapes = [(32, 32768, 30000), (4, 20000, 12289), (1, 8192, 8192), (63, 8192, 8000), (2, 262144, 200000), (3, 600000, 555555)]
+    need = max(X.lib().xs_hip_softmax_scratch(r, w) for r, w, _ in shapes)
+    scratch.ptr(need)
+    outs = {}
+    for rows, width, valid in shapes:
+        assert X.lib().xs_hip_softmax_scratch(rows, width) > 0, (rows, width)
+        x = (rng.standard_normal((rows, width)) * 3).astype(np.float32)
+        step(f"softmax split one launch [{rows}, {width}] valid {valid}")
+        got = X.softmax_masked(dev(x), 0.0883883461356163, valid, scratch).numpy()
+        assert_f32_close(got, ora.softmax_masked(x, 0.0883883461356163, valid), what=f"split {rows}x{width}")
+        assert _tickets_idle(scratch, rows), "ticket count not back to 0"
+        outs[(rows, width)] = (x, valid, got)
+    try:
+        X.lib().xs_hip_set_spin_limit(0)
+        for (rows, width), (x, valid, got) in outs.items():
+            step(f"softmax split fallback (no wait) [{rows}, {width}]")
+            alone = X.softmax_masked(dev(x), 0.0883883461356163, valid, scratch).numpy()
+            assert_exact(alone, got, f"fallback {rows}x{width}")
+            assert _tickets_idle(scratch, rows), "ticket count not back to 0 (fallback)"
+    finally:
+        X.lib().xs_hip_set_spin_limit(1 << 14)
+    for (rows, width), (x, valid, got) in list(outs.items())[:2]:
+        step(f"softmax split after the fallback calls [{rows}, {width}]")
+        assert_exact(X.softmax_masked(dev(x), 0.0883883461356163, valid, scratch).numpy(), got, "again")
+
+
 def test_softmax_config2a_full(ora):
     cfg = W.config2a()
     s = cfg.arrays["scores"]
@@ -482,7 +530,7 @@ def test_argmax_config2b_full(ora):
     cfg = W.config2b()
     x = cfg.arrays["logits"]
     scratch = X.TopkScratch()
-    for rep in range(3):  # the self-resetting arrival counters across calls
+    for rep in range(3):
         step(f"argmax config 2b [1, 151936] call {rep}")
         v, i = X.topk(dev(x), 1, scratch)
         assert int(i.numpy()[0, 0]) == cfg.params["ties"][0]
@@ -500,6 +548,61 @@ def test_argmax_rows(ora, rows, width):
     wv, wi = ora.topk(x, 1)
     assert_exact(i.numpy(), wi)
     assert_exact(v.numpy(), wv)
+
+
+def test_argmax_one_launch_config2b(ora):
+    """xs_hip_argmax (the one-launch form the bench times) on config 2b's row: the lowest of the four planted ties,
+    bit-exact with the oracle and with xs_hip_topk(k = 1); three calls in a row on one scratch, which each call
+    returns to zero."""
+    cfg = W.config2b()
+    x = cfg.arrays["logits"]
+    scratch = X.Scratch()
+    n = X.lib().xs_hip_argmax_scratch(1, x.shape[1])
+    assert n > 0
+    wv, wi = ora.topk(x, 1)
+    for rep in range(3):
+        step(f"argmax one launch config 2b call {rep}")
+        v, i = X.argmax(dev(x), scratch)
+        assert int(i.numpy()[0]) == cfg.params["ties"][0]
+        assert_exact(i.numpy(), wi[:, 0])
+        assert_exact(v.numpy(), wv[:, 0])
+        assert not _scratch_bytes(scratch, n).any(), "scratch not returned to zero"
+
+
+@pytest.mark.parametrize("rows,width,offset", [(64, 151936, 0), (16, 151936, 0), (3, 1025, 0), (7, 4096, 1),
+                                               (2, 1023, 0), (5, 3, 0), (1, 2_000_001, 3), (300, 9000, 0)])
+def test_argmax_one_launch_rows(ora, rows, width, offset):
+    """Many exact ties, NaN entries, a row of nothing but NaN, -0 beside +0, unaligned rows (offset elements) and
+    widths off the vector: xs_hip_argmax against the oracle's topk(k = 1), bit for bit."""
+    rng = np.random.default_rng(rows * 11 + width)
+    x = rng.integers(-50, 50, (rows, width)).astype(np.float32)
+    x[0, rng.integers(0, width, 4)] = np.nan
+    if rows > 1:
+        x[1, :] = np.nan
+    if rows > 2:
+        x[2, :] = -0.0
+        x[2, width // 2] = 0.0
+    buf = np.zeros(rows * width + offset, np.float32)
+    buf[offset:] = x.ravel()
+    d = dev(buf)
+    view = X.DeviceTensor(d.buf, X.F32, (rows, width), 4 * offset)
+    step(f"argmax one launch [{rows}, {width}] offset {offset}")
+    scratch = X.Scratch()
+    v, i = X.argmax(view, scratch)
+    wv, wi = topk_skipping_nan(x, 1)  # the kernels' NaN rule (cpu-ref's order where a row holds no NaN)
+    assert_exact(i.numpy(), wi[:, 0])
+    assert_exact(v.numpy().view(np.uint32), wv[:, 0].view(np.uint32))
+    clean = ~np.isnan(x).any(axis=1)
+    ov, oi = ora.topk(x[clean], 1)
+    assert_exact(i.numpy()[clean], oi[:, 0])
+    tv, ti = X.topk(view, 1)
+    assert_exact(i.numpy(), ti.numpy()[:, 0])
+    n = X.lib().xs_hip_argmax_scratch(rows, width)
+    if n:
+        assert not _scratch_bytes(scratch, n).any(), "scratch not returned to zero"
+        step(f"argmax one launch [{rows}, {width}] again on the same scratch")
+        v2, i2 = X.argmax(view, scratch)
+        assert_exact(i2.numpy(), i.numpy())
 
 
 def test_topk_k_gt_1(ora):
@@ -662,6 +765,26 @@ def test_rope_config3_full(ora):
             n0 = xf[..., :64] ** 2 + xf[..., 64:] ** 2
             n1 = yf[..., :64] ** 2 + yf[..., 64:] ** 2
             assert np.allclose(n0, n1, rtol=5e-3, atol=1e-3)
+
+
+def test_rope_qk_config3_full(ora):
+    """The launch the bench times for config 3 (xs_hip_rope2: Q [8192, 32, 128] and K [8192, 8, 128] f16 in one
+    launch) against the oracle's cpu_ref::rope at full size, each within one f16 ulp, and in place."""
+    cfg = W.config3()
+    a = cfg.arrays
+    pos = dev(a["positions"])
+    f = dev(a["inv_freq"])
+    step("rope_qk config 3 q [8192, 32, 128] + k [8192, 8, 128] f16, one launch")
+    yq, yk = X.rope_qk(dev(a["q"], F16), dev(a["k"], F16), pos, f)
+    for name, y in (("q", yq.numpy()), ("k", yk.numpy())):
+        want = ora.rope(ora.widen(a[name], F16), a["positions"], a["inv_freq"])
+        n_diff = assert_ulp(y, ora.narrow(want, F16), "f16", what=f"rope_qk {name}")
+        assert n_diff <= y.size * 1e-4
+    step("rope_qk config 3 in place")
+    dq, dk = dev(a["q"], F16), dev(a["k"], F16)
+    X.rope_qk(dq, dk, pos, f, in_place=True)
+    assert_exact(dq.numpy().view(np.uint16), yq.numpy().view(np.uint16), "q in place")
+    assert_exact(dk.numpy().view(np.uint16), yk.numpy().view(np.uint16), "k in place")
 
 
 @pytest.mark.parametrize("xdt", [F32, F16])

@@ -211,6 +211,54 @@ __device__ __forceinline__ double group_sum_f64(double v) {
     return v;
 }
 
+// Reductions over the whole wave64 with DPP alone (no LDS-routed shuffle): the four steps within 16-lane rows, then
+// row_bcast:15 (row r takes lane 16 r - 1, rows 1 and 3) and row_bcast:31 (rows 2 and 3 take lane 31), after which
+// lane 63 holds the wave's result; v_readlane makes it wave-uniform. Lanes a masked DPP step does not write keep the
+// operation's identity, so the combination order is fixed and every wave produces the same bits for the same inputs.
+namespace dpp {
+constexpr int kRowBcast15 = 0x142;
+constexpr int kRowBcast31 = 0x143;
+}  // namespace dpp
+
+template <int Ctrl, int RowMask>
+__device__ __forceinline__ int dpp_masked_i(int v, int identity) {
+    return __builtin_amdgcn_update_dpp(identity, v, Ctrl, RowMask, 0xF, false);
+}
+
+template <typename Op>
+__device__ __forceinline__ float wave_reduce(float v, float identity) {
+    v = Op::apply(v, dpp_f<dpp::kQuadXor1>(v));
+    v = Op::apply(v, dpp_f<dpp::kQuadXor2>(v));
+    v = Op::apply(v, dpp_f<dpp::kRowHalfMirror>(v));
+    v = Op::apply(v, dpp_f<dpp::kRowMirror>(v));
+    const int id = __float_as_int(identity);
+    v = Op::apply(v, __int_as_float(dpp_masked_i<dpp::kRowBcast15, 0xA>(__float_as_int(v), id)));
+    v = Op::apply(v, __int_as_float(dpp_masked_i<dpp::kRowBcast31, 0xC>(__float_as_int(v), id)));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+template <int Ctrl, int RowMask>
+__device__ __forceinline__ double dpp_masked_d(double v) {  // identity 0.0
+    const uint64_t u = __double_as_longlong(v);
+    const uint32_t lo = static_cast<uint32_t>(dpp_masked_i<Ctrl, RowMask>(static_cast<int>(u), 0));
+    const uint32_t hi = static_cast<uint32_t>(dpp_masked_i<Ctrl, RowMask>(static_cast<int>(u >> 32), 0));
+    return __longlong_as_double(static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo));
+}
+
+// f64 sum over the wave, as wave_reduce.
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    v += dpp_d<dpp::kQuadXor1>(v);
+    v += dpp_d<dpp::kQuadXor2>(v);
+    v += dpp_d<dpp::kRowHalfMirror>(v);
+    v += dpp_d<dpp::kRowMirror>(v);
+    v += dpp_masked_d<dpp::kRowBcast15, 0xA>(v);
+    v += dpp_masked_d<dpp::kRowBcast31, 0xC>(v);
+    const uint64_t u = __double_as_longlong(v);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u), 63));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u >> 32), 63));
+    return __longlong_as_double(static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo));
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // Index arithmetic.
 

@@ -13,11 +13,10 @@
 // exponentiated.
 //
 // Few wide rows (the decode step's [heads, 1, keys] scores) would leave most of the chip idle with one workgroup per
-// row, so with caller scratch a row is split over `chunks` workgroups of kChunk keys, in two launches that need no
-// atomics or cross-workgroup waits: the first writes each chunk's (max m_j, sum s_j of exp(x - m_j)) to scratch; the
-// second reads the row's partials (one lane per chunk: M = max m_j, S = sum s_j exp(m_j - M) in f64), reads its chunk
-// again -- from the L2 of the same XCD, since both launches map a chunk to the same workgroup id -- and writes
-// exp(x - M) / S.
+// row, so with caller scratch a row is split over `chunks` workgroups in ONE launch: each reduces its chunk to
+// (max m_j, f64 sum s_j of exp(x - m_j)), publishes it through the scratch with device-scope atomics, waits for the
+// row's other chunks (a bounded wait, with a local fallback), combines the row's partials and writes its chunk's
+// outputs from the values it still holds in registers -- the scores are read from HBM once and written once.
 #include <cmath>
 
 #include "common.h"
@@ -171,52 +170,30 @@ __global__ __launch_bounds__(kBlock) void softmax_any(SoftmaxArgs p) {
     }
 }
 
-constexpr int kChunkVpt = 1;                      // 128-bit vectors per lane in a chunk
-constexpr int64_t kChunk = kBlock * kChunkVpt * 4;  // keys per chunk: 1024
-constexpr int64_t kMaxRows = 65535;
-constexpr int kMaxChunks = 64;                      // the second launch combines a row's partials in one wave
-
-// Max over the block; every thread gets it. `lds` is written once per launch (each reduction has its own array), so
-// no barrier follows the reads.
-__device__ __forceinline__ float block_max(float v, float* lds) {
-    v = group_reduce<64, OpMax>(v);
-    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float m = lds[0];
-    for (int i = 1; i < kBlock / 64; ++i) m = fmaxf(m, lds[i]);
-    return m;
-}
-
-// Sum over the block, as block_max.
-__device__ __forceinline__ double block_sum(double v, double* lds) {
-    v = group_sum_f64<64>(v);
-    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
-    __syncthreads();
-    double s = 0.0;
-    for (int i = 0; i < kBlock / 64; ++i) s += lds[i];
-    return s;
-}
-
+constexpr int kMaxChunks = 64;       // one wave combines a row's partials, a chunk a lane
 __device__ __forceinline__ int64_t row_valid(const SoftmaxArgs& p, int64_t row) {
     const int64_t v = p.valid_len != nullptr ? p.valid_len[row] : p.valid_all;
     return v < 0 ? 0 : (v > p.width ? p.width : v);
 }
 
-// Loads the chunk's valid keys scaled (-inf for masked ones) and returns how many of its vectors are in range.
+// The scaled keys of one chunk (VPT 128-bit vectors a lane, lane t holding vectors t + k * BLOCK of the chunk), -inf
+// for masked ones and past the row. Plain loads: at a few KiB a workgroup the load latency is the cost, and the
+// non-temporal form measured slower there.
+template <int BLOCK, int VPT>
 __device__ __forceinline__ void load_chunk(const SoftmaxArgs& p, int64_t row, int chunk, int64_t valid,
-                                           float (&s)[kChunkVpt][4]) {
+                                           float (&s)[VPT][4]) {
     const float* xr = p.x + row * p.row_stride;
-    const int64_t v0 = chunk * (kChunk / 4);
+    const int64_t v0 = static_cast<int64_t>(chunk) * (BLOCK * VPT);
     const int64_t nvec = p.width / 4;
-    u32x4 raw[kChunkVpt];
+    u32x4 raw[VPT];
 #pragma unroll
-    for (int k = 0; k < kChunkVpt; ++k) {
-        const int64_t v = v0 + threadIdx.x + k * kBlock;
+    for (int k = 0; k < VPT; ++k) {
+        const int64_t v = v0 + threadIdx.x + k * BLOCK;
         if (v < nvec && v * 4 < valid) raw[k] = ld128(xr + v * 4);
     }
 #pragma unroll
-    for (int k = 0; k < kChunkVpt; ++k) {
-        const int64_t v = v0 + threadIdx.x + k * kBlock;
+    for (int k = 0; k < VPT; ++k) {
+        const int64_t v = v0 + threadIdx.x + k * BLOCK;
         if (v < nvec && v * 4 < valid) {
             unpack<F32>(raw[k], s[k]);
 #pragma unroll
@@ -228,95 +205,250 @@ __device__ __forceinline__ void load_chunk(const SoftmaxArgs& p, int64_t row, in
     }
 }
 
-// Launch 1, grid (chunks, rows): partial[row][chunk] = (m_j as f32 bits, s_j as f64 bits).
-__global__ __launch_bounds__(kBlock) void softmax_partials(SoftmaxArgs p, int chunks, uint64_t* __restrict__ partial) {
-    __shared__ float lds_f[kBlock / 64];
-    __shared__ double lds_d[kBlock / 64];
-    const int64_t row = blockIdx.y;
-    const int chunk = blockIdx.x;
-    const int64_t valid = row_valid(p, row);
-    float s[kChunkVpt][4];
-    load_chunk(p, row, chunk, valid, s);
+// A workgroup barrier that orders LDS only. __syncthreads() also waits for every global access the workgroup has in
+// flight (its release fence covers global memory), which here would put the latency of an atomic still on its way to
+// memory in front of work that does not need it.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// exp(a - b) for a <= b as f64: in f32 with the subtraction's rounding error folded in while the result is a normal
+// f32 (a - b >= -80), else in f64.
+__device__ __forceinline__ double exp_gap(float a, float b) {
+    return a - b >= -80.0f ? static_cast<double>(exp_diff(a, b))
+                           : exp(static_cast<double>(a) - static_cast<double>(b));
+}
+
+// Partials of one chunk held in registers. Each wave takes its own maximum m_w and replaces its values by
+// exp(x - m_w), summed in f32 (s_w); one LDS stage hands the waves' (m_w, s_w) to wave 0, whose lane w holds wave w's
+// pair: m_j = max m_w and s_j = sum s_w exp(m_w - m_j) in f64, returned wave-uniform in wave 0 (the other waves'
+// m_j, s_j are unspecified). A wave whose keys are all masked or -inf has m_w = -inf, exponentials 0 and adds
+// nothing (its exponentials relative to its own -inf maximum would be NaN). Every reduction runs in a fixed order, so
+// the same chunk gives the same bits in any workgroup. The LDS arrays are read after the barrier: a caller that
+// reuses them puts a barrier before the next call.
+template <int BLOCK, int VPT>
+__device__ __forceinline__ void chunk_stats(float (&s)[VPT][4], float* lds_m, float* lds_s, float& m_w, float& m_j,
+                                            double& s_j) {
     float m = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < kChunkVpt; ++k)
+    for (int k = 0; k < VPT; ++k)
 #pragma unroll
         for (int i = 0; i < 4; ++i) m = fmaxf(m, s[k][i]);
-    m = block_max(m, lds_f);
-    // A chunk whose keys are all masked or -inf adds nothing against any finite M (and its exponentials relative to
-    // its own -inf maximum would be NaN), so its sum is 0.
-    double sum = 0.0;
-    if (m != -INFINITY) {
+    m_w = wave_reduce<OpMax>(m, -INFINITY);
+    float lane_sum = 0.0f;
 #pragma unroll
-        for (int k = 0; k < kChunkVpt; ++k)
+    for (int k = 0; k < VPT; ++k)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sum += static_cast<double>(exp_diff(s[k][i], m));
+        for (int i = 0; i < 4; ++i) {
+            s[k][i] = m_w != -INFINITY ? exp_diff(s[k][i], m_w) : 0.0f;
+            lane_sum += s[k][i];
+        }
+    const float s_w = wave_reduce<OpSum>(lane_sum, 0.0f);
+    constexpr int kWaves = BLOCK / 64;
+    if ((threadIdx.x & 63) == 0) {
+        lds_m[threadIdx.x >> 6] = m_w;
+        lds_s[threadIdx.x >> 6] = s_w;
     }
-    sum = block_sum(sum, lds_d);
-    if (threadIdx.x == 0) {
-        uint64_t* out = partial + (row * chunks + chunk) * 2;
-        out[0] = __float_as_uint(m);
-        out[1] = static_cast<uint64_t>(__double_as_longlong(sum));
+    lds_barrier();
+    if (threadIdx.x < 64) {
+        const int l = threadIdx.x;
+        const float mw = l < kWaves ? lds_m[l] : -INFINITY;
+        const float sw = l < kWaves ? lds_s[l] : 0.0f;
+        const float mx = group_reduce<kWaves, OpMax>(mw);
+        const double sx = group_sum_f64<kWaves>(mw != -INFINITY ? static_cast<double>(sw) * exp_gap(mw, mx) : 0.0);
+        m_j = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(mx)));
+        const uint64_t u = __double_as_longlong(sx);
+        s_j = __longlong_as_double(static_cast<int64_t>(
+            (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(u >> 32))))
+             << 32) |
+            static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(u)))));
     }
 }
 
-// Launch 2, grid (chunks, rows): combines the row's partials and writes the chunk's outputs.
-__global__ __launch_bounds__(kBlock) void softmax_finish(SoftmaxArgs p, int chunks,
-                                                         const uint64_t* __restrict__ partial) {
+// Wave 0, lane j holding chunk j's partial (m_l, s_l): the row's M = max m_j and 1 / S, S = sum s_j exp(m_j - M) in
+// f64, into LDS. M = -inf (every key masked or -inf) makes S NaN, as cpu-ref's exp(-inf - (-inf)) makes the row NaN.
+__device__ __forceinline__ void combine_row(float m_l, double s_l, int chunks, float* s_M, double* s_rS) {
+    const int lane = threadIdx.x;
+    const float M = wave_reduce<OpMax>(lane < chunks ? m_l : -INFINITY, -INFINITY);
+    const double t = lane >= chunks     ? 0.0
+                     : m_l != -INFINITY ? s_l * exp_gap(m_l, M)
+                                        : (M == -INFINITY ? NAN : 0.0);
+    const double S = wave_sum_f64(t);
+    if (lane == 0) {
+        *s_M = M;
+        *s_rS = 1.0 / S;
+    }
+}
+
+// Scratch of the split launch, all 64-bit words, zero-filled before its first use. Row r owns a fixed block of
+// kRowWords words whatever the call's shape (so calls of any shapes can follow each other on one scratch):
+//   word 0: the row's ticket counter, (generation << 32) | tickets taken this call;
+//   words 8 + 128 b ..: bank b of partial pairs, chunk j at 2 j: (m_j bits | 1 << 32, s_j bits ^ 1 << 63), never 0
+//   once written, so a zero word means "not yet published" and a reader needs no ordering between the two words.
+// A call uses bank (generation & 1); every workgroup of the row takes a ticket first, and the one that takes the
+// row's last ticket rolls the counter to the next generation and clears the other bank -- the previous call's, whose
+// readers are all done, since that call's kernel has ended -- so the next call finds its bank zero, and nothing is
+// left to do at the end of the kernel. Every access is a relaxed device-scope atomic, which this part keeps coherent
+// across the XCDs' L2s without cache write-back or invalidation.
+constexpr int kMaxSplitRows = 256;  // a split launch has fewer than 256 rows
+constexpr int64_t kBankWords = 2 * kMaxChunks;
+constexpr int64_t kRowWords = 8 + 2 * kBankWords;
+
+__device__ __forceinline__ uint64_t enc_max(float m) { return (uint64_t{1} << 32) | __float_as_uint(m); }
+__device__ __forceinline__ uint64_t enc_sum(double s) {
+    return static_cast<uint64_t>(__double_as_longlong(s)) ^ (uint64_t{1} << 63);
+}
+__device__ __forceinline__ float dec_max(uint64_t w) { return __uint_as_float(static_cast<uint32_t>(w)); }
+__device__ __forceinline__ double dec_sum(uint64_t w) {
+    return __longlong_as_double(static_cast<long long>(w ^ (uint64_t{1} << 63)));
+}
+__device__ __forceinline__ uint64_t ld_sync(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_sync(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One launch, grid (chunks, rows) of BLOCK threads, chunk = BLOCK * VPT * 4 keys. Each workgroup reduces its chunk
+// to (m_j, s_j), keeping the chunk's exp(x - m_j) in registers, publishes the pair, waits (at most `spin` polls) for
+// the row's other chunks, combines the row's partials -- M = max m_j, S = sum s_j exp(m_j - M) in f64, lane j holding
+// chunk j so every workgroup adds them in one order -- and writes its chunk's exp(x - m_j) * (exp(m_j - M) / S): the
+// scores are read once and exponentiated once. A workgroup whose wait runs out (its row's chunks not all resident:
+// another kernel holding the CUs, or the spin limit a test sets) computes every chunk's partial of its row itself with
+// the same reductions, so its result has the same bits, and still departs.
+template <int BLOCK, int VPT>
+__global__ __launch_bounds__(BLOCK) void softmax_split(SoftmaxArgs p, int chunks, uint64_t* __restrict__ sync,
+                                                       int spin) {
+    __shared__ float lds_m[BLOCK / 64];
+    __shared__ float lds_s[BLOCK / 64];
     __shared__ float s_M;
-    __shared__ double s_S;
+    __shared__ double s_rS;
+    __shared__ int s_ready;
     const int64_t row = blockIdx.y;
     const int chunk = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const bool wave0 = threadIdx.x < 64;
+    uint64_t* rb = sync + row * kRowWords;
     const int64_t valid = row_valid(p, row);
-    float s[kChunkVpt][4];
-    load_chunk(p, row, chunk, valid, s);
-    if (threadIdx.x < 64) {
-        const int j = threadIdx.x;
-        const uint64_t* pr = partial + row * chunks * 2;
-        const float mj = j < chunks ? __uint_as_float(static_cast<uint32_t>(pr[2 * j])) : -INFINITY;
-        const double sj = j < chunks ? __longlong_as_double(static_cast<long long>(pr[2 * j + 1])) : 0.0;
-        const float M = group_reduce<64, OpMax>(mj);
-        // M = -inf: every key masked or -inf; cpu-ref's exp(-inf - (-inf)) makes the row NaN.
-        const double t = mj != -INFINITY ? sj * exp(static_cast<double>(mj) - static_cast<double>(M))
-                                         : (M == -INFINITY && j < chunks ? static_cast<double>(NAN) : 0.0);
-        const double S = group_sum_f64<64>(t);
-        if (j == 0) {
-            s_M = M;
-            s_S = S;
+    // The ticket comes back while the chunk loads.
+    uint64_t ticket = 0;
+    if (threadIdx.x == 0)
+        ticket = __hip_atomic_fetch_add(rb, uint64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    float s[VPT][4];
+    load_chunk<BLOCK, VPT>(p, row, chunk, valid, s);
+    float mw, mj;
+    double sj;
+    chunk_stats<BLOCK, VPT>(s, lds_m, lds_s, mw, mj, sj);
+    uint64_t* slots = rb;
+    if (wave0) {
+        ticket = __shfl(ticket, 0, 64);
+        const uint64_t bank = (ticket >> 32) & 1;
+        slots = rb + 8 + bank * kBankWords;
+        if (lane == 0) {
+            __hip_atomic_store(slots + 2 * chunk, enc_max(mj), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(slots + 2 * chunk + 1, enc_sum(sj), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (static_cast<uint32_t>(ticket) == static_cast<uint32_t>(chunks - 1)) {
+            // The row's last ticket: the next generation, and the other bank cleared for it.
+            if (lane == 0)
+                __hip_atomic_fetch_add(rb, (uint64_t{1} << 32) - static_cast<uint64_t>(chunks), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            uint64_t* other = rb + 8 + (bank ^ 1) * kBankWords;
+            st_sync(other + lane, 0);
+            st_sync(other + 64 + lane, 0);
         }
     }
-    __syncthreads();
-    const float M = s_M;
-    const double rinv = 1.0 / s_S;
+    // Wave 0 polls the row's partials, lane j reading chunk j's pair, and combines them once all are there.
+    if (wave0) {
+        bool ready = false;
+        for (int it = 0; it < spin; ++it) {
+            uint64_t w0 = 1, w1 = 1;
+            if (lane < chunks) {
+                w0 = ld_sync(slots + 2 * lane);
+                w1 = ld_sync(slots + 2 * lane + 1);
+            }
+            if (__all(w0 != 0 && w1 != 0)) {
+                combine_row(dec_max(w0), dec_sum(w1), chunks, &s_M, &s_rS);
+                ready = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (lane == 0) s_ready = ready ? 1 : 0;
+    }
+    lds_barrier();
+    if (!s_ready) {
+        // Fallback: every chunk of the row from x, a chunk at a time, wave 0's lane j keeping chunk j's partial.
+        float m_l = -INFINITY;
+        double s_l = 0.0;
+        for (int j = 0; j < chunks; ++j) {
+            lds_barrier();  // the previous chunk's LDS reads are done
+            float t[VPT][4];
+            load_chunk<BLOCK, VPT>(p, row, j, valid, t);
+            float tw, m;
+            double sum;
+            chunk_stats<BLOCK, VPT>(t, lds_m, lds_s, tw, m, sum);
+            if (lane == j) {
+                m_l = m;
+                s_l = sum;
+            }
+        }
+        if (wave0) combine_row(m_l, s_l, chunks, &s_M, &s_rS);
+        lds_barrier();
+    }
+    // This wave's factor exp(m_w - M) / S; a NaN sum (NaN keys, or every key masked) makes every output NaN, masked
+    // ones too.
+    const double factor = (mw != -INFINITY ? exp_gap(mw, s_M) : 0.0) * s_rS;
     float* yr = p.y + row * p.row_stride;
-    const int64_t v0 = chunk * (kChunk / 4);
+    const int64_t v0 = static_cast<int64_t>(chunk) * (BLOCK * VPT);
     const int64_t nvec = p.width / 4;
 #pragma unroll
-    for (int k = 0; k < kChunkVpt; ++k) {
-        const int64_t v = v0 + threadIdx.x + k * kBlock;
+    for (int k = 0; k < VPT; ++k) {
+        const int64_t v = v0 + threadIdx.x + k * BLOCK;
         if (v < nvec) {
             float o[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                // masked keys: exp(-inf - M) = 0 (NaN when the sum is)
-                const float e = s[k][i] == -INFINITY ? 0.0f : exp_diff(s[k][i], M);
-                o[i] = static_cast<float>(static_cast<double>(e) * rinv);
-            }
+            for (int i = 0; i < 4; ++i) o[i] = static_cast<float>(static_cast<double>(s[k][i]) * factor);
             st128_nt(yr + v * 4, pack<F32>(o));
         }
     }
 }
 
-int64_t split_chunks(int64_t rows, int64_t width) {
-    const int64_t chunks = (width + kChunk - 1) / kChunk;
-    // Split only rows whose one-workgroup form would leave the chip mostly idle.
-    if (chunks < 2 || chunks > kMaxChunks || rows > kMaxRows || rows * 4 >= 1024 || width % 4 != 0) return 0;
-    return chunks;
+// The split launch's shape: 1024-thread workgroups (16 waves: the per-element work of a chunk spread thin, one LDS
+// stage for the chunk's partial), VPT vectors a lane, and at most max_blocks workgroups -- half of what the chip holds
+// at once at the kernel's register count (one 1024-thread workgroup a CU at up to 128 registers, two at up to 64),
+// so every chunk of a row is resident while its row waits. block 0 = no split. Measured at config 2a's 32 rows of
+// 32768 (the rest of the shapes within 8%): 8 chunks a row of 4096 keys in 1024 threads 5.8-6.0 us a call; 16 chunks
+// of 2048 in 512 threads 6.4 us; 8 of 4096 in 512 threads (two vectors a lane) 6.5 us; 32 of 1024 in 256 threads
+// 12.7 us (the wait for the row's partials grows with the pollers and chunks).
+struct SplitShape {
+    int block = 0, vpt = 0;
+    int64_t max_blocks = 0;
+    int64_t chunk() const { return static_cast<int64_t>(block) * vpt * 4; }
+};
+constexpr SplitShape kSplitShapes[] = {{1024, 1, 256}, {1024, 2, 128}, {1024, 4, 128}};
+
+// A row is split only when its one-workgroup form would leave the chip mostly idle (fewer than kMaxSplitRows rows),
+// into the smallest chunks that keep the launch within its shape's max_blocks and a row within kMaxChunks chunks.
+SplitShape split_shape(int64_t rows, int64_t width) {
+    if (width % 4 != 0 || rows >= kMaxSplitRows) return {};
+    for (const SplitShape& sh : kSplitShapes) {
+        const int64_t chunks = (width + sh.chunk() - 1) / sh.chunk();
+        if (chunks < 2) return {};
+        if (chunks <= kMaxChunks && rows * chunks <= sh.max_blocks) return sh;
+    }
+    return {};
 }
 
-size_t split_scratch_bytes(int64_t rows, int64_t chunks) {
-    return (static_cast<size_t>(rows * chunks) * 16 + 255) / 256 * 256;
-}
+int64_t split_chunks(int64_t width, const SplitShape& sh) { return (width + sh.chunk() - 1) / sh.chunk(); }
+
+size_t split_scratch_bytes(int64_t rows) { return static_cast<size_t>(rows * kRowWords) * 8; }
+
+// Polls a split workgroup makes before computing its row alone (a test sets it small to take that path).
+int g_spin_limit = 1 << 14;
 
 template <int LPR>
 int go_vec(hipStream_t s, const SoftmaxArgs& p, int nv) {
@@ -339,16 +471,19 @@ constexpr int kMaxNv = 8;
 
 int launch_softmax(hipStream_t s, const SoftmaxArgs& p, void* scratch) {
     if (p.rows == 0) return XS_HIP_OK;
-    const int64_t chunks = split_chunks(p.rows, p.width);
-    if (scratch != nullptr && chunks > 0 && aligned16(p.x) && aligned16(p.y) && p.row_stride % 4 == 0) {
+    const SplitShape sh = split_shape(p.rows, p.width);
+    if (scratch != nullptr && sh.block > 0 && aligned16(p.x) && aligned16(p.y) && p.row_stride % 4 == 0) {
         if (reinterpret_cast<uintptr_t>(scratch) % 16 != 0)
             return fail(XS_HIP_EINVAL, "xs_hip_softmax_masked: scratch must be 16-byte aligned");
-        auto* partial = static_cast<uint64_t*>(scratch);
+        auto* sync = static_cast<uint64_t*>(scratch);
+        const int chunks = static_cast<int>(split_chunks(p.width, sh));
         const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(p.rows));
-        softmax_partials<<<grid, kBlock, 0, s>>>(p, static_cast<int>(chunks), partial);
-        int rc = check_launch("xs_hip_softmax_masked");
-        if (rc != XS_HIP_OK) return rc;
-        softmax_finish<<<grid, kBlock, 0, s>>>(p, static_cast<int>(chunks), partial);
+        const int sp = g_spin_limit;
+        switch (sh.vpt) {
+            case 1: softmax_split<1024, 1><<<grid, 1024, 0, s>>>(p, chunks, sync, sp); break;
+            case 2: softmax_split<1024, 2><<<grid, 1024, 0, s>>>(p, chunks, sync, sp); break;
+            default: softmax_split<1024, 4><<<grid, 1024, 0, s>>>(p, chunks, sync, sp); break;
+        }
         return check_launch("xs_hip_softmax_masked");
     }
     // The in-register kernel needs whole 128-bit vectors; the three-pass kernel handles y aliasing x by reading the
@@ -393,8 +528,8 @@ int xs_hip_softmax(void* stream, const float* x, float* y, int64_t rows, int64_t
 
 size_t xs_hip_softmax_scratch(int64_t rows, int64_t width) {
     if (rows <= 0 || width <= 0) return 0;
-    const int64_t chunks = split_chunks(rows, width);
-    return chunks > 0 ? split_scratch_bytes(rows, chunks) : 0;
+    const SplitShape sh = split_shape(rows, width);
+    return sh.block > 0 ? split_scratch_bytes(rows) : 0;
 }
 
 int xs_hip_softmax_masked(void* stream, const float* x, float* y, int64_t rows, int64_t width, int64_t row_stride,
@@ -407,5 +542,7 @@ int xs_hip_softmax_masked(void* stream, const float* x, float* y, int64_t rows, 
     const SoftmaxArgs p{x, y, rows, width, row_stride, scale, valid_len, valid_len_all};
     return launch_softmax(as_stream(stream), p, scratch);
 }
+
+void xs_hip_set_spin_limit(int polls) { g_spin_limit = polls < 0 ? 0 : polls; }
 
 }  // extern "C"

@@ -843,6 +843,131 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 using namespace xs_hip;
 
+// ---- argmax in one launch --------------------------------------------------------------------------------------
+//
+// grid (chunks, rows) of kBlock threads; a workgroup reduces `span` values of its row from chunk * span, kBlock * VPT * 4
+// at a time (plain loads: at a few KiB a workgroup the load latency is the cost, and the non-temporal form measured
+// 0.3-0.4 us slower), to the largest order word (the order above: the lower index wins an exact tie, NaN is never
+// picked). A row of one chunk (span = width) writes its result there. Otherwise each workgroup but the row's last
+// chunk publishes its word into the row's slot of `sync` with one device-scope atomic store and exits; the row's last
+// chunk -- the row's last workgroup to be dispatched, so every other chunk of its row is already running or done and
+// none of them waits on anything -- polls the row's slots until all are published, takes the largest, writes the
+// row's value and index, and returns the slots to zero. `sync` holds rows * chunks 64-bit words, zero at entry and at
+// exit; a published word is never 0 (a chunk with no non-NaN value publishes 1, below every element's word, whose low
+// half, the complement of an index below 2^31, is at least 2^31). Every access to it is a relaxed device-scope atomic,
+// which this part keeps coherent across the XCDs' L2s without cache write-back or invalidation. (A ticket counter a
+// workgroup takes at its start, as the split softmax does, measured 1 us slower here: 149 workgroups' atomics on one
+// address queue up.)
+constexpr int kArgMaxChunks = 256;
+constexpr int kArgMaxSplitRows = 256;
+constexpr int kArgmaxPolls = 1 << 24;  // the poller's bound: far past the time its row's other chunks take to finish
+
+__device__ __forceinline__ uint64_t block_max_u64(uint64_t v) {
+    __shared__ uint64_t sv[kBlock / 64];
+    v = wave_max_u64(v);
+    if ((threadIdx.x & 63) == 0) sv[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = sv[0];
+    for (int w = 1; w < kBlock / 64; ++w) v = sv[w] > v ? sv[w] : v;
+    return v;
+}
+
+template <int VPT>
+__global__ __launch_bounds__(kBlock) void argmax_split(const float* __restrict__ x, float* __restrict__ values,
+                                                       int32_t* __restrict__ indices, int64_t width, int chunks,
+                                                       int64_t span, bool vec, uint64_t* __restrict__ sync) {
+    const int64_t row = blockIdx.y;
+    const int chunk = blockIdx.x;
+    const float* xr = x + row * width;
+    const int64_t begin = static_cast<int64_t>(chunk) * span;
+    const int64_t end = begin + span < width ? begin + span : width;
+    uint64_t best = 0;
+    for (int64_t start = begin; start < end; start += kBlock * VPT * 4) {
+        if (vec) {
+            u32x4 raw[VPT];
+#pragma unroll
+            for (int k = 0; k < VPT; ++k) {
+                const int64_t idx = start + static_cast<int64_t>(threadIdx.x + k * kBlock) * 4;
+                if (idx < end) raw[k] = ld128(xr + idx);
+            }
+#pragma unroll
+            for (int k = 0; k < VPT; ++k) {
+                const int64_t idx = start + static_cast<int64_t>(threadIdx.x + k * kBlock) * 4;
+                if (idx < end) {
+                    float f[4];
+                    unpack<F32>(raw[k], f);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint64_t w = order_word(f[i], idx + i);
+                        best = w > best ? w : best;
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < VPT; ++k)
+                for (int i = 0; i < 4; ++i) {
+                    const int64_t j = start + static_cast<int64_t>(threadIdx.x + k * kBlock) * 4 + i;
+                    if (j < end) {
+                        const uint64_t w = order_word(xr[j], j);
+                        best = w > best ? w : best;
+                    }
+                }
+        }
+    }
+    best = block_max_u64(best);
+    if (chunks == 1) {
+        if (threadIdx.x == 0) put_pick(xr, values, indices, row, best);
+        return;
+    }
+    uint64_t* slots = sync + row * chunks;
+    if (chunk != chunks - 1) {
+        if (threadIdx.x == 0)
+            __hip_atomic_store(slots + chunk, best == 0 ? uint64_t{1} : best, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    if (threadIdx.x >= 64) return;
+    const int lane = threadIdx.x;
+    for (int it = 0; it < kArgmaxPolls; ++it) {
+        uint64_t m = 0;
+        bool all = true;
+        for (int j = lane; j < chunks - 1; j += 64) {
+            const uint64_t w = __hip_atomic_load(slots + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            all = all && w != 0;
+            m = w > m ? w : m;
+        }
+        if (__all(all)) {
+            m = wave_max_u64(m == 1 ? 0 : m);
+            best = m > best ? m : best;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    if (lane == 0) put_pick(xr, values, indices, row, best);
+    for (int j = lane; j < chunks - 1; j += 64)
+        __hip_atomic_store(slots + j, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Launch shape of xs_hip_argmax: vectors a lane per pass (1, 2, 4 or 8) and chunks a row. Rows are split into chunks
+// of kBlock * VPT * 4 values, the smallest VPT keeping the launch within about eight workgroups a CU (2048) and a row
+// within kArgMaxChunks; 256 rows or more, or rows too wide for that, take one workgroup a row (chunks = 1).
+struct ArgmaxShape {
+    int vpt = 1;
+    int64_t chunks = 1;
+};
+
+ArgmaxShape argmax_shape(int64_t rows, int64_t width) {
+    if (rows < kArgMaxSplitRows) {
+        for (int vpt = 1; vpt <= 8; vpt *= 2) {
+            const int64_t chunk = static_cast<int64_t>(kBlock) * vpt * 4;
+            const int64_t chunks = (width + chunk - 1) / chunk;
+            if (chunks <= kArgMaxChunks && (rows * chunks <= 2048 || vpt == 8)) return {vpt, chunks};
+        }
+    }
+    return {4, 1};
+}
+
 extern "C" {
 
 size_t xs_hip_topk_scratch(int64_t rows, int64_t width, int64_t k) {
@@ -913,6 +1038,41 @@ int xs_hip_topk(void* stream, const float* x, float* values, int32_t* indices, i
                                                                                                         k, scratch);
     topk_wide_finish<<<static_cast<unsigned>(rows), kBlock, 0, s>>>(x, values, indices, width, k, chunks, scratch);
     return check_launch("xs_hip_topk");
+}
+
+size_t xs_hip_argmax_scratch(int64_t rows, int64_t width) {
+    if (rows <= 0 || width <= 0) return 0;
+    const int64_t chunks = argmax_shape(rows, width).chunks;
+    return chunks <= 1 ? 0 : align_up(static_cast<size_t>(rows * chunks) * sizeof(uint64_t), 256);
+}
+
+int xs_hip_argmax(void* stream, const float* x, float* values, int32_t* indices, int64_t rows, int64_t width,
+                  void* scratch) {
+    if (rows < 0 || width <= 0)
+        return fail(XS_HIP_EINVAL, "xs_hip_argmax: " + std::to_string(rows) + " rows of " + std::to_string(width));
+    if (width > INT32_MAX)
+        return fail(XS_HIP_EUNSUPPORTED, "xs_hip_argmax: rows wider than 2^31 - 1 have no i32 index");
+    if (rows == 0) return XS_HIP_OK;
+    if (x == nullptr || values == nullptr || indices == nullptr)
+        return fail(XS_HIP_EINVAL, "xs_hip_argmax: null buffer");
+    if (rows > kMaxRows) return fail(XS_HIP_EUNSUPPORTED, "xs_hip_argmax: more than 65535 rows in one call");
+    const ArgmaxShape sh = argmax_shape(rows, width);
+    if (sh.chunks > 1 && (scratch == nullptr || reinterpret_cast<uintptr_t>(scratch) % 8 != 0))
+        return fail(XS_HIP_EINVAL, "xs_hip_argmax: rows of " + std::to_string(width) +
+                                       " need xs_hip_argmax_scratch bytes of zero-filled, 8-byte aligned scratch");
+    const bool vec = width % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
+    const int64_t span = sh.chunks > 1 ? static_cast<int64_t>(kBlock) * sh.vpt * 4 : width;
+    const dim3 grid(static_cast<unsigned>(sh.chunks), static_cast<unsigned>(rows));
+    const hipStream_t s = as_stream(stream);
+    auto* sync = static_cast<uint64_t*>(scratch);
+    const int c = static_cast<int>(sh.chunks);
+    switch (sh.vpt) {
+        case 1: argmax_split<1><<<grid, kBlock, 0, s>>>(x, values, indices, width, c, span, vec, sync); break;
+        case 2: argmax_split<2><<<grid, kBlock, 0, s>>>(x, values, indices, width, c, span, vec, sync); break;
+        case 4: argmax_split<4><<<grid, kBlock, 0, s>>>(x, values, indices, width, c, span, vec, sync); break;
+        default: argmax_split<8><<<grid, kBlock, 0, s>>>(x, values, indices, width, c, span, vec, sync); break;
+    }
+    return check_launch("xs_hip_argmax");
 }
 
 }  // extern "C"

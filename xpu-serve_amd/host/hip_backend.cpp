@@ -81,6 +81,8 @@ xs_dtype abi(DType t) {
 }
 
 size_t align_up(size_t n) { return (n + 255) & ~size_t{255}; }
+// A node whose launch uses the session's zero-filled sync scratch rather than an arena block.
+constexpr int32_t kSyncScratch = -2;
 
 // Device memory owned by the session.
 class DeviceMemory {
@@ -252,9 +254,10 @@ private:
         std::vector<int32_t> conv;              // per (node, output 0): arena block of its f32 conversion, or -1
         std::vector<std::vector<Value>> convert_before;  // per node: values converted to f32 before its launch
         std::vector<size_t> block_offset;       // arena offset of each block
-        std::vector<int32_t> scratch;           // per node: its scratch block, or -1
+        std::vector<int32_t> scratch;           // per node: its scratch block, -1, or kSyncScratch
         std::vector<size_t> scratch_bytes;
         size_t arena_bytes = 0;
+        size_t sync_bytes = 0;                  // the session's zero-filled scratch the step's launches need
         // Captured steps by key-count bucket (see Program::run): the executable graph, the arena generation its
         // addresses belong to, and how often the bucket has run.
         struct Captured {
@@ -325,6 +328,15 @@ public:
         if (arena_.grow(bytes)) ++arena_gen_;
     }
     uint64_t arena_gen() const { return arena_gen_; }
+    // Scratch of the launches whose workgroups combine partials within one launch (the split softmax): zero-filled
+    // when allocated, and every such launch leaves it ready for the next, so the session's launches (one stream, in
+    // order) share it. Growing it moves it, as the arena.
+    char* sync() const { return sync_.get(); }
+    void grow_sync(size_t bytes) {
+        if (bytes == 0 || !sync_.grow(bytes)) return;
+        check(xs_hip_memset(sync_.get(), 0, sync_.size(), stream_), "sync scratch");
+        ++arena_gen_;
+    }
     // HIP-graph replay of repeated steps: the "graphs" backend option ("1", the default, or "0").
     bool graphs() const { return graphs_; }
     // The step record a replayed step reads from device memory: [first token the step appends, keys held]. Its host
@@ -366,6 +378,7 @@ private:
     std::vector<KvState> kv_;
     std::map<std::string, Leaf> leaves_;
     DeviceMemory arena_;
+    DeviceMemory sync_;
     uint64_t arena_gen_ = 0;
     bool graphs_ = true;
     DeviceMemory step_;
@@ -956,8 +969,14 @@ Program::RunPlan& Program::plan_for(int64_t T, std::span<const std::string> only
             bytes = xs_hip_topk_scratch(numel(x) / std::max<int64_t>(width, 1), width,
                                         std::get<graph::TopKAttrs>(nd.attrs).k);
         } else if (plan_[i].op == Op::Softmax) {
+            // Not in the arena: a split softmax needs its scratch zero-filled at entry (and leaves it so).
             const Dims& x = p.shapes[i][0];
-            bytes = xs_hip_softmax_scratch(numel(x) / std::max<int64_t>(x.back(), 1), x.back());
+            const size_t sync = xs_hip_softmax_scratch(numel(x) / std::max<int64_t>(x.back(), 1), x.back());
+            if (sync > 0) {
+                p.scratch[i] = kSyncScratch;
+                p.sync_bytes = std::max(p.sync_bytes, sync);
+            }
+            continue;
         } else if (plan_[i].op == Op::Attention) {
             const Dims& q = p.shapes[i][0];
             const Dims& k = g_.type(nd.inputs[1]).shape;
@@ -1179,10 +1198,8 @@ void Program::launch(size_t i, const RunPlan& p, int64_t T, int64_t L, int64_t r
         case Op::Softmax: {
             float* y = reinterpret_cast<float*>(ptr(p, Value{static_cast<int32_t>(i), 0}));
             const int64_t rows = rows_of(out), width = out.back();
-            if (p.scratch[i] >= 0) {
-                check(xs_hip_softmax_masked(st, f32(0), y, rows, width, width, 1.0f, nullptr, width,
-                                            s_.arena().get() + p.block_offset[static_cast<size_t>(p.scratch[i])]),
-                      what);
+            if (p.scratch[i] == kSyncScratch) {
+                check(xs_hip_softmax_masked(st, f32(0), y, rows, width, width, 1.0f, nullptr, width, s_.sync()), what);
             } else {
                 check(xs_hip_softmax(st, f32(0), y, rows, width), what);
             }
@@ -1352,6 +1369,7 @@ void Program::run(const TensorMap& inputs, TensorMap& outputs, std::span<const s
     }
     RunPlan& p = plan_for(T, only);
     s_.grow_arena(p.arena_bytes);
+    s_.grow_sync(p.sync_bytes);
     // The host side goes through page-locked staging, so every copy is asynchronous and the step waits once: the step
     // record, then the inputs, then the outputs.
     size_t stage_bytes = 256;

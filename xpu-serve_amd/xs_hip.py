@@ -102,6 +102,9 @@ _SIGS = {
     "xs_hip_softmax": [_P, _P, _P, _I64, _I64],
     "xs_hip_softmax_masked": [_P, _P, _P, _I64, _I64, _I64, _F, _P, _I64, _P],
     "xs_hip_softmax_scratch": [_I64, _I64],
+    "xs_hip_set_spin_limit": [_INT],
+    "xs_hip_argmax": [_P, _P, _P, _P, _I64, _I64, _P],
+    "xs_hip_argmax_scratch": [_I64, _I64],
     "xs_hip_topk_scratch": [_I64, _I64, _I64],
     "xs_hip_topk": [_P, _P, _P, _P, _I64, _I64, _I64, _P],
     "xs_hip_rope": [_P, _INT, _P, _INT, _P, _P, _INT, _P, _I64, _I64, _I64, _I64, _I64, _P],
@@ -121,7 +124,8 @@ _SIGS = {
 }
 _RESTYPES = {"xs_hip_topk_scratch": C.c_size_t, "xs_hip_softmax_scratch": C.c_size_t,
              "xs_hip_attention_i8_split": C.c_int64, "xs_hip_attention_i8_scratch": C.c_size_t,
-             "xs_hip_last_error": C.c_char_p}
+             "xs_hip_last_error": C.c_char_p, "xs_hip_set_spin_limit": None,
+             "xs_hip_argmax_scratch": C.c_size_t}
 
 _lib_handle = None
 
@@ -442,6 +446,23 @@ def topk(x: DeviceTensor, k: int, scratch: Optional[TopkScratch] = None,
     indices = DeviceTensor.empty(I32, shape)
     s = (scratch or _default_scratch).get(rows, width, k)
     call("xs_hip_topk", stream, C.c_void_p(x.ptr), C.c_void_p(values.ptr), C.c_void_p(indices.ptr), rows, width, k,
+         C.c_void_p(s))
+    return values, indices
+
+
+_argmax_scratch = Scratch()
+
+
+def argmax(x: DeviceTensor, scratch: Optional[Scratch] = _argmax_scratch,
+           stream=None) -> Tuple[DeviceTensor, DeviceTensor]:
+    """xs_hip_argmax: (values f32, indices i32) [...] of each row's maximum, the lower index on a tie -- topk(x, 1)
+    in one launch. `scratch` is zero-filled and each call leaves it so."""
+    width = x.shape[-1]
+    rows = x.numel // width
+    values = DeviceTensor.empty(F32, tuple(x.shape[:-1]))
+    indices = DeviceTensor.empty(I32, tuple(x.shape[:-1]))
+    s = scratch.ptr(lib().xs_hip_argmax_scratch(rows, width))
+    call("xs_hip_argmax", stream, C.c_void_p(x.ptr), C.c_void_p(values.ptr), C.c_void_p(indices.ptr), rows, width,
          C.c_void_p(s))
     return values, indices
 
