@@ -328,6 +328,16 @@ int xs_hip_attention_i8_at(void* stream, const float* q, const void* k_codes, co
                            float scale, float softcap, int64_t window, int causal, int64_t split, void* scratch);
 int64_t xs_hip_attention_i8_split(int64_t tokens, int64_t kv_heads, int64_t kv_len);
 size_t xs_hip_attention_i8_scratch(int64_t tokens, int64_t q_heads, int64_t head_dim, int64_t split);
+/* xs_hip_attention_i8 with no scratch argument and no allocation: a split's partial rows go to a device array of
+ * 8 MiB (8388608 bytes) that the library holds on each GPU it runs on until the process ends; a split needing more
+ * (xs_hip_attention_i8_scratch bytes) is refused with XS_HIP_EINVAL. No reference counterpart: it is for callers that
+ * cannot allocate device memory -- code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc. Same results as xs_hip_attention_i8 (the same kernels). Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (two streams, or two host threads) race. */
+int xs_hip_attention_i8_noalloc(void* stream, const float* q, const void* k_codes, const void* k_scales,
+                                const void* v_codes, const void* v_scales, float* out, int64_t tokens, int64_t q_heads,
+                                int64_t kv_heads, int64_t head_dim, int64_t kv_len, float scale, float softcap,
+                                int64_t window, int causal, int64_t split);
 
 /* ---- Strided copy -------------------------------------------------------------------------------------------- */
 

@@ -23,6 +23,8 @@
 #include <cmath>
 #include <type_traits>
 
+#include <mutex>
+
 #include "common.h"
 
 namespace xs_hip {
@@ -708,6 +710,39 @@ int attention_i8(void* stream, const float* q, const void* k_codes, const void* 
     return check_launch(what);
 }
 
+// ---- The no-allocation entry point ---------------------------------------------------------------------------
+//
+// Its split partials live in `scratch`, a file-scope device array of kNoAllocScratchBytes that every GPU the library
+// runs on holds until the process ends (the loader places it with the code object, zero-filled; nothing needs to
+// start at zero: each split writes its partial rows before the combine reads them). In host code the array's name
+// stands for a host-side shadow, not a device address: the device address is looked up once per device, with that
+// device current, and kept.
+constexpr size_t kNoAllocScratchBytes = size_t{8} << 20;
+__device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+
+// The device address of `scratch` on the current device, or an error code.
+int noalloc_scratch(void** out, const char* what) {
+    static std::mutex mu;
+    static void* addr[kMaxDevices] = {};
+    int dev = 0;
+    const int rc = check_hip(hipGetDevice(&dev), what);
+    if (rc != XS_HIP_OK) return rc;
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(XS_HIP_EUNSUPPORTED, std::string(what) + ": device " + std::to_string(dev) + " past " +
+                                             std::to_string(kMaxDevices));
+    std::lock_guard<std::mutex> lock(mu);
+    if (addr[dev] == nullptr) {
+        void* p = nullptr;
+        const int r = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), what);
+        if (r != XS_HIP_OK) return r;
+        addr[dev] = p;
+    }
+    *out = addr[dev];
+    return XS_HIP_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -728,6 +763,27 @@ int xs_hip_attention_i8_at(void* stream, const float* q, const void* k_codes, co
         return fail(XS_HIP_EINVAL, "xs_hip_attention_i8_at: kv_len must be an 8-byte aligned device int64");
     return attention_i8(stream, q, k_codes, k_scales, v_codes, v_scales, out, tokens, q_heads, kv_heads, head_dim,
                         kv_capacity, kv_len, scale, softcap, window, causal, split, scratch, "xs_hip_attention_i8_at");
+}
+
+int xs_hip_attention_i8_noalloc(void* stream, const float* q, const void* k_codes, const void* k_scales,
+                                const void* v_codes, const void* v_scales, float* out, int64_t tokens, int64_t q_heads,
+                                int64_t kv_heads, int64_t head_dim, int64_t kv_len, float scale, float softcap,
+                                int64_t window, int causal, int64_t split) {
+    const char* what = "xs_hip_attention_i8_noalloc";
+    void* buf = nullptr;
+    if (split > 1) {
+        const size_t need = xs_hip_attention_i8_scratch(tokens, q_heads, head_dim, split);
+        if (need > kNoAllocScratchBytes)
+            return fail(XS_HIP_EINVAL, std::string(what) + ": split " + std::to_string(split) + " of " +
+                                           std::to_string(tokens) + " x " + std::to_string(q_heads) +
+                                           " query rows of " + std::to_string(head_dim) + " needs " +
+                                           std::to_string(need) + " bytes of scratch; this entry point holds " +
+                                           std::to_string(kNoAllocScratchBytes));
+        const int rc = noalloc_scratch(&buf, what);
+        if (rc != XS_HIP_OK) return rc;
+    }
+    return attention_i8(stream, q, k_codes, k_scales, v_codes, v_scales, out, tokens, q_heads, kv_heads, head_dim,
+                        kv_len, nullptr, scale, softcap, window, causal, split, buf, what);
 }
 
 }  // extern "C"

@@ -119,6 +119,8 @@ _SIGS = {
     "xs_hip_attention_i8": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _F, _I64, _INT, _I64, _P],
     "xs_hip_attention_i8_at": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _F, _F, _I64, _INT, _I64,
                                _P],
+    "xs_hip_attention_i8_noalloc": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _F, _I64, _INT,
+                                    _I64],
     "xs_hip_attention_i8_split": [_I64, _I64, _I64],
     "xs_hip_attention_i8_scratch": [_I64, _I64, _I64, _I64],
 }
