@@ -65,22 +65,22 @@ def test_builder_checks():
     with pytest.raises(S.BackendError, match="cannot broadcast"):
         g.add(x, y)
     w = g.constant(np.ones(4, np.float32), S.F32)
-    with pytest.raises(S.BackendError, match="rms_norm weight"):
+    with pytest.raises(S.BackendError, match="rms_norm: the weight must be"):
         g.rms_norm(x, w)
-    with pytest.raises(S.BackendError, match="topk"):
+    with pytest.raises(S.BackendError, match="topk: k = 9"):
         g.topk(x, 9)
-    with pytest.raises(S.BackendError, match="symbolic"):
+    with pytest.raises(S.BackendError, match="symbolic axis T"):
         g.slice(x, 0, 0, 2)
-    with pytest.raises(S.BackendError, match="element count"):
+    with pytest.raises(S.BackendError, match="change the element count"):
         g.reshape(x, [S.T, 4])
-    with pytest.raises(S.BackendError, match="duplicate graph input"):
+    with pytest.raises(S.BackendError, match="an input named .x. exists already"):
         g.input("x", S.F32, [4])
     q = g.input("q", S.F32, [S.T, 4, 64])
     pos = g.input("pos", S.I32, [S.T])
-    with pytest.raises(S.BackendError, match="inv_freq"):
+    with pytest.raises(S.BackendError, match="inv_freq must be f32"):
         g.rope(q, pos, g.constant(np.ones(16, np.float32), S.F32))
     slot = g.kv_slot(2, 64, label="a")
-    with pytest.raises(S.BackendError, match="expects k, v"):
+    with pytest.raises(S.BackendError, match="appends k and v of"):
         g.kv_cache(slot, q, q)
 
 
@@ -138,8 +138,8 @@ def test_graph_validation():
     g.kv_slot(2, 64, label="unused")
     x = g.input("x", S.F32, [S.T, 4])
     g.output("y", g.silu(x))
-    _refusal(g, "used 0 times")
-    _refusal(S.Graph(), "no outputs")
+    _refusal(g, "has 0 cache nodes")
+    _refusal(S.Graph(), "nothing is marked as an output")
 
 
 def test_graphs_option_values():
