@@ -293,6 +293,15 @@ int xs_hip_quantize_kv_pair(void* stream, xs_dtype x_dtype, const void* k, const
                             void* v_codes, void* v_scales, int64_t rows, int64_t width, const int64_t* row0,
                             int64_t rows_per_unit, int64_t capacity_rows);
 
+/* The Float KV format's append: a step's keys k and values v, both [rows, width] of x_dtype (f32, f16 or bf16), stored
+ * as rows of row_dtype (XS_F16 at f16 precision, XS_F32 at f32; RNE) -- at rows [0, rows) of k_rows / v_rows with row0
+ * NULL, or at row row0[0] * rows_per_unit of caches of capacity_rows rows, read from device memory when the kernel runs
+ * (rows past the capacity are written nowhere); v and v_rows both NULL append keys only. Replaces the SYCL session's
+ * float append (sycl_backend.cpp:2224-2231: to_half, or a copy at f32) in one launch for keys and values. */
+int xs_hip_kv_store_pair(void* stream, xs_dtype x_dtype, const void* k, const void* v, xs_dtype row_dtype,
+                         void* k_rows, void* v_rows, int64_t rows, int64_t width, const int64_t* row0,
+                         int64_t rows_per_unit, int64_t capacity_rows);
+
 /* y [rows, width] = x with each group of 128 values rotated as the TurboQuant formats rotate a row (inverse = 0), or
  * rotated back (inverse = 1); f32, 16-byte aligned, y may be x. Replaces sycl_be::kv_rotate (sycl_kernels.h:219-221);
  * semantics quant::turbo::rotate_group (kv_turbo.cpp:118-129). */
@@ -328,6 +337,22 @@ int xs_hip_attention_i8_at(void* stream, const float* q, const void* k_codes, co
                            float scale, float softcap, int64_t window, int causal, int64_t split, void* scratch);
 int64_t xs_hip_attention_i8_split(int64_t tokens, int64_t kv_heads, int64_t kv_len);
 size_t xs_hip_attention_i8_scratch(int64_t tokens, int64_t q_heads, int64_t head_dim, int64_t split);
+/* Decode attention over a float KV cache: keys and values [kv_len, kv_heads, head_dim] of kv_dtype (XS_F16 or XS_F32;
+ * the Float KV format: f16 rows at f16 precision, f32 at f32), q and out as xs_hip_attention_i8, the same key
+ * selection, scale, softcap, split and scratch (xs_hip_attention_i8_split, xs_hip_attention_i8_scratch) -- cpu_ref::
+ * attention (ops.cpp:113-156, 535-594) over the rows the cache holds, f32 accumulation. Replaces
+ * sycl_be::attention_rows<KV> with attention_combine (sycl_kernels.h, KV = half or float; dispatch
+ * sycl_backend.cpp:2274-2290). q, out, k, v 16-byte aligned. */
+int xs_hip_attention(void* stream, xs_dtype kv_dtype, const float* q, const void* k, const void* v, float* out,
+                     int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t kv_len, float scale,
+                     float softcap, int64_t window, int causal, int64_t split, void* scratch);
+/* xs_hip_attention over a cache of kv_capacity rows of which the kernel reads how many it holds from the device int64
+ * at kv_len when it runs (clamped to [0, kv_capacity]): for steps replayed from captured HIP graphs. No reference
+ * counterpart, as xs_hip_attention_i8_at. */
+int xs_hip_attention_at(void* stream, xs_dtype kv_dtype, const float* q, const void* k, const void* v, float* out,
+                        int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t kv_capacity,
+                        const int64_t* kv_len, float scale, float softcap, int64_t window, int causal, int64_t split,
+                        void* scratch);
 /* xs_hip_attention_i8 with no scratch argument and no allocation: a split's partial rows go to a device array of
  * 8 MiB (8388608 bytes) that the library holds on each GPU it runs on until the process ends; a split needing more
  * (xs_hip_attention_i8_scratch bytes) is refused with XS_HIP_EINVAL. No reference counterpart: it is for callers that

@@ -187,6 +187,20 @@ int xsg_output(void* g, const char* name, int64_t v) {
     }));
 }
 
+// The graph's output names, one a line (the same buffer protocol as xsg_dump).
+int64_t xsg_outputs(void* g, char* buf, int64_t len) {
+    return guard([&] {
+        std::string s;
+        for (const auto& o : static_cast<Graph*>(g)->outputs()) s += o.name + "\n";
+        if (buf != nullptr && len > 0) {
+            const size_t n = std::min<size_t>(s.size(), static_cast<size_t>(len - 1));
+            std::memcpy(buf, s.data(), n);
+            buf[n] = 0;
+        }
+        return static_cast<int64_t>(s.size());
+    });
+}
+
 int64_t xsg_dump(void* g, char* buf, int64_t len) {
     return guard([&] {
         const std::string s = static_cast<Graph*>(g)->dump();

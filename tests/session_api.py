@@ -14,7 +14,7 @@ F32, F16, BF16, I64, I32 = 0, 1, 2, 3, 4
 NP = {F32: np.float32, F16: np.float16, BF16: np.uint16, I64: np.int64, I32: np.int32}
 # xs::graph::OpKind values of the unary ops.
 SCALE, TANH, GELU_TANH, SOFTCAP, SIGMOID, SILU, SOFTPLUS, CLAMP, GELU = 7, 8, 9, 10, 11, 12, 13, 14, 34
-KV_FLOAT, KV_I8 = 0, 1
+KV_FLOAT, KV_I8, KV_TURBO4 = 0, 1, 2
 SLICE_END = (1 << 63) - 1
 T, L = -1, -2
 
@@ -60,6 +60,7 @@ def lib():
         "xsg_reduce_sum": ([P, I64_, C.c_int], I64_),
         "xsg_output": ([P, C.c_char_p, I64_], C.c_int),
         "xsg_dump": ([P, C.c_char_p, I64_], I64_),
+        "xsg_outputs": ([P, C.c_char_p, I64_], I64_),
         "xsw_new": ([], P), "xsw_free": ([P], None),
         "xsw_add": ([P, C.c_char_p, C.c_int, C.c_int, dims, P], C.c_int),
         "xss_compile": ([C.c_int, C.POINTER(P), P, C.c_int, I64_, C.c_int, C.c_int, C.c_char_p], P),
@@ -292,11 +293,10 @@ class Session:
     def _output_names(g, only):
         if only:
             return list(only)
-        names = []
-        for line in g.dump().splitlines():
-            if line.startswith("output "):
-                names.append(line.split()[1])
-        return names
+        n = lib().xsg_outputs(g.h, None, 0)
+        buf = C.create_string_buffer(int(n) + 1)
+        lib().xsg_outputs(g.h, buf, n + 1)
+        return [name for name in buf.value.decode().split("\n") if name]
 
     def num_cached(self, program=0):
         return _ok(lib().xss_num_cached(self.h, program))

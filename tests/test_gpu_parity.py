@@ -63,6 +63,74 @@ def gelu_noise(x, b):
 # ---------------------------------------------------------------------------------------------------------------
 # int8 KV
 
+def test_kv_quantize_tiny_rows(ora):
+    """Rows whose |x| maximum is below 127 / FLT_MAX (f32 and bf16 reach it): 127 / amax overflows to inf, the
+    reference's nearbyint(x * inf) clamps to +-127 for a nonzero x, and 0 * inf = NaN gives code 0 (quant.cpp:259-267).
+    Beside them ordinary rows, and the f32 scalar path (a width off the vector)."""
+    rng = np.random.default_rng(57)
+    for width in (128, 100):
+        x = (rng.standard_normal((8, width)) * 1e-38).astype(np.float32)
+        x[0] = 0.0
+        x[1, :] = 0.0
+        x[1, 3] = -1e-40          # a subnormal alone in its row
+        x[2, ::3] = 0.0           # zeros among tiny values
+        x[5:] = rng.standard_normal((3, width)).astype(np.float32)  # ordinary rows
+        step(f"kv quantize tiny f32 rows [8, {width}]")
+        c, sc = X.quantize_kv(dev(x))
+        wc, ws = ora.quantize_kv(x)
+        assert_exact(c.numpy(), wc, f"tiny codes width {width}")
+        assert_exact(sc.numpy(), ws, f"tiny scales width {width}")
+        assert (np.abs(wc[1]) == np.where(x[1] != 0, 127, 0)).all()
+    xb = ora.narrow((rng.standard_normal((4, 128)) * 1e-38).astype(np.float32), BF16)
+    step("kv quantize tiny bf16 rows [4, 128]")
+    c, sc = X.quantize_kv(dev(xb, BF16))
+    wc, ws = ora.quantize_kv(ora.widen(xb, BF16))
+    assert_exact(c.numpy(), wc, "tiny bf16 codes")
+    assert_exact(sc.numpy(), ws, "tiny bf16 scales")
+
+
+def test_kv_store_pair(ora):
+    """The Float format's append: f32 / f16 / bf16 keys and values stored as f16 rows (RNE, overflow to inf) or f32 rows,
+    at the host row and at a device-held row with the rows past the capacity dropped; the scalar path for a width off
+    the vector."""
+    rng = np.random.default_rng(58)
+    for xdt in (F32, F16, BF16):
+        for rdt in (F16, F32):
+            for width in (128, 20):
+                rows, cap, at = 12, 40, 30  # a device row 30: rows 30..39 written, 40, 41 dropped
+                k = (rng.standard_normal((rows, width)) * 3).astype(np.float32)
+                k[0, 0] = 70000.0 if xdt == F32 else 1.0
+                v = (rng.standard_normal((rows, width))).astype(np.float32)
+                if xdt != F32:
+                    k, v = ora.narrow(k, xdt), ora.narrow(v, xdt)
+                kw = ora.widen(k, xdt) if xdt != F32 else k
+                vw = ora.widen(v, xdt) if xdt != F32 else v
+                step(f"kv store pair {DT[xdt]} -> {DT[rdt]} width {width}")
+                for row0 in (None, at):
+                    n_rows = cap if row0 is not None else rows
+                    ky = X.DeviceTensor.from_numpy(np.zeros((n_rows, width), np.float32 if rdt == F32 else np.float16),
+                                                   rdt)
+                    vy = X.DeviceTensor.from_numpy(np.zeros((n_rows, width), np.float32 if rdt == F32 else np.float16),
+                                                   rdt)
+                    rd = _dev_i64(row0) if row0 is not None else None
+                    kd, vd = dev(k, xdt), dev(v, xdt)  # held until the launch has run
+                    X.call("xs_hip_kv_store_pair", None, xdt, vp_(kd), vp_(vd), rdt, vp_(ky), vp_(vy),
+                           rows, width, C.c_void_p(rd.ptr) if rd else None, 1, cap)
+                    X.synchronize()
+                    first = row0 or 0
+                    n = min(rows, n_rows - first)
+                    for got, src in ((ky.numpy(), kw), (vy.numpy(), vw)):
+                        want = np.zeros_like(got)
+                        want[first:first + n] = ora.narrow(src[:n], rdt) if rdt != F32 else src[:n]
+                        assert_exact(got.view(np.uint16 if rdt == F16 else np.uint32),
+                                     want.view(np.uint16 if rdt == F16 else np.uint32),
+                                     f"{DT[xdt]}->{DT[rdt]} w{width} row0 {row0}")
+
+
+def vp_(t):
+    return C.c_void_p(t.ptr)
+
+
 def test_kv_quantize_goldens(ora):
     g = golden("kv_i8")
     step("kv quantize goldens f32 [64, 128]")
@@ -1058,6 +1126,85 @@ def test_attention_i8_decode_full_size(ora):
     k_rt = ora.dequantize_kv(kc.numpy(), ks.numpy()).reshape(k.shape)
     v_rt = ora.dequantize_kv(vc.numpy(), vs.numpy()).reshape(v.shape)
     assert_attention_close(y, ora.attention(q, k_rt, v_rt, 1.0 / math.sqrt(d)), "decode full size")
+
+
+# ---- the float KV cache's reader (f16 rows at f16 precision, f32 at f32) -------------------------------------------
+
+def test_attention_float_goldens(ora):
+    """The reference cpu-ref's own attention outputs (golden vectors written by the compiled reference) over f32 rows:
+    the f32 cache holds exactly the rows cpu-ref attends over."""
+    g = golden("attention")
+    hkv = g["k"].shape[1]
+    k, v = dev(g["k"]), dev(g["v"])
+    for name in ("causal", "window", "full", "softcap"):
+        scale, cap, window, causal = g[name + "_args"]
+        want = ora.attention(g["q"], g["k"], g["v"], float(scale), float(cap), int(window), bool(causal))
+        for split in (1, 3, 0):
+            step(f"attention f32 rows, oracle of golden {name} split {split}")
+            y = X.attention(dev(g["q"]), k, v, hkv, float(scale), float(cap), int(window), bool(causal), split).numpy()
+            assert_attention_close(y, want, f"{name} split {split}")
+
+
+@pytest.mark.parametrize("t,hq,hkv,d,n,window,cap,causal", [
+    (1, 32, 8, 128, 4097, 0, 0.0, True),
+    (4, 8, 8, 64, 1000, 0, 0.0, True),
+    (2, 12, 4, 128, 777, 100, 0.0, True),
+    (1, 16, 2, 256, 3000, 0, 30.0, True),
+    (3, 6, 1, 64, 500, 0, 0.0, False),
+    (2, 16, 2, 128, 2048, 64, 0.0, False),
+    (1, 40, 5, 128, 1500, 0, 0.0, True),
+    (5, 10, 2, 64, 5, 0, 0.0, True),
+    (1, 8, 1, 128, 70000, 0, 0.0, True),
+])
+@pytest.mark.parametrize("kvdt", [F32, F16])
+def test_attention_float_shapes(ora, t, hq, hkv, d, n, window, cap, causal, kvdt):
+    """xs_hip_attention over f32 rows, and over f16 rows (the oracle then attends over the same f16-rounded rows),
+    at the reference's f32 device bar, with splits 1, 7 and the library's."""
+    rng = np.random.default_rng(90 + n)
+    q = rng.standard_normal((t, hq, d)).astype(np.float32)
+    k = ora.narrow(rng.standard_normal((n, hkv, d)).astype(np.float32), kvdt) if kvdt != F32 else \
+        rng.standard_normal((n, hkv, d)).astype(np.float32)
+    v = ora.narrow(rng.standard_normal((n, hkv, d)).astype(np.float32), kvdt) if kvdt != F32 else \
+        rng.standard_normal((n, hkv, d)).astype(np.float32)
+    kw = ora.widen(k, kvdt) if kvdt != F32 else k
+    vw = ora.widen(v, kvdt) if kvdt != F32 else v
+    scale = 1.0 / math.sqrt(d)
+    want = ora.attention(q, kw, vw, scale, cap, window, causal)
+    kd, vd = dev(k, kvdt), dev(v, kvdt)
+    for split in (1, 7, 0):
+        step(f"attention {DT[kvdt]} rows T{t} H{hq}/{hkv} D{d} N{n} w{window} cap{cap} causal {causal} split {split}")
+        y = X.attention(dev(q), kd, vd, hkv, scale, cap, window, causal, split).numpy()
+        assert_attention_close(y, want, f"attention {DT[kvdt]} split {split}")
+
+
+def test_attention_float_at_device_length(ora):
+    """xs_hip_attention_at with the key count in device memory: bit-exact with xs_hip_attention at that count and the
+    same split; clamped to the capacity above it."""
+    rng = np.random.default_rng(91)
+    hq, hkv, d, cap = 8, 2, 128, 600
+    k = ora.narrow(rng.standard_normal((cap, hkv, d)).astype(np.float32), F16)
+    v = ora.narrow(rng.standard_normal((cap, hkv, d)).astype(np.float32), F16)
+    kd, vd = dev(k, F16), dev(v, F16)
+    scale = 1.0 / math.sqrt(d)
+    for t, n, n_dev in ((1, 257, 257), (3, 64, 64), (1, 600, 1600)):
+        q = dev(rng.standard_normal((t, hq, d)).astype(np.float32))
+        split = X.lib().xs_hip_attention_i8_split(t, hkv, cap)
+        nbytes = int(X.lib().xs_hip_attention_i8_scratch(t, hq, d, split))
+        sc = X.DeviceBuffer(nbytes) if nbytes else None
+        step(f"attention_at f16 T{t} n{n} (device {n_dev}) split {split}")
+        outs = []
+        for at in (False, True):
+            out = X.DeviceTensor.empty(F32, (t, hq, d))
+            head = [X.F16, C.c_void_p(q.ptr), C.c_void_p(kd.ptr), C.c_void_p(vd.ptr), C.c_void_p(out.ptr), t, hq, hkv, d]
+            tail = [C.c_float(scale), C.c_float(0.0), 0, 1, split, C.c_void_p(sc.ptr) if sc else None]
+            if at:
+                nd = _dev_i64(n_dev)
+                X.call("xs_hip_attention_at", None, *head, cap, C.c_void_p(nd.ptr), *tail)
+            else:
+                X.call("xs_hip_attention", None, *head, n, *tail)
+            X.synchronize()
+            outs.append(out.numpy())
+        assert_exact(outs[1], outs[0], f"T{t} n{n}")
 
 
 def test_attention_i8_cache_beyond_2gib():

@@ -1,7 +1,7 @@
 """The HIP backend (xs::Backend "hip" and its Session) on step graphs.
 
-CPU tests: the graph builders' checks and the backend's refusals (ops it has no kernel for, float KV caches, KV
-values read by anything but attention), which come before any device work. GPU tests: graphs of the path's ops run
+CPU tests: the graph builders' checks and the backend's refusals (ops it has no kernel for, KV formats and
+precisions it does not take, KV values read by anything but attention), which come before any device work. GPU tests: graphs of the path's ops run
 through Session::run and compared with the oracle (oracle/oracle.cpp, the restatement of cpu-ref) evaluating the same
 nodes one by one in graph order -- each fused launch must equal the unfused nodes (f32 within 1e-5 relative, exact
 where the ops are), the int8 KV cache across steps must give what cpu-ref's cache of round-tripped rows gives (the
@@ -115,9 +115,11 @@ def _kv_graph(extra=None):
     return g
 
 
-def test_refuses_float_kv_cache():
-    _refusal(_kv_graph(), "KV cache format", kv=(S.KV_FLOAT, S.KV_FLOAT))
-    _refusal(_kv_graph(), "KV cache format", kv=(S.KV_I8, S.KV_FLOAT))
+def test_refuses_unsupported_kv_formats_and_precisions():
+    _refusal(_kv_graph(), "KV cache format i8:auto", kv=(S.KV_I8, S.KV_FLOAT))
+    _refusal(_kv_graph(), "KV cache format turbo4", kv=(S.KV_TURBO4, S.KV_TURBO4))
+    with pytest.raises(S.BackendError, match="precision must be f16 or f32, got bf16"):
+        S.Session(_kv_graph(), kv=(S.KV_FLOAT, S.KV_FLOAT), precision=S.BF16)
 
 
 def test_refuses_kv_values_outside_attention():
@@ -395,6 +397,116 @@ def test_kv_decode_steps(ora, hq, hkv, d, window, softcap):
     one(4)
 
 
+class _FloatCache:
+    """The Float KV format's rows: cpu-ref keeps the f32 rows (quant::round_trip_kv leaves Float rows as they are,
+    kv_format.cpp:57-61); a device at f16 precision stores them as f16 (the SYCL session's to_half,
+    sycl_backend.cpp:2224-2228). `f16`: what the f16 rows hold (each value rounded to f16, RNE)."""
+
+    def __init__(self, ora, hkv, d, f16):
+        self.ora, self.f16 = ora, f16
+        self.k, self.v = np.zeros((0, hkv, d), np.float32), np.zeros((0, hkv, d), np.float32)
+        self.k32, self.v32 = self.k, self.v
+
+    def rt(self, x):
+        return self.ora.widen(self.ora.narrow(x, S.F16), S.F16) if self.f16 else x
+
+    def append(self, k, v):
+        self.k = np.concatenate([self.k, self.rt(k)])
+        self.v = np.concatenate([self.v, self.rt(v)])
+        self.k32 = np.concatenate([self.k32, k])
+        self.v32 = np.concatenate([self.v32, v])
+
+    def truncate(self, n):
+        self.k, self.v, self.k32, self.v32 = self.k[:n], self.v[:n], self.k32[:n], self.v32[:n]
+
+
+# The reference's device bar for attention at f16 precision (tests/unit/backend/device_attention.cpp:23).
+F16_ATOL, F16_RTOL = 4e-3, 4e-3
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("precision", [S.F16, S.F32])
+@pytest.mark.parametrize("hq,hkv,d,window,softcap", [(32, 8, 128, 0, 0.0), (12, 4, 64, 5, 0.0), (4, 1, 256, 0, 30.0)])
+def test_float_kv_decode_steps(ora, precision, hq, hkv, d, window, softcap):
+    """The Float KV format -- the reference's default SessionOptions (precision f16, kv auto) and f32 precision: a
+    prefill, decode steps, a KvRead program, truncate and reset. Against the oracle over the rows the cache holds
+    (f16-rounded at f16 precision, the f32 rows at f32) at the reference's f32 device bar, and at f16 precision also
+    against cpu-ref's own cache of f32 rows at the reference's f16 device bar."""
+    rng = np.random.default_rng(16 + d)
+    prefill, reader = _kv_programs(hq, hkv, d, window, softcap)
+    f16 = precision == S.F16
+    step(f"session float kv ({'f16' if f16 else 'f32'} rows) H{hq}/{hkv} D{d} w{window} cap{softcap}")
+    s = S.Session([prefill, reader], max_context=64, kv=(S.KV_FLOAT, S.KV_FLOAT), precision=precision)
+    cache = _FloatCache(ora, hkv, d, f16)
+    scale = 1 / math.sqrt(d)
+
+    def one(tokens, program=0):
+        q = rng.standard_normal((tokens, hq, d)).astype(np.float32)
+        inputs = {"q": (q, S.F32)}
+        if program == 0:
+            k = rng.standard_normal((tokens, hkv, d)).astype(np.float32)
+            v = rng.standard_normal((tokens, hkv, d)).astype(np.float32)
+            inputs.update({"k": (k, S.F32), "v": (v, S.F32)})
+            cache.append(k, v)
+        o = s.run(inputs, program=program)["o"]
+        what = f"program {program}, {tokens} tokens at L {len(cache.k)}"
+        attention_close(o, ora.attention(q, cache.k, cache.v, scale, softcap, window, True), what)
+        if f16:
+            attention_close(o, ora.attention(q, cache.k32, cache.v32, scale, softcap, window, True),
+                            what + " (cpu-ref's f32 rows)", atol=F16_ATOL, rtol=F16_RTOL)
+
+    one(7)
+    for _ in range(3):
+        one(1)
+    one(2, program=1)
+    s.truncate(6)
+    cache.truncate(6)
+    one(1)
+    one(3)
+    assert s.num_cached() == 10
+    s.reset()
+    cache.truncate(0)
+    one(4)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("graphs", ["1", "0"])
+def test_float_kv_many_steps(ora, graphs):
+    """Forty decode steps over the f16-row cache with the repeated steps replayed from captured graphs (the append's
+    row and the attention's key count read from the device step record) or launched one by one."""
+    hq, hkv, d = 8, 2, 128
+    rng = np.random.default_rng(97)
+    prefill, reader = _kv_programs(hq, hkv, d)
+    step(f"session float kv 40 steps graphs={graphs}")
+    s = S.Session([prefill, reader], max_context=64, kv=(S.KV_FLOAT, S.KV_FLOAT), precision=S.F16,
+                  options={"graphs": graphs})
+    cache = _FloatCache(ora, hkv, d, True)
+    scale = 1 / math.sqrt(d)
+
+    def one(tokens, program=0):
+        q = rng.standard_normal((tokens, hq, d)).astype(np.float32)
+        inputs = {"q": (q, S.F32)}
+        if program == 0:
+            k = rng.standard_normal((tokens, hkv, d)).astype(np.float32)
+            v = rng.standard_normal((tokens, hkv, d)).astype(np.float32)
+            inputs.update({"k": (k, S.F32), "v": (v, S.F32)})
+            cache.append(k, v)
+        o = s.run(inputs, program=program)["o"]
+        attention_close(o, ora.attention(q, cache.k, cache.v, scale, 0.0, 0, True),
+                        f"graphs={graphs} program {program}, {tokens} tokens at L {len(cache.k)}")
+
+    one(8)
+    for i in range(40):
+        one(1)
+        if i % 9 == 4:
+            one(1, program=1)
+    s.truncate(20)
+    cache.truncate(20)
+    for _ in range(5):
+        one(1)
+    assert s.num_cached() == 25
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("graphs", ["1", "0"])
 def test_kv_decode_many_steps(ora, graphs):
@@ -492,6 +604,73 @@ def test_decoder_steps_replayed_match_eager():
         attention_close(a, b, f"decode step {i}", atol=1e-4, rtol=1e-3)
     print(f"[session] 8-layer decode step (Session::run timed in C++): {t_on:.1f} us with graph replay, {t_off:.1f} us "
           f"launched one by one", flush=True)
+
+
+@pytest.mark.gpu
+def test_decoder_under_default_options(ora):
+    """The decoder-shaped graph (2 layers: residual add + RMSNorm, the Q and K RoPE pair, the KV append, attention, the
+    gated multiply) under the reference's default SessionOptions -- precision f16, the Float KV format, so f16 rows --
+    for a prefill and decode steps, replayed from captured graphs. Every step against the oracle evaluating the same
+    nodes in graph order over the rows the cache holds (f16-rounded), and against cpu-ref's f32 rows at the
+    reference's f16 device bar."""
+    hq, hkv, d, layers = 8, 2, 64, 2
+    hid = hq * d
+    rng = np.random.default_rng(98)
+    nw = (1 + 0.1 * rng.standard_normal(hid)).astype(np.float32)
+    inv = (1.0 / (1e6 ** (np.arange(0, d, 2) / d))).astype(np.float32)
+    w = S.Weights()
+    w.add("norm", nw)
+    w.add("inv", inv)
+    g = S.Graph()
+    x = g.input("x", S.F32, [S.T, hid])
+    r = g.input("r", S.F32, [S.T, hid])
+    pos = g.input("pos", S.I64, [S.T])
+    nwv, fi = g.weight(w, "norm"), g.weight(w, "inv")
+    for layer in range(layers):
+        h = g.add(x, r)
+        n = g.rms_norm(h, nwv)
+        qr = g.rope(g.reshape(n, [S.T, hq, d]), pos, fi)
+        k = g.reshape(g.slice(n, 1, 0, hkv * d), [S.T, hkv, d])
+        ka, va = g.kv_cache(g.kv_slot(hkv, d, 0, label=f"l{layer}"), g.rope(k, pos, fi), k)
+        x = g.mul(g.silu(g.reshape(g.attention(qr, ka, va, 1 / math.sqrt(d)), [S.T, hid])), n)
+        r = h
+    g.output("x", x)
+    step("session decoder under default options (f16 precision, float KV)")
+    s = S.Session(g, w, max_context=128, kv=(S.KV_FLOAT, S.KV_FLOAT), precision=S.F16)
+    caches = [_FloatCache(ora, hkv, d, True) for _ in range(layers)]
+
+    def oracle_step(xv, rv, pv, rows):
+        xo = xv
+        for layer in range(layers):
+            h = ora.binary(0, xo, rv)
+            nn = ora.rms_norm(h, nw, 1e-6)
+            qq = ora.rope(nn.reshape(-1, hq, d), pv, inv)
+            kk = nn[:, : hkv * d].reshape(-1, hkv, d)
+            kr = ora.rope(kk, pv, inv)
+            c = caches[layer]
+            if rows == "held":
+                c.append(kr, kk)
+                ks, vs = c.k, c.v
+            else:
+                ks, vs = c.k32, c.v32
+            att = ora.attention(qq, ks, vs, 1 / math.sqrt(d))
+            xo = ora.binary(1, ora.unary(SILU, att.reshape(-1, hid)), nn)
+            rv = h
+        return xo
+
+    feed = np.random.default_rng(99)
+    p0 = 0
+    for t in [12] + [1] * 8:
+        xv = feed.standard_normal((t, hid)).astype(np.float32)
+        rv = feed.standard_normal((t, hid)).astype(np.float32)
+        pv = np.arange(p0, p0 + t).astype(np.int64)
+        got = s.run({"x": (xv, S.F32), "r": (rv, S.F32), "pos": (pv, S.I64)})["x"]
+        want = oracle_step(xv, rv, pv, "held")
+        attention_close(got, want, f"decoder step at {p0} ({t} tokens)", atol=1e-4, rtol=1e-3)
+        attention_close(got, oracle_step(xv, rv, pv, "f32"), f"decoder step at {p0} vs cpu-ref's f32 rows",
+                        atol=F16_ATOL, rtol=F16_RTOL)
+        p0 += t
+    assert s.num_cached() == p0
 
 
 @pytest.mark.gpu

@@ -591,6 +591,200 @@ __global__ __launch_bounds__(256) void attention_combine_rows(const float* part,
     }
 }
 
+// ---- Decode attention over a float cache (f16 or f32 rows) --------------------------------------------------------
+//
+// The reader of the float KV format (SessionOptions::kv Float: f16 rows at f16 precision, f32 at f32; reference
+// src/quant/kv_format.h:12, sycl_backend.cpp:2224-2228): keys and values [N, Hkv, D] of T. Semantics as the int8
+// reader above over the values the rows hold. Launcher replaced: sycl_be::attention_rows<KV> with attention_combine
+// (src/backend/sycl/sycl_kernels.h, attention_rows / attention_combine), KV = half or float.
+//
+// Layout: one 256-thread workgroup per (token, KV head, key split), for all G query heads of that KV head, so each key
+// and value row is read once for them. The split's keys go in tiles of 256: thread i scores key i of the tile for the
+// G heads (its row's dot products with q, which sits in LDS, f32 fused multiply-adds), the tile's max and sum of
+// exponentials per head come from wave reductions and one LDS stage, and the weighted sum runs with thread t holding
+// four dims of every head over the tile's keys t / (D / 4) + k (1024 / D), k = 0, 1, ...: the value rows' loads of a
+// wave cover whole rows. One online softmax per head; the partial sums of the 1024 / D key subsets add up in LDS at the
+// end. With one split the workgroup writes the output; with several, partial rows as the int8 reader writes them.
+constexpr int kFloatTile = 256;
+
+template <typename KV, int G, int D, bool CAP>
+__global__ __launch_bounds__(256) void attention_float_rows(AttnArgs a, const void* kp, const void* vp) {
+    constexpr int kS = 1024 / D;   // key subsets of the weighted sum
+    constexpr int kD4 = D / 4;     // 4-dim groups a row
+    constexpr int kEl = 16 / sizeof(typename KV::storage);  // elements of one 128-bit load
+    __shared__ __align__(16) float q_s[G][D];
+    __shared__ float p_s[G][kFloatTile];
+    __shared__ float red[2][4][G];
+    __shared__ __align__(16) float acc_s[kS][G][D];
+    const auto* kr = static_cast<const typename KV::storage*>(kp);
+    const auto* vr = static_cast<const typename KV::storage*>(vp);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t t = blockIdx.y / a.kv_heads;
+    const int64_t kvh = blockIdx.y - t * a.kv_heads;
+    const int sp = blockIdx.x;
+
+    for (int i = tid; i < G * D; i += 256) q_s[i / D][i % D] = a.q[(t * a.q_heads + kvh * G + i / D) * D + i % D];
+
+    int64_t first, last;
+    key_range(a, keys_of(a), t, first, last);
+    const int64_t len = last >= first ? last - first + 1 : 0;
+    const int64_t per = (len + a.split - 1) / a.split;
+    const int64_t k0 = first + sp * per;
+    const int64_t k1 = k0 + per - 1 < last ? k0 + per - 1 : last;
+    float m[G], l[G], acc[G][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[g][e] = 0.0f;
+    }
+    const int dg = tid % kD4, sub = tid / kD4;
+    __syncthreads();
+    for (int64_t j0 = k0; j0 <= k1; j0 += kFloatTile) {
+        // Scores of key j0 + tid for every head.
+        const int64_t j = j0 + tid;
+        float s[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) s[g] = 0.0f;
+        if (j <= k1) {
+            const auto* row = kr + (j * a.kv_heads + kvh) * D;
+#pragma unroll 4
+            for (int c = 0; c < D; c += kEl) {
+                float kf[kEl];
+                unpack<KV>(ld128(row + c), kf);
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+#pragma unroll
+                    for (int e = 0; e < kEl; ++e) s[g] = fmaf(q_s[g][c + e], kf[e], s[g]);
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float x = s[g] * a.scale;
+                if constexpr (CAP) x = a.softcap * tanhf(x / a.softcap);
+                s[g] = x;
+            }
+        } else {
+#pragma unroll
+            for (int g = 0; g < G; ++g) s[g] = -INFINITY;
+        }
+        // The tile's max per head, then exponentials and their sum.
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float w = wave_reduce<OpMax>(s[g], -INFINITY);
+            if (lane == 0) red[0][wave][g] = w;
+        }
+        __syncthreads();
+        float c[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float mt = fmaxf(fmaxf(red[0][0][g], red[0][1][g]), fmaxf(red[0][2][g], red[0][3][g]));
+            const float mn = fmaxf(m[g], mt);
+            c[g] = m[g] == -INFINITY ? 0.0f : __expf(m[g] - mn);
+            m[g] = mn;
+            const float p = s[g] == -INFINITY ? 0.0f : __expf(s[g] - mn);
+            p_s[g][tid] = p;
+            const float w = wave_reduce<OpSum>(p, 0.0f);
+            if (lane == 0) red[1][wave][g] = w;
+        }
+        __syncthreads();
+        // The weighted sum of the tile's value rows.
+        const int64_t n = k1 - j0 + 1 < kFloatTile ? k1 - j0 + 1 : kFloatTile;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            l[g] = l[g] * c[g] + ((red[1][0][g] + red[1][1][g]) + (red[1][2][g] + red[1][3][g]));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[g][e] *= c[g];
+        }
+        for (int k = sub; k < n; k += kS) {
+            const auto* row = vr + ((j0 + k) * a.kv_heads + kvh) * D + 4 * dg;
+            float vf[4];
+            if constexpr (sizeof(typename KV::storage) == 4) {
+                unpack<KV>(ld128(row), vf);
+            } else {
+                const uint2 w2 = *reinterpret_cast<const uint2*>(row);
+                vf[0] = KV::load(static_cast<uint16_t>(w2.x & 0xffffu));
+                vf[1] = KV::load(static_cast<uint16_t>(w2.x >> 16));
+                vf[2] = KV::load(static_cast<uint16_t>(w2.y & 0xffffu));
+                vf[3] = KV::load(static_cast<uint16_t>(w2.y >> 16));
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float p = p_s[g][k];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
+            }
+        }
+        __syncthreads();  // p_s and red are rewritten by the next tile
+    }
+    // The key subsets' sums add up; then the output, or the partial row with its (max, sum).
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+        *reinterpret_cast<u32x4*>(&acc_s[sub][g][4 * dg]) =
+            u32x4{__float_as_uint(acc[g][0]), __float_as_uint(acc[g][1]), __float_as_uint(acc[g][2]),
+                  __float_as_uint(acc[g][3])};
+    __syncthreads();
+    for (int i = tid; i < G * D; i += 256) {
+        const int g = i / D, d = i % D;
+        float sum = 0.0f;
+#pragma unroll
+        for (int q = 0; q < kS; ++q) sum += acc_s[q][g][d];
+        const int64_t hh = kvh * G + g;
+        if (a.part == nullptr) {
+            a.out[(t * a.q_heads + hh) * D + d] = sum / l[g];
+        } else {
+            const int64_t pi = (t * a.q_heads + hh) * a.split + sp;
+            a.part[pi * D + d] = sum;
+            if (d == 0) {
+                float* ml = a.part + a.tokens * a.q_heads * a.split * D + 2 * pi;
+                ml[0] = m[g];
+                ml[1] = l[g];
+            }
+        }
+    }
+}
+
+template <typename KV, int G>
+int launch_float_g(hipStream_t s, const AttnArgs& a, const void* k, const void* v) {
+    const dim3 grid(static_cast<unsigned>(a.split), static_cast<unsigned>(a.tokens * a.kv_heads));
+    const bool cap = a.softcap > 0.0f;
+    switch (a.head_dim) {
+        case 64:
+            if (cap) attention_float_rows<KV, G, 64, true><<<grid, 256, 0, s>>>(a, k, v);
+            else attention_float_rows<KV, G, 64, false><<<grid, 256, 0, s>>>(a, k, v);
+            break;
+        case 128:
+            if (cap) attention_float_rows<KV, G, 128, true><<<grid, 256, 0, s>>>(a, k, v);
+            else attention_float_rows<KV, G, 128, false><<<grid, 256, 0, s>>>(a, k, v);
+            break;
+        case 256:
+            if (cap) attention_float_rows<KV, G, 256, true><<<grid, 256, 0, s>>>(a, k, v);
+            else attention_float_rows<KV, G, 256, false><<<grid, 256, 0, s>>>(a, k, v);
+            break;
+        default:
+            return fail(XS_HIP_EUNSUPPORTED, "xs_hip_attention: head_dim " + std::to_string(a.head_dim) +
+                                                 " (supported: 64, 128, 256)");
+    }
+    return check_launch("xs_hip_attention");
+}
+
+template <typename KV>
+int launch_float(hipStream_t s, const AttnArgs& a, const void* k, const void* v) {
+    switch (a.q_heads / a.kv_heads) {
+        case 1: return launch_float_g<KV, 1>(s, a, k, v);
+        case 2: return launch_float_g<KV, 2>(s, a, k, v);
+        case 3: return launch_float_g<KV, 3>(s, a, k, v);
+        case 4: return launch_float_g<KV, 4>(s, a, k, v);
+        case 5: return launch_float_g<KV, 5>(s, a, k, v);
+        case 6: return launch_float_g<KV, 6>(s, a, k, v);
+        case 7: return launch_float_g<KV, 7>(s, a, k, v);
+        case 8: return launch_float_g<KV, 8>(s, a, k, v);
+        default:
+            return fail(XS_HIP_EUNSUPPORTED, "xs_hip_attention: " + std::to_string(a.q_heads / a.kv_heads) +
+                                                 " query heads per KV head (supported: 1 to 8)");
+    }
+}
+
 // KV heads a workgroup of `waves` waves: the largest power of two up to `waves` dividing kv_heads.
 int heads_per_group(int64_t kv_heads, int waves) {
     int hg = waves;
@@ -743,9 +937,67 @@ int noalloc_scratch(void** out, const char* what) {
     return XS_HIP_OK;
 }
 
+// Both float entry points: as attention_i8, over rows of kv_dtype (F16 or F32).
+int attention_float(void* stream, xs_dtype kv_dtype, const float* q, const void* k, const void* v, float* out,
+                    int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t kv_len,
+                    const int64_t* kv_len_dev, float scale, float softcap, int64_t window, int causal, int64_t split,
+                    void* scratch, const char* what) {
+    if (tokens < 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || kv_len < 0 || window < 0 || split < 1 ||
+        q_heads % kv_heads != 0)
+        return fail(XS_HIP_EINVAL, std::string(what) + ": q [" + std::to_string(tokens) + ", " +
+                                       std::to_string(q_heads) + ", " + std::to_string(head_dim) + "] over " +
+                                       std::to_string(kv_len) + " keys of " + std::to_string(kv_heads) +
+                                       " KV heads, split " + std::to_string(split));
+    if (kv_dtype != XS_F16 && kv_dtype != XS_F32)
+        return fail(XS_HIP_EUNSUPPORTED, std::string(what) + ": key and value rows of " + dtype_name(kv_dtype) +
+                                             " (supported: f16, f32)");
+    if (tokens == 0) return XS_HIP_OK;
+    if ((causal || window > 0) && kv_len < tokens)
+        return fail(XS_HIP_EINVAL, std::string(what) + ": " + std::to_string(kv_len) + " keys for " +
+                                       std::to_string(tokens) + " queries");
+    if (kv_len == 0) return fail(XS_HIP_EINVAL, std::string(what) + ": no keys");
+    if (q == nullptr || k == nullptr || v == nullptr || out == nullptr)
+        return fail(XS_HIP_EINVAL, std::string(what) + ": null buffer");
+    if (split > 1 && scratch == nullptr)
+        return fail(XS_HIP_EINVAL, std::string(what) + ": split " + std::to_string(split) +
+                                       " needs xs_hip_attention_i8_scratch bytes of scratch");
+    if (split > kMaxSplit || tokens * kv_heads > 65535)
+        return fail(XS_HIP_EUNSUPPORTED, std::string(what) + ": launch too large");
+    if (!aligned16(q) || !aligned16(out) || !aligned16(k) || !aligned16(v) || head_dim % 16 != 0 ||
+        (split > 1 && reinterpret_cast<uintptr_t>(scratch) % 16 != 0))
+        return fail(XS_HIP_EINVAL, std::string(what) + ": q, out, keys, values and scratch must be 16-byte aligned "
+                                                       "and head_dim a multiple of 16");
+    AttnArgs a{q, nullptr, nullptr, nullptr, nullptr, out, split > 1 ? static_cast<float*>(scratch) : nullptr, tokens,
+               q_heads, kv_heads, head_dim, kv_len, window, scale, softcap, causal ? 1 : 0, static_cast<int>(split), 1,
+               kv_len_dev};
+    const hipStream_t s = as_stream(stream);
+    const int rc = kv_dtype == XS_F16 ? launch_float<F16>(s, a, k, v) : launch_float<F32>(s, a, k, v);
+    if (rc != XS_HIP_OK || split == 1) return rc;
+    attention_combine_rows<<<static_cast<unsigned>(tokens * q_heads * (head_dim / kCombineDims)), 256, 0, s>>>(
+        static_cast<const float*>(scratch), out, static_cast<int>(split), head_dim, tokens * q_heads);
+    return check_launch(what);
+}
+
 }  // namespace
 
 extern "C" {
+
+int xs_hip_attention(void* stream, xs_dtype kv_dtype, const float* q, const void* k, const void* v, float* out,
+                     int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t kv_len, float scale,
+                     float softcap, int64_t window, int causal, int64_t split, void* scratch) {
+    return attention_float(stream, kv_dtype, q, k, v, out, tokens, q_heads, kv_heads, head_dim, kv_len, nullptr, scale,
+                           softcap, window, causal, split, scratch, "xs_hip_attention");
+}
+
+int xs_hip_attention_at(void* stream, xs_dtype kv_dtype, const float* q, const void* k, const void* v, float* out,
+                        int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t kv_capacity,
+                        const int64_t* kv_len, float scale, float softcap, int64_t window, int causal, int64_t split,
+                        void* scratch) {
+    if (kv_len == nullptr || reinterpret_cast<uintptr_t>(kv_len) % 8 != 0)
+        return fail(XS_HIP_EINVAL, "xs_hip_attention_at: kv_len must be an 8-byte aligned device int64");
+    return attention_float(stream, kv_dtype, q, k, v, out, tokens, q_heads, kv_heads, head_dim, kv_capacity, kv_len,
+                           scale, softcap, window, causal, split, scratch, "xs_hip_attention_at");
+}
 
 int xs_hip_attention_i8(void* stream, const float* q, const void* k_codes, const void* k_scales, const void* v_codes,
                         const void* v_scales, float* out, int64_t tokens, int64_t q_heads, int64_t kv_heads,

@@ -41,6 +41,15 @@ __device__ __forceinline__ uint32_t code_bits(float x, float inv) {
     return __float_as_uint(x * inv + 12582912.0f);
 }
 
+// code_bits for a row whose 127 / amax overflowed to inf (0 < amax < 127 / FLT_MAX, which only f32 and bf16 inputs
+// reach): x * inv is then +-inf for a nonzero x, which the reference's clamp takes to +-127, and NaN for 0 (code 0);
+// the scalar form gives exactly that. `huge` is uniform over a row.
+template <typename T>
+__device__ __forceinline__ uint32_t row_code(float x, float inv, bool huge) {
+    if constexpr (T::dtype == XS_F16) return code_bits(x, inv);  // |x| >= 2^-24: 127 / amax is finite
+    return huge ? static_cast<uint32_t>(quantize_code(x, inv)) : code_bits(x, inv);
+}
+
 // The low bytes of four words, packed in order into one word.
 __device__ __forceinline__ uint32_t pack_low_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);  // a.b0 | b.b0 << 8
@@ -128,15 +137,18 @@ __global__ __launch_bounds__(kQBlock) void quantize_i8_vec(const typename T::sto
                 for (int i = 0; i < VEC; ++i) amax = fmaxf(amax, fabsf(f[k][i]));
             amax = group_reduce<L, OpMax>(amax);
             const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+            const bool huge = inv > 3.40282347e38f;
             if (r < rows) {
 #pragma unroll
                 for (int k = 0; k < VPL; ++k) {
                     int8_t* out = codes + r * width + (l + k * L) * VEC;
-                    const uint32_t w0 = pack_low_bytes(code_bits(f[k][0], inv), code_bits(f[k][1], inv),
-                                                       code_bits(f[k][2], inv), code_bits(f[k][3], inv));
+                    const uint32_t w0 =
+                        pack_low_bytes(row_code<T>(f[k][0], inv, huge), row_code<T>(f[k][1], inv, huge),
+                                       row_code<T>(f[k][2], inv, huge), row_code<T>(f[k][3], inv, huge));
                     if constexpr (VEC == 8) {
-                        const uint32_t w1 = pack_low_bytes(code_bits(f[k][4], inv), code_bits(f[k][5], inv),
-                                                           code_bits(f[k][6], inv), code_bits(f[k][7], inv));
+                        const uint32_t w1 =
+                            pack_low_bytes(row_code<T>(f[k][4], inv, huge), row_code<T>(f[k][5], inv, huge),
+                                           row_code<T>(f[k][6], inv, huge), row_code<T>(f[k][7], inv, huge));
                         typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
                         __builtin_nontemporal_store(u32x2{w0, w1}, reinterpret_cast<u32x2*>(out));
                     } else {
@@ -327,6 +339,67 @@ int quantize_i8(void* stream, xs_dtype x_dtype, const void* x, void* codes, void
     }
 }
 
+// ---- The float KV format: a step's keys and values appended as rows of the cache's float type -------------------
+//
+// The Float format stores each appended row as the precision's float (quant::round_trip_kv leaves it as is:
+// src/quant/kv_format.cpp:57-61): f16 rows at f16 precision (the SYCL session's to_half, sycl_backend.cpp:2224-2228,
+// RNE), f32 rows at f32. One launch writes keys and values: unit u of 8 elements (or one element, off the vector path)
+// of row r goes to row `first` + r of its cache, `first` = row0[0] * unit rows when the destination is read from
+// device memory (a step replayed from a captured graph), rows past the cache written nowhere.
+template <typename XT, typename YT, bool VEC>
+__global__ __launch_bounds__(256) void kv_store_rows(const void* k, const void* v, void* ky, void* vy, int64_t rows,
+                                                     int64_t width, QuantDest dest) {
+    int64_t first = 0, limit = rows;
+    if (dest.row0 != nullptr) {
+        first = dest.row0[0] * dest.unit;
+        limit = first < 0 ? 0 : (dest.cap - first < rows ? dest.cap - first : rows);
+    }
+    const int64_t per = VEC ? 8 : 1;
+    const int64_t units = limit > 0 ? limit * (width / per) : 0;
+    const int64_t total = v != nullptr ? 2 * units : units;  // no values: keys only
+    for (int64_t u = blockIdx.x * 256 + threadIdx.x; u < total; u += static_cast<int64_t>(gridDim.x) * 256) {
+        const bool is_v = u >= units;
+        const int64_t e = (is_v ? u - units : u) * per;  // element of the step's [rows, width]
+        const auto* x = static_cast<const typename XT::storage*>(is_v ? v : k) + e;
+        auto* y = static_cast<typename YT::storage*>(is_v ? vy : ky) + first * width + e;
+        if constexpr (VEC) {
+            float f[8];
+            if constexpr (sizeof(typename XT::storage) == 4) {
+                unpack<XT>(ld128(x), f);
+                unpack<XT>(ld128(x + 4), f + 4);
+            } else {
+                unpack<XT>(ld128(x), f);
+            }
+            if constexpr (sizeof(typename YT::storage) == 4) {
+                st128(y, pack<YT>(f));
+                st128(y + 4, pack<YT>(f + 4));
+            } else {
+                st128(y, pack<YT>(f));
+            }
+        } else {
+            *y = YT::store(XT::load(*x));
+        }
+    }
+}
+
+template <typename XT, typename YT>
+int launch_kv_store(hipStream_t s, const void* k, const void* v, void* ky, void* vy, int64_t rows, int64_t width,
+                    const QuantDest& dest, const char* what) {
+    const bool vec = width % 8 == 0 && aligned16(k) && aligned16(v) && aligned16(ky) && aligned16(vy);  // null: aligned
+    const int64_t units = 2 * rows * (vec ? width / 8 : width);
+    const unsigned grid = grid_for(units, 256);
+    if (vec) kv_store_rows<XT, YT, true><<<grid, 256, 0, s>>>(k, v, ky, vy, rows, width, dest);
+    else kv_store_rows<XT, YT, false><<<grid, 256, 0, s>>>(k, v, ky, vy, rows, width, dest);
+    return check_launch(what);
+}
+
+template <typename XT>
+int kv_store_from(hipStream_t s, xs_dtype row_dtype, const void* k, const void* v, void* ky, void* vy, int64_t rows,
+                  int64_t width, const QuantDest& dest, const char* what) {
+    if (row_dtype == XS_F16) return launch_kv_store<XT, F16>(s, k, v, ky, vy, rows, width, dest, what);
+    return launch_kv_store<XT, F32>(s, k, v, ky, vy, rows, width, dest, what);
+}
+
 }  // namespace
 }  // namespace xs_hip
 
@@ -410,6 +483,31 @@ int xs_hip_dequantize_kv(void* stream, xs_kv_format format, const void* codes, c
         default:
             return fail(XS_HIP_EINVAL, std::string("xs_hip_dequantize_kv: out must be f32, f16 or bf16, got ") +
                                            dtype_name(out_dtype));
+    }
+}
+
+int xs_hip_kv_store_pair(void* stream, xs_dtype x_dtype, const void* k, const void* v, xs_dtype row_dtype,
+                         void* k_rows, void* v_rows, int64_t rows, int64_t width, const int64_t* row0,
+                         int64_t rows_per_unit, int64_t capacity_rows) {
+    const char* what = "xs_hip_kv_store_pair";
+    if (rows < 0 || width <= 0 || (row0 != nullptr && (rows_per_unit < 0 || capacity_rows < 0)))
+        return fail(XS_HIP_EINVAL, std::string(what) + ": rows " + std::to_string(rows) + " of width " +
+                                       std::to_string(width) + ", " + std::to_string(rows_per_unit) +
+                                       " rows a unit, capacity " + std::to_string(capacity_rows));
+    if (!is_float_dtype(x_dtype) || (row_dtype != XS_F16 && row_dtype != XS_F32))
+        return fail(XS_HIP_EUNSUPPORTED, std::string(what) + ": " + dtype_name(x_dtype) + " rows into a cache of " +
+                                             dtype_name(row_dtype) + " (inputs f32, f16 or bf16; cache f16 or f32)");
+    if (rows == 0) return XS_HIP_OK;
+    if (k == nullptr || k_rows == nullptr || (v == nullptr) != (v_rows == nullptr))
+        return fail(XS_HIP_EINVAL, std::string(what) + ": null buffer");
+    if (reinterpret_cast<uintptr_t>(row0) % 8 != 0)
+        return fail(XS_HIP_EINVAL, std::string(what) + ": row0 must be 8-byte aligned");
+    const QuantDest dest = row0 != nullptr ? QuantDest{row0, rows_per_unit, capacity_rows} : QuantDest{};
+    const hipStream_t s = as_stream(stream);
+    switch (x_dtype) {
+        case XS_F32: return kv_store_from<F32>(s, row_dtype, k, v, k_rows, v_rows, rows, width, dest, what);
+        case XS_F16: return kv_store_from<F16>(s, row_dtype, k, v, k_rows, v_rows, rows, width, dest, what);
+        default: return kv_store_from<BF16>(s, row_dtype, k, v, k_rows, v_rows, rows, width, dest, what);
     }
 }
 

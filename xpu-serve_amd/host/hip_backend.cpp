@@ -33,10 +33,14 @@
 //  - a KvCache's keys and values, of one dtype: one quantize launch (no reference counterpart).
 // Reshape is a view; Slice is a view when it keeps whole leading rows or only an act-bias-mul reads it, else a copy.
 //
-// What it refuses: MatMul and the other ops with no kernel here (the GEMM path is outside this library), float KV
-// caches (the cache is int8: SessionOptions::kv must be i8 for keys and values), KV outputs read by anything but
-// Attention, and attention with a key bias, groups, blocks, relative bias or an anchored window. Activations are
-// computed and kept in f32 whatever SessionOptions::precision asks (the f32 semantics of cpu-ref).
+// KV formats (SessionOptions::kv): i8 keys and values (int8 codes and f32 scales), or the Float format -- rows of the
+// precision's float (f16 at f16 precision, the reference's default; f32 at f32), as the SYCL session stores them.
+// SessionOptions::precision is f16 or f32, as for cpu-ref (cpu_backend.cpp:75-76), and as there the activations are
+// computed and kept in f32 either way (cpu_backend.cpp:611); the precision picks the Float format's row type.
+//
+// What it refuses: MatMul and the other ops with no kernel here (the GEMM path is outside this library), a precision
+// other than f16 or f32, the TurboQuant KV formats and mixed key/value formats, KV outputs read by anything but
+// Attention, and attention with a key bias, groups, blocks, relative bias or an anchored window.
 #include <algorithm>
 #include <cstring>
 #include <limits>
@@ -221,7 +225,10 @@ struct Loc {
 struct KvState {
     int64_t heads = 0, dim = 0, cap = 0;
     int64_t len = 0;
-    DeviceMemory kc, ks, vc, vs;  // codes int8 [cap, heads, dim], scales f32 [cap, heads]
+    // What the slot stores (SessionOptions::kv): I8 -- codes int8 [cap, heads, dim] in kc / vc and scales f32
+    // [cap, heads] in ks / vs; or the Float format's rows [cap, heads, dim] of F16 (f16 precision) or F32 in kc / vc.
+    DType rows = DType::I8;
+    DeviceMemory kc, ks, vc, vs;
     std::string label;
 };
 
@@ -367,6 +374,7 @@ public:
         k.dim = s.head_dim;
         k.cap = options_.max_context;
         k.label = s.label;
+        k.rows = options_.kv.k == quant::KvFormat::I8 ? DType::I8 : options_.precision;
         kv_.push_back(std::move(k));
         return static_cast<int>(kv_.size() - 1);
     }
@@ -513,21 +521,21 @@ Program::Program(const Graph& g, HipSession& s, size_t index) : g_(g), s_(s), in
                      "softmax, top-k, reduce, RoPE, int8 KV cache and attention ops)");
         }
     }
-    // KV outputs feed attention only; the slots are int8.
+    // KV outputs feed attention only: the slots hold the cache's own format (int8 codes, or f16 / f32 rows).
     for (size_t i = 0; i < n; ++i) {
         if (nodes[i].kind != OpKind::KvCache && nodes[i].kind != OpKind::KvRead) continue;
         for (size_t r : reader_nodes[i]) {
             XS_CHECK(nodes[r].kind == OpKind::Attention, "hip: ", where(i), " is read by ", where(r),
-                     "; the int8 KV cache is read only by attention on this backend");
+                     "; the KV cache is read only by attention on this backend");
         }
         for (const auto& o : g_.outputs())
             XS_CHECK(static_cast<size_t>(o.value.node) != i, "hip: graph output '", o.name, "' is a KV cache");
     }
     if (!g_.kv_slots().empty()) {
         const auto& kv = s_.options().kv;
-        XS_CHECK(kv.k == quant::KvFormat::I8 && kv.v == quant::KvFormat::I8, "hip: the KV cache format ",
-                 quant::kv_format_name(kv.k), ":", quant::kv_format_name(kv.v),
-                 " is not supported; this backend stores i8 keys and values (SessionOptions::kv = i8)");
+        XS_CHECK(kv.k == kv.v && (kv.k == quant::KvFormat::I8 || kv.k == quant::KvFormat::Float),
+                 "hip: the KV cache format ", quant::kv_format_name(kv.k), ":", quant::kv_format_name(kv.v),
+                 " is not supported; this backend stores keys and values as i8, or as the precision's float (auto)");
         for (const auto& slot : g_.kv_slots()) slot_of_.push_back(s_.slot_for(slot));
     }
     for (const Node& nd : nodes) {
@@ -1259,6 +1267,26 @@ void Program::launch(size_t i, const RunPlan& p, int64_t T, int64_t L, int64_t r
             KvState& kv = s_.kv()[static_cast<size_t>(slot)];
             const int64_t first = L - T;  // rows [L - T, L) of the slot
             const Value k = np.reads[0], v = np.reads[1];
+            if (kv.rows != DType::I8) {  // the Float format: rows of the precision's float
+                const bool at = replay_cap > 0;  // the first token read from the step record at replay
+                const size_t skip = at ? 0 : static_cast<size_t>(first * kv.heads * kv.dim) * dtype_size(kv.rows);
+                const int64_t* row0 = at ? s_.step_record() : nullptr;
+                const xs_dtype rd = abi(kv.rows);
+                if (dtype(k) == dtype(v)) {
+                    check(xs_hip_kv_store_pair(st, abi(dtype(k)), ptr(p, k), ptr(p, v), rd, kv.kc.get() + skip,
+                                               kv.vc.get() + skip, T * kv.heads, kv.dim, row0, kv.heads,
+                                               kv.cap * kv.heads),
+                          "KvCache");
+                } else {
+                    check(xs_hip_kv_store_pair(st, abi(dtype(k)), ptr(p, k), nullptr, rd, kv.kc.get() + skip, nullptr,
+                                               T * kv.heads, kv.dim, row0, kv.heads, kv.cap * kv.heads),
+                          "KvCache");
+                    check(xs_hip_kv_store_pair(st, abi(dtype(v)), ptr(p, v), nullptr, rd, kv.vc.get() + skip, nullptr,
+                                               T * kv.heads, kv.dim, row0, kv.heads, kv.cap * kv.heads),
+                          "KvCache");
+                }
+                return;
+            }
             if (dtype(k) == dtype(v)) {  // keys and values in one launch
                 const bool at = replay_cap > 0;  // the first token read from the step record at replay
                 const int64_t skip = at ? 0 : first * kv.heads;
@@ -1294,6 +1322,20 @@ void Program::launch(size_t i, const RunPlan& p, int64_t T, int64_t L, int64_t r
             const int64_t split = xs_hip_attention_i8_split(qs[0], kv.heads, replay_cap > 0 ? replay_cap : L);
             auto* out_p = reinterpret_cast<float*>(ptr(p, Value{static_cast<int32_t>(i), 0}));
             char* scratch = split > 1 ? s_.arena().get() + p.block_offset[static_cast<size_t>(p.scratch[i])] : nullptr;
+            if (kv.rows != DType::I8) {  // the Float format's rows
+                if (replay_cap > 0) {
+                    check(xs_hip_attention_at(st, abi(kv.rows), f32(0), kv.kc.get(), kv.vc.get(), out_p, qs[0], qs[1],
+                                              kv.heads, qs[2], kv.cap, s_.step_record() + 1, a.scale, a.softcap,
+                                              a.sliding_window, a.causal ? 1 : 0, split, scratch),
+                          what);
+                } else {
+                    check(xs_hip_attention(st, abi(kv.rows), f32(0), kv.kc.get(), kv.vc.get(), out_p, qs[0], qs[1],
+                                           kv.heads, qs[2], L, a.scale, a.softcap, a.sliding_window, a.causal ? 1 : 0,
+                                           split, scratch),
+                          what);
+                }
+                return;
+            }
             if (replay_cap > 0) {  // the key count read from the step record at replay
                 check(xs_hip_attention_i8_at(st, f32(0), kv.kc.get(), kv.ks.get(), kv.vc.get(), kv.vs.get(), out_p,
                                              qs[0], qs[1], kv.heads, qs[2], kv.cap, s_.step_record() + 1, a.scale,
@@ -1502,6 +1544,10 @@ HipSession::HipSession(std::span<const Graph* const> programs, const WeightStore
     XS_CHECK(!programs.empty(), "hip: nothing to compile");
     XS_CHECK(options_.max_context > 0, "hip: max_context ", options_.max_context);
     XS_CHECK(options_.rewind_tokens >= 0, "hip: rewind_tokens ", options_.rewind_tokens);
+    // As cpu-ref (cpu_backend.cpp:75-76, 611): f16 or f32, and activations computed in f32 either way; the precision
+    // picks the Float KV format's row type (f16 rows at f16 precision, f32 rows at f32).
+    XS_CHECK(options_.precision == DType::F16 || options_.precision == DType::F32,
+             "hip: session precision must be f16 or f32, got ", dtype_name(options_.precision));
     for (const auto& [key, value] : options_.extra) {
         XS_CHECK(key == "graphs", "hip: unknown backend option '", key, "' (known: graphs)");
         XS_CHECK(value == "0" || value == "1", "hip: backend option graphs=", value, " (expected 0 or 1)");
@@ -1526,10 +1572,13 @@ HipSession::HipSession(std::span<const Graph* const> programs, const WeightStore
     try {
         for (KvState& k : kv_) {
             const auto rows = static_cast<size_t>(k.cap * k.heads);
-            k.kc.grow(rows * static_cast<size_t>(k.dim));
-            k.vc.grow(rows * static_cast<size_t>(k.dim));
-            k.ks.grow(rows * 4);
-            k.vs.grow(rows * 4);
+            const size_t width = static_cast<size_t>(k.dim) * dtype_size(k.rows);
+            k.kc.grow(rows * width);
+            k.vc.grow(rows * width);
+            if (k.rows == DType::I8) {
+                k.ks.grow(rows * 4);
+                k.vs.grow(rows * 4);
+            }
         }
         step_.grow(2 * sizeof(int64_t));
         staging(256);
