@@ -330,6 +330,18 @@ inline void attention_rows_quantized(Stream q, const float* qp, const KvQuantize
                   "attention_rows_quantized");
 }
 
+// attention_rows<KV> + attention_combine (sycl_kernels.h, attention_rows / attention_combine) over a float cache, KV =
+// half or float: keys and values [kv_len, kv_heads, head_dim]; `part` holds attention_scratch(s, split) bytes when
+// split > 1.
+template <typename KV>
+void attention_rows(Stream q, const float* qp, const KV* k, const KV* v, float* out, const AttentionShape& s,
+                    int64_t split, float* part) {
+    static_assert(std::is_same_v<KV, half> || std::is_same_v<KV, float>, "float caches hold half or float rows");
+    detail::check(xs_hip_attention(q, detail::dtype_of<KV>(), qp, k, v, out, s.tokens, s.q_heads, s.kv_heads,
+                                   s.head_dim, s.kv_len, s.scale, s.softcap, s.window, s.causal ? 1 : 0, split, part),
+                  "attention_rows");
+}
+
 // ---- Device memory -------------------------------------------------------------------------------------------------
 
 // Owns `bytes` of device memory, freed on destruction; the counterpart of the SYCL backend's USM DeviceBuffer

@@ -133,6 +133,33 @@ int hipbe_dequantize_kv_f16(void* q, const void* codes, const void* scales, void
     });
 }
 
+// attention_rows<half> (the Float format at f16) and attention_rows_quantized (int8) with the split the launcher
+// suggests and its scratch.
+int hipbe_attention(void* q, int f16_rows, const float* qp, const void* k, const void* k_scales, const void* v,
+                    const void* v_scales, float* out, int64_t tokens, int64_t q_heads, int64_t kv_heads,
+                    int64_t head_dim, int64_t kv_len, float scale) {
+    return guarded([&] {
+        hb::AttentionShape s;
+        s.tokens = tokens;
+        s.q_heads = q_heads;
+        s.kv_heads = kv_heads;
+        s.head_dim = head_dim;
+        s.kv_len = kv_len;
+        s.scale = scale;
+        const int64_t split = hb::attention_split(s);
+        hb::DeviceBuffer part(hb::attention_scratch(s, split));
+        if (f16_rows) {
+            hb::attention_rows(q, qp, static_cast<const hb::half*>(k), static_cast<const hb::half*>(v), out, s, split,
+                               static_cast<float*>(part.get()));
+        } else {
+            hb::KvQuantized kv{{hb::KvFormat::I8, static_cast<const uint8_t*>(k), static_cast<const uint8_t*>(k_scales)},
+                               {hb::KvFormat::I8, static_cast<const uint8_t*>(v), static_cast<const uint8_t*>(v_scales)}};
+            hb::attention_rows_quantized(q, qp, kv, out, s, split, static_cast<float*>(part.get()));
+        }
+        if (xs_hip_stream_synchronize(q) != XS_HIP_OK) throw hb::Error(xs_hip_last_error());
+    });
+}
+
 int hipbe_quantize_kv_turbo() {
     return guarded([&] {
         hb::quantize_kv<float>(nullptr, hb::KvFormat::Turbo4, nullptr, nullptr, nullptr, 4, 100);  // not whole groups

@@ -40,6 +40,7 @@ def shim():
         "hipbe_dequantize_kv_f16": [_P, _P, _P, _P, _L, _L],
         "hipbe_binary_n_mismatch": [],
         "hipbe_quantize_kv_turbo": [],
+        "hipbe_attention": [_P, _I, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, C.c_float],
     }
     for name, args in sigs.items():
         getattr(L, name).argtypes = args
@@ -212,3 +213,32 @@ def test_hip_be_rope_and_kv(shim, ora):
     back = X.DeviceTensor.empty(F16, (1000, 128))
     run(shim, "hipbe_dequantize_kv_f16", None, codes.ptr, scales.ptr, back.ptr, 1000, 128)
     assert_exact(back.numpy(), ora.narrow(ora.dequantize_kv(wc, ws), F16), "hip_be dequantize")
+
+
+@pytest.mark.gpu
+def test_hip_be_attention(shim, ora):
+    """attention_rows<half> over f16 rows and attention_rows_quantized over int8 codes, through the launcher surface,
+    against the oracle over the values each cache holds (the reference's f32 device bar for attention)."""
+    rng = np.random.default_rng(16)
+    t, hq, hkv, d, n = 1, 16, 4, 128, 3000
+    q = rng.standard_normal((t, hq, d)).astype(np.float32)
+    k = ora.narrow(rng.standard_normal((n, hkv, d)).astype(np.float32), F16)
+    v = ora.narrow(rng.standard_normal((n, hkv, d)).astype(np.float32), F16)
+    qd, kd, vd = dev(q), dev(k, F16), dev(v, F16)
+    out = X.DeviceTensor.empty(F32, (t, hq, d))
+    scale = 1.0 / np.sqrt(d)
+    print("[gpu] hip_be attention_rows<half> [1, 16, 128] over 3000 keys", flush=True)
+    run(shim, "hipbe_attention", None, 1, qd.ptr, kd.ptr, None, vd.ptr, None, out.ptr, t, hq, hkv, d, n,
+        C.c_float(scale))
+    want = ora.attention(q, ora.widen(k, F16), ora.widen(v, F16), scale)
+    err = np.abs(out.numpy().astype(np.float64) - want)
+    assert (err <= 1e-5 + 1e-4 * np.abs(want)).all(), "hip_be attention_rows<half>"
+    kc, ks = X.quantize_kv(X.DeviceTensor.from_numpy(ora.widen(k, F16).reshape(n * hkv, d)))
+    vc, vs = X.quantize_kv(X.DeviceTensor.from_numpy(ora.widen(v, F16).reshape(n * hkv, d)))
+    print("[gpu] hip_be attention_rows_quantized int8", flush=True)
+    run(shim, "hipbe_attention", None, 0, qd.ptr, kc.ptr, ks.ptr, vc.ptr, vs.ptr, out.ptr, t, hq, hkv, d, n,
+        C.c_float(scale))
+    want = ora.attention(q, ora.dequantize_kv(kc.numpy(), ks.numpy()).reshape(n, hkv, d),
+                         ora.dequantize_kv(vc.numpy(), vs.numpy()).reshape(n, hkv, d), scale)
+    err = np.abs(out.numpy().astype(np.float64) - want)
+    assert (err <= 1e-4 + 1e-4 * np.abs(want)).all(), "hip_be attention_rows_quantized"
