@@ -541,44 +541,108 @@ def build_ops(only):
 # ---------------------------------------------------------------------------------------------------------------
 # CPU baseline (the oracle package is test infrastructure: used here only for this reported baseline leg)
 
+def _time_cpu(fn, seconds):
+    """Seconds per call of fn, over about `seconds` of repeated calls (after one untimed call)."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            return el / n, n, el
+
+
 def cpu_baseline(seconds):
+    """The reference CPU path on this host's cores, per configuration: the reference's own cpu-ref backend
+    (oracle/_ref/libxsref.so, compiled from the reference's sources) where it was built, else the repository's
+    restatement (oracle/liboracle.so). cpu-ref's ops are single-threaded, so every op entry is 1 core; the f16 / bf16
+    widening the reference threads (util/half.cpp:58-78, min(hardware threads, n / 2^20) threads) is timed on its
+    own. Each op runs on a bounded sample of its configuration (rows or tokens), for about `seconds` / 8 seconds,
+    extrapolated to the full call by the sample's share of its units."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O  # noqa: E402
     ref = O.reference()
     kind = "reference" if ref is not None else "port"
     impl = ref if ref is not None else O.oracle()
+    ora = O.oracle()
+    per_op = seconds / 8
+    ops = {}
+
+    def record(name, fn, sample_units, full_units, full_bytes, what):
+        per_call, n, el = _time_cpu(fn, per_op if name != "swiglu_bias" else 2 * per_op)
+        full = per_call * full_units / sample_units
+        ops[name] = {"us_per_full_call": round(full * 1e6, 1), "gb_s": round(full_bytes / full / 1e9, 4), "cores": 1,
+                     "kind": kind, "sample": f"{what}: {n} calls in {el:.1f} s, extrapolated x{full_units / sample_units:g}"}
+
+    # config 1: SwiGLU with bias, bf16 (Add, Silu, Mul through cpu-ref, then the bf16 narrowing)
     a = W.config1().arrays
     rows, cols = a["gate"].shape
-    sample_rows = 256
-    g, u, b = a["gate"][:sample_rows], a["up"][:sample_rows], a["bias"]
-
-    def once():
-        if kind == "reference":
-            y = impl.act_bias_mul(O.SILU, g, u, b, O.BF16)
-        else:
-            y = impl.act_bias_mul(O.SILU, impl.widen(g, O.BF16), impl.widen(u, O.BF16), impl.widen(b, O.BF16))
-        return impl.narrow(y, O.BF16)
-
-    once()
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        once()
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    per_call = el / n
-    sample_bytes = 3 * sample_rows * cols * 2 + cols * 2
+    sr = 256
+    g, u, b = a["gate"][:sr], a["up"][:sr], a["bias"]
+    if kind == "reference":
+        swiglu = lambda: impl.narrow(impl.act_bias_mul(O.SILU, g, u, b, O.BF16), O.BF16)  # noqa: E731
+    else:
+        gw, uw, bw = impl.widen(g, O.BF16), impl.widen(u, O.BF16), impl.widen(b, O.BF16)
+        swiglu = lambda: impl.narrow(impl.act_bias_mul(O.SILU, gw, uw, bw), O.BF16)  # noqa: E731
+    record("swiglu_bias", swiglu, sr, rows, W.ALGO_BYTES["swiglu_bias"],
+           f"rows 0..{sr - 1} of configs[1] [{rows}, {cols}] bf16")
+    # config 0: RMSNorm + residual, f32, the full call
+    c0 = W.config0().arrays
+    record("rmsnorm_residual", lambda: impl.add_rms_norm(c0["x"], c0["residual"], c0["weight"], 1e-6), 1, 1,
+           W.ALGO_BYTES["rmsnorm_residual"], "configs[0] [512, 2560] f32, the full call")
+    # config 2a: scaled, masked softmax, the full call
+    c2 = W.config2a()
+    scores = c2.arrays["scores"].reshape(-1, c2.arrays["scores"].shape[-1])
+    record("softmax_masked", lambda: impl.softmax_masked(scores, c2.params["scale"], c2.params["valid_len"]), 1, 1,
+           W.ALGO_BYTES["softmax_masked"], "configs[2] scores [32, 32768] masked at 30000, the full call")
+    # config 2b: argmax = topk(k = 1), the full call
+    logits = W.config2b().arrays["logits"]
+    record("argmax", lambda: impl.topk(logits, 1), 1, 1, W.ALGO_BYTES["argmax"], "configs[2] logits [1, 151936]")
+    # config 3: RoPE of Q and K, f16, a token sample
+    c3 = W.config3().arrays
+    st = 256
+    q3, k3, p3, f3 = c3["q"][:st], c3["k"][:st], c3["positions"][:st], c3["inv_freq"]
+    if kind == "reference":
+        rope = lambda: (impl.rope(q3, p3, f3, x_dtype=O.F16), impl.rope(k3, p3, f3, x_dtype=O.F16))  # noqa: E731
+    else:
+        qw, kw = impl.widen(q3, O.F16), impl.widen(k3, O.F16)
+        rope = lambda: (impl.rope(qw, p3, f3), impl.rope(kw, p3, f3))  # noqa: E731
+    record("rope_qk", rope, st, c3["q"].shape[0], W.ALGO_BYTES["rope_qk"],
+           f"tokens 0..{st - 1} of configs[3] Q [8192, 32, 128] and K [8192, 8, 128] f16")
+    # config 4: int8 KV quantize (keys and values), and the round trip (the reference's CPU cache stores the
+    # dequantized rows: quantize then dequantize, round_trip_kv_i8; it has no separate dequantize)
+    c4 = W.config4().arrays
+    kr = c4["k"].reshape(-1, c4["k"].shape[-1])
+    vr = c4["v"].reshape(-1, c4["v"].shape[-1])
+    sq = 8192
+    kf, vf = ora.widen(kr[:sq], O.F16), ora.widen(vr[:sq], O.F16)
+    quant = (lambda: (impl.quantize_kv_rows(kf), impl.quantize_kv_rows(vf))) if kind == "reference" else \
+        (lambda: (impl.quantize_kv(kf), impl.quantize_kv(vf)))
+    record("kv_quantize", quant, sq, kr.shape[0], W.ALGO_BYTES["kv_quantize"],
+           f"rows 0..{sq - 1} of configs[4] K and V [524288, 128] (f16 widened beforehand), quantize_kv_row_i8")
+    if kind == "reference":
+        record("kv_round_trip", lambda: (impl.round_trip_kv(kf), impl.round_trip_kv(vf)), sq, kr.shape[0],
+               W.ALGO_BYTES["kv_dequantize"],
+               f"rows 0..{sq - 1} of configs[4] K and V, round_trip_kv_i8 (quantize + dequantize: the reference CPU "
+               "path's dequantize has no entry of its own)")
+    # the threaded widening: configs[1]'s gate, bf16 -> f32
+    gate = a["gate"]
+    n_el = gate.size
+    hw = os.cpu_count() or 1
+    threads = max(1, min(hw, n_el >> 20))
+    widen = (lambda: impl.widen(gate, O.BF16))
+    per_call, n, el = _time_cpu(widen, per_op)
+    widen_entry = {"us_per_full_call": round(per_call * 1e6, 1), "gb_s": round(n_el * 6 / per_call / 1e9, 3),
+                   "threads": threads, "kind": kind,
+                   "sample": f"configs[1] gate [2048, 9728] bf16 -> f32 (util/half.cpp's threaded conversion: "
+                             f"min(hardware threads {hw}, n / 2^20 = {n_el >> 20}) threads), {n} calls in {el:.1f} s"}
     cpu = open("/proc/cpuinfo").read() if os.path.exists("/proc/cpuinfo") else ""
     model = next((l.split(":", 1)[1].strip() for l in cpu.splitlines() if l.startswith("model name")), "unknown")
-    return {"value": round(sample_bytes / per_call / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
-            "sample": f"SwiGLU bias bf16 rows 0..{sample_rows - 1} of configs[1] ([{sample_rows}, {cols}], "
-                      f"{sample_bytes} algorithmic bytes), {n} calls in {el:.1f} s through "
-                      + ("the reference cpu-ref backend's Session::run (Add, Silu, Mul) + f32->bf16"
-                         if kind == "reference" else "the oracle restatement"),
-            "us_per_full_call": round(per_call * (rows / sample_rows) * 1e6, 1),
-            "host_cpu": model, "nproc": os.cpu_count()}
+    head = ops["swiglu_bias"]
+    return {"value": head["gb_s"], "unit": "GB/s", "cores": 1, "kind": kind, "sample": head["sample"],
+            "us_per_full_call": head["us_per_full_call"], "per_config": ops, "widen_bf16_threaded": widen_entry,
+            "host_cpu": model, "nproc": hw}
 
 
 def measured_traffic():
@@ -601,7 +665,7 @@ def main():
     ap.add_argument("--repeats", type=int, default=5)
     ap.add_argument("--only", type=str, default=None, help="comma-separated op names (or 'copy', 'copy_<n>KiB', 'copy_<n>MiB')")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=16.0)
     ap.add_argument("--warm-seconds", type=float, default=0.3,
                     help="sustained graph replay before each op's timed windows (0 under hardware-counter runs, "
                          "where every dispatch is serialized)")

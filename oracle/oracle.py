@@ -361,6 +361,7 @@ class Reference(_Base, _Turbo):
         L.xsref_quantize_kv_row_i8.argtypes = [_fp, _L, _i8]
         L.xsref_quantize_kv_row_i8.restype = C.c_float
         L.xsref_round_trip_kv_i8.argtypes = [_fp, _L, _L]
+        L.xsref_quantize_kv_rows.argtypes = [_fp, _L, _L, _i8, _fp]
         L.xsref_kv_cache_i8.argtypes = [C.c_int, _P, _P, _L, _L, _L, _fp, _fp]
         L.xsref_turbo_quantize.argtypes = [_fp, _L, C.c_int, _u8, _u16]
         L.xsref_turbo_decode.argtypes = [_u8, _u16, _L, C.c_int, _fp]
@@ -534,6 +535,15 @@ class Reference(_Base, _Turbo):
             row_codes = np.empty(width, np.int8)
             scales[r] = self.lib.xsref_quantize_kv_row_i8(np.ascontiguousarray(xr[r]), width, row_codes)
             codes[r] = row_codes
+        return codes, scales
+
+    def quantize_kv_rows(self, x):
+        """quantize_kv_row_i8 over every row of x [rows, width] f32 in one native call: (codes, scales)."""
+        x = np.ascontiguousarray(x, np.float32)
+        rows, width = x.shape
+        codes = np.empty((rows, width), np.int8)
+        scales = np.empty(rows, np.float32)
+        self.lib.xsref_quantize_kv_rows(x, rows, width, codes, scales)
         return codes, scales
 
     def round_trip_kv(self, x):

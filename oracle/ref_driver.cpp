@@ -330,6 +330,12 @@ float xsref_quantize_kv_row_i8(const float* x, int64_t width, int8_t* codes) {
 
 void xsref_round_trip_kv_i8(float* x, int64_t rows, int64_t width) { quant::round_trip_kv_i8(x, rows, width); }
 
+// quantize_kv_row_i8 over `rows` rows in one call (codes [rows, width], scales [rows]): the reference's quantize loop
+// without a Python call per row, for timing.
+void xsref_quantize_kv_rows(const float* x, int64_t rows, int64_t width, int8_t* codes, float* scales) {
+    for (int64_t r = 0; r < rows; ++r) scales[r] = quant::quantize_kv_row_i8(x + r * width, width, codes + r * width);
+}
+
 // The KV rows a session's int8 cache holds after appending k, v [tokens, kv_heads, head_dim] (float dtype `dtype`):
 // KvCache through the backend with kv = i8 for keys and values.
 int xsref_kv_cache_i8(int dtype, const void* k, const void* v, int64_t tokens, int64_t kv_heads, int64_t head_dim,

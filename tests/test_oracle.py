@@ -356,6 +356,25 @@ def test_kv_goldens(ora):
 # Cross-check with the compiled reference on larger random inputs (only where the reference tree was built here).
 
 @pytest.mark.skipif(reference() is None, reason="oracle/_ref not built (no reference tree on this host)")
+def test_reference_quantize_rows_and_tiny_rows(ora):
+    """The batched reference quantize (the CPU baseline's timing entry) equals the reference's row function called row by
+    row, and the oracle's quantize; rows whose 127 / amax overflows (|x| < 3.7e-37) clamp nonzero codes to +-127 and
+    give 0 for zeros, in all three."""
+    ref = reference()
+    rng = np.random.default_rng(12)
+    x = (rng.standard_normal((40, 128)) * 2).astype(np.float32)
+    x[3] = (rng.standard_normal(128) * 1e-38).astype(np.float32)
+    x[3, ::4] = 0.0
+    c1, s1 = ref.quantize_kv_rows(x)
+    c2, s2 = ref.quantize_kv(x)
+    c3, s3 = ora.quantize_kv(x)
+    for c, sc in ((c2, s2), (c3, s3)):
+        assert_exact(c1, c)
+        assert_exact(s1, sc)
+    assert (np.abs(c1[3]) == np.where(x[3] != 0, 127, 0)).all()
+
+
+@pytest.mark.skipif(reference() is None, reason="oracle/_ref not built (no reference tree on this host)")
 def test_oracle_matches_compiled_reference(ora):
     ref = reference()
     rng = np.random.default_rng(11)

@@ -259,6 +259,15 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return __longlong_as_double(static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo));
 }
 
+// A workgroup barrier that orders LDS only. __syncthreads() also waits for every global access the workgroup has in
+// flight (its release fence covers global memory), which here would put the latency of an atomic still on its way to
+// memory in front of work that does not need it.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // Index arithmetic.
 

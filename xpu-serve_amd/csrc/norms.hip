@@ -41,17 +41,19 @@ struct NormArgs {
 // Threads of a workgroup of LPR lanes a row: kBlock when LPR divides it (several rows a workgroup), else one row.
 constexpr int norm_block(int lpr) { return lpr < kBlock && kBlock % lpr == 0 ? kBlock : lpr; }
 
-// Sum over the LPR lanes of a row (f64): shuffles inside a wave, one LDS stage across the row's waves. REUSE: `partial`
-// held an earlier sum of this launch, whose reads must finish first.
+// Sum over the LPR lanes of a row (f64): DPP inside a wave, one LDS stage across the row's waves (an LDS-only barrier:
+// the residual stores already issued need not land first). REUSE: `partial` held an earlier sum of this launch, whose
+// reads must finish first.
 template <int LPR, int BLOCK, bool REUSE = false>
 __device__ __forceinline__ double row_sum(double v, double* partial) {
     constexpr int WAVES_PER_ROW = LPR > 64 ? LPR / 64 : 1;
-    v = group_sum_f64<(LPR < 64 ? LPR : 64)>(v);
+    if constexpr (LPR >= 64) v = wave_sum_f64(v);
+    else v = group_sum_f64<LPR>(v);
     if constexpr (WAVES_PER_ROW > 1) {
         const int wave = threadIdx.x >> 6;
-        if constexpr (REUSE) __syncthreads();
+        if constexpr (REUSE) lds_barrier();
         if ((threadIdx.x & 63) == 0) partial[wave] = v;
-        __syncthreads();
+        lds_barrier();
         const int first = (wave / WAVES_PER_ROW) * WAVES_PER_ROW;
         v = 0.0;
 #pragma unroll
@@ -77,10 +79,22 @@ __global__ __launch_bounds__(norm_block(LPR)) void row_norm_vec(NormArgs p) {
 
     float h[NV][VEC];
     u32x4 raw_x[NV], raw_r[NV * (VEC == 4 ? 1 : 2)];
+    // The weight and bias vectors the outputs need (rows share them: they come from the caches), loaded with the row.
+    float wv[NV][VEC], bv[NV][VEC];
     // Issue every load of the row first.
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
         const int64_t v = l + static_cast<int64_t>(k) * LPR;
+        if (v < nvec) {
+            if (MODE != kL2Clip && p.w != nullptr) {
+                unpack<F32>(ld128(p.w + v * VEC), wv[k]);
+                if constexpr (VEC == 8) unpack<F32>(ld128(p.w + v * VEC + 4), wv[k] + 4);
+            }
+            if (MODE != kL2Clip && p.bias != nullptr) {
+                unpack<F32>(ld128(p.bias + v * VEC), bv[k]);
+                if constexpr (VEC == 8) unpack<F32>(ld128(p.bias + v * VEC + 4), bv[k] + 4);
+            }
+        }
         if (live && v < nvec) {
             raw_x[k] = ld128_nt(xr + v * VEC);
             if (p.r != nullptr) {
@@ -147,27 +161,19 @@ __global__ __launch_bounds__(norm_block(LPR)) void row_norm_vec(NormArgs p) {
     for (int k = 0; k < NV; ++k) {
         const int64_t v = l + static_cast<int64_t>(k) * LPR;
         if (v < nvec) {
-            float o[VEC], wv[VEC], bv[VEC];
-            if (MODE != kL2Clip && p.w != nullptr) {
-                unpack<F32>(ld128(p.w + v * VEC), wv);
-                if constexpr (VEC == 8) unpack<F32>(ld128(p.w + v * VEC + 4), wv + 4);
-            }
-            if (MODE != kL2Clip && p.bias != nullptr) {
-                unpack<F32>(ld128(p.bias + v * VEC), bv);
-                if constexpr (VEC == 8) unpack<F32>(ld128(p.bias + v * VEC + 4), bv + 4);
-            }
+            float o[VEC];
 #pragma unroll
             for (int i = 0; i < VEC; ++i) {
                 if constexpr (MODE == kLayer) {
                     double t = (static_cast<double>(h[k][i]) - mean) * scale;
-                    if (p.w != nullptr) t *= static_cast<double>(wv[i]);
-                    if (p.bias != nullptr) t += static_cast<double>(bv[i]);
+                    if (p.w != nullptr) t *= static_cast<double>(wv[k][i]);
+                    if (p.bias != nullptr) t += static_cast<double>(bv[k][i]);
                     o[i] = static_cast<float>(t);
                 } else {
                     double t = static_cast<double>(h[k][i]) * scale;
-                    if (p.w != nullptr) t *= static_cast<double>(wv[i]);
+                    if (MODE == kRms && p.w != nullptr) t *= static_cast<double>(wv[k][i]);
                     o[i] = static_cast<float>(t);
-                    if (p.bias != nullptr) o[i] = o[i] + bv[i];
+                    if (MODE == kRms && p.bias != nullptr) o[i] = o[i] + bv[k][i];
                 }
             }
             if constexpr (sizeof(SY) == 2 && VEC == 4) {

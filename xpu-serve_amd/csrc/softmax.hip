@@ -205,15 +205,6 @@ __device__ __forceinline__ void load_chunk(const SoftmaxArgs& p, int64_t row, in
     }
 }
 
-// A workgroup barrier that orders LDS only. __syncthreads() also waits for every global access the workgroup has in
-// flight (its release fence covers global memory), which here would put the latency of an atomic still on its way to
-// memory in front of work that does not need it.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // exp(a - b) for a <= b as f64: in f32 with the subtraction's rounding error folded in while the result is a normal
 // f32 (a - b >= -80), else in f64.
 __device__ __forceinline__ double exp_gap(float a, float b) {
