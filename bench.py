@@ -102,6 +102,8 @@ def time_op(op, steps, warmup, repeats, stream, warm_seconds):
         X.call("xs_hip_graph_launch", graph, stream)
         X.call("xs_hip_event_record", end, stream)
         graph_ms.append(_elapsed(start, end) / steps)
+    # The graph's last replay has ended (its end event was waited on); the stream is idle before the graph goes.
+    X.call("xs_hip_stream_synchronize", stream)
     X.call("xs_hip_graph_destroy", graph)
     eager_ms = []
     for _ in range(repeats):
@@ -283,6 +285,27 @@ def op_softmax():
 
 
 def op_argmax():
+    """Config 2b through xs_hip_topk with k = 1 (the reference's call, sycl_be::topk): two launches through a
+    scratch of any contents -- faster on MI355X than the one-launch form (argmax_one_launch), whose publish and
+    coherent poll cost more than the kernel boundary they save."""
+    c = W.config2b()
+    width = c.arrays["logits"].shape[1]
+    x0 = X.DeviceTensor.from_numpy(c.arrays["logits"])
+    nscratch = X.lib().xs_hip_topk_scratch(1, width, 1)
+
+    def mk():
+        sc = X.DeviceBuffer(nscratch)
+        s = (dcopy(x0), X.DeviceTensor.empty(X.F32, (1, 1)), X.DeviceTensor.empty(X.I32, (1, 1)), sc)
+        need(s[0], width * 4, "argmax")
+        return s
+
+    def go(s, stream):
+        x, v, i, sc = s
+        X.call("xs_hip_topk", stream, vp(x), vp(v), vp(i), 1, width, 1, C.c_void_p(sc.ptr))
+    return Op("argmax", W.ALGO_BYTES["argmax"], width * 4, mk, go, 2, "argmax_chunks")
+
+
+def op_argmax_one_launch():
     """Config 2b through xs_hip_argmax: one launch, its zero-filled scratch shared by the calls (one stream, in
     order; each call leaves it zero-filled)."""
     c = W.config2b()
@@ -299,27 +322,7 @@ def op_argmax():
     def go(s, stream):
         x, v, i = s
         X.call("xs_hip_argmax", stream, vp(x), vp(v), vp(i), 1, width, C.c_void_p(sp))
-    return Op("argmax", W.ALGO_BYTES["argmax"], width * 4, mk, go, 1, "argmax_split")
-
-
-def op_argmax_topk():
-    """Config 2b through xs_hip_topk with k = 1 (the reference's call, sycl_be::topk): two launches through a
-    scratch of any contents."""
-    c = W.config2b()
-    width = c.arrays["logits"].shape[1]
-    x0 = X.DeviceTensor.from_numpy(c.arrays["logits"])
-    nscratch = X.lib().xs_hip_topk_scratch(1, width, 1)
-
-    def mk():
-        sc = X.DeviceBuffer(nscratch)
-        s = (dcopy(x0), X.DeviceTensor.empty(X.F32, (1, 1)), X.DeviceTensor.empty(X.I32, (1, 1)), sc)
-        need(s[0], width * 4, "argmax")
-        return s
-
-    def go(s, stream):
-        x, v, i, sc = s
-        X.call("xs_hip_topk", stream, vp(x), vp(v), vp(i), 1, width, 1, C.c_void_p(sc.ptr))
-    return Op("argmax_topk_k1", W.ALGO_BYTES["argmax"], width * 4, mk, go, 2, "argmax_chunks")
+    return Op("argmax_one_launch", W.ALGO_BYTES["argmax"], width * 4, mk, go, 1, "argmax_split")
 
 
 # Top-k shapes of the reference's callers (models/common/blocks.cpp:29-52, models/drafters/dflash.cpp:362): a
@@ -506,7 +509,7 @@ def op_copy(n=256 << 20, name="copy"):
 
 
 OP_ORDER = ["swiglu_bias", "swiglu_bias_strided", "rmsnorm_residual", "rmsnorm_residual_separate", "softmax_masked",
-            "argmax", "argmax_topk_k1", "rope_qk", "rope_qk_separate", "kv_quantize", "kv_dequantize", "attention_i8_decode", "layer_norm", "l2_clip",
+            "argmax", "argmax_one_launch", "rope_qk", "rope_qk_separate", "kv_quantize", "kv_dequantize", "attention_i8_decode", "layer_norm", "l2_clip",
             "reduce_sum_rows", "reduce_sum_cols", "unary_softcap", "kv_turbo4_quantize", "kv_turbo4_dequantize",
             "topk_shortlist", "topk_moe_router", "topk_draft_candidates"]
 
@@ -525,7 +528,7 @@ def build_ops(only):
         yield {"swiglu_bias": op_swiglu, "swiglu_bias_strided": op_swiglu_strided, "rmsnorm_residual": op_rmsnorm,
                "rmsnorm_residual_separate": op_rmsnorm_separate,
                "softmax_masked": op_softmax, "argmax": op_argmax,
-               "argmax_topk_k1": op_argmax_topk, "rope_qk": op_rope,
+               "argmax_one_launch": op_argmax_one_launch, "rope_qk": op_rope,
                "rope_qk_separate": lambda: op_rope(True), "copy": op_copy,
                "kv_quantize": lambda: op_kv_quantize(kv), "kv_dequantize": lambda: op_kv_dequantize(kv),
                "attention_i8_decode": lambda: op_attention_i8(kv), "unary_softcap": op_unary_softcap,
@@ -646,13 +649,13 @@ def cpu_baseline(seconds):
 
 
 def measured_traffic():
-    """HBM bytes per launch of each workload kernel, read from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
-    (already scaled by the copy-kernel calibration recorded there). None where the summary is absent."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic_pmc_all_ops.md")
+    """HBM bytes per call of each op, read from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (one op a
+    process, already scaled by the copy-kernel calibration recorded there). Empty where the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_per_op.md")
     try:
         text = open(path).read()
         block = text.split("```json", 1)[1].split("```", 1)[0]
-        return json.loads(block)["traffic_bytes_per_launch"]
+        return json.loads(block)["traffic_bytes_per_call"]
     except (OSError, IndexError, ValueError, KeyError):
         return {}
 
@@ -690,7 +693,12 @@ def main():
 
     head_name = "swiglu_bias" if "swiglu_bias" in results else next(iter(results))
     head = results[head_name]
-    traffic = measured_traffic().get(head_name)
+    measured = measured_traffic()
+    for name, r in results.items():
+        t = measured.get(name)
+        r["traffic"] = t
+        r["traffic_ratio"] = round(t / r["bytes"], 4) if t else None
+    traffic = measured.get(head_name)
     line = {
         "metric": METRIC,
         "value": head["gb_s"],
@@ -709,7 +717,7 @@ def main():
                    "entry_point": "xs_hip_act_bias_mul_2d", "algorithmic_bytes_per_call": W.ALGO_BYTES["swiglu_bias"]},
         "roofline": {"bound": "hbm", "achieved": head["gb_s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": head["frac_of_peak"], "traffic": traffic,
-                     "traffic_source": "profiles/hbm_traffic_pmc_all_ops.md" if traffic else None,
+                     "traffic_source": "profiles/hbm_traffic_per_op.md" if traffic else None,
                      "kernel": head["kernel"], "avg_launch_us": head["us_per_call"] / head["launches"]},
         "device": dev_name,
         "ops": results,
