@@ -354,6 +354,28 @@ int xs_hip_attention_at(void* stream, xs_dtype kv_dtype, const float* q, const v
                         int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t kv_capacity,
                         const int64_t* kv_len, float scale, float softcap, int64_t window, int causal, int64_t split,
                         void* scratch);
+/* Decode attention over a quantized cache of any pair of formats the reference reads (kv_formats_supported,
+ * sycl_kernels.h:209-212): int8 keys and values (then exactly xs_hip_attention_i8), keys and values in the same
+ * TurboQuant format, or int8 keys with TurboQuant values. Each stream as xs_hip_quantize_kv writes it: int8 codes
+ * [kv_len, kv_heads, head_dim] with f32 scales [kv_len, kv_heads]; TurboQuant codes [kv_len * kv_heads *
+ * head_dim / 128, 16 * bits] bytes with f16 norms [kv_len * kv_heads * head_dim / 128]. cpu_ref::attention over the
+ * values the cache stores (quant::round_trip_kv, kv_format.cpp:57-61), computed in the formats' rotated domain: the
+ * query rotated as the rows are, the weighted sum rotated back. q, out, key selection, scale, softcap, split and
+ * scratch as xs_hip_attention_i8; with TurboQuant values head_dim is 128, 256 or 512. Codes 16-byte aligned. Other
+ * pairs are refused with XS_HIP_EUNSUPPORTED ("keys in <k> with values in <v>"). Replaces
+ * sycl_be::attention_rows_quantized + attention_combine (sycl_kernels.h:236-240; rows as sycl_kv_rows.h:37-100). */
+int xs_hip_attention_quantized(void* stream, xs_kv_format k_format, xs_kv_format v_format, const float* q,
+                               const void* k_codes, const void* k_scales, const void* v_codes, const void* v_scales,
+                               float* out, int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                               int64_t kv_len, float scale, float softcap, int64_t window, int causal, int64_t split,
+                               void* scratch);
+/* xs_hip_attention_quantized over a cache of kv_capacity keys of which the kernel reads how many it holds from the
+ * device int64 at kv_len (clamped to [0, kv_capacity]). No reference counterpart, as xs_hip_attention_i8_at. */
+int xs_hip_attention_quantized_at(void* stream, xs_kv_format k_format, xs_kv_format v_format, const float* q,
+                                  const void* k_codes, const void* k_scales, const void* v_codes,
+                                  const void* v_scales, float* out, int64_t tokens, int64_t q_heads, int64_t kv_heads,
+                                  int64_t head_dim, int64_t kv_capacity, const int64_t* kv_len, float scale,
+                                  float softcap, int64_t window, int causal, int64_t split, void* scratch);
 /* xs_hip_attention_i8 with no scratch argument and no allocation: a split's partial rows go to a device array of
  * 8 MiB (8388608 bytes) that the library holds on each GPU it runs on until the process ends; a split needing more
  * (xs_hip_attention_i8_scratch bytes) is refused with XS_HIP_EINVAL. No reference counterpart: it is for callers that

@@ -318,15 +318,16 @@ inline size_t attention_scratch(const AttentionShape& s, int64_t split) {
     return xs_hip_attention_i8_scratch(s.tokens, s.q_heads, s.head_dim, split);
 }
 
-// attention_rows_quantized + attention_combine (sycl_kernels.h:238-240) for int8 keys and values: `part` holds
-// attention_scratch(s, split) bytes when split > 1.
+// attention_rows_quantized + attention_combine (sycl_kernels.h:238-240): int8 keys and values, both in the same
+// TurboQuant format, or int8 keys with TurboQuant values (kv_formats_supported, sycl_kernels.h:209-212); other pairs
+// throw. `part` holds attention_scratch(s, split) bytes when split > 1.
 inline void attention_rows_quantized(Stream q, const float* qp, const KvQuantized& kv, float* out,
                                      const AttentionShape& s, int64_t split, float* part) {
-    if (kv.k.format != KvFormat::I8 || kv.v.format != KvFormat::I8)
-        throw Error("hip_be::attention_rows_quantized: only int8 keys and values are read on this device");
-    detail::check(xs_hip_attention_i8(q, qp, kv.k.codes, kv.k.scales, kv.v.codes, kv.v.scales, out, s.tokens,
-                                      s.q_heads, s.kv_heads, s.head_dim, s.kv_len, s.scale, s.softcap, s.window,
-                                      s.causal ? 1 : 0, split, part),
+    detail::check(xs_hip_attention_quantized(q, static_cast<xs_kv_format>(kv.k.format),
+                                             static_cast<xs_kv_format>(kv.v.format), qp, kv.k.codes, kv.k.scales,
+                                             kv.v.codes, kv.v.scales, out, s.tokens, s.q_heads, s.kv_heads,
+                                             s.head_dim, s.kv_len, s.scale, s.softcap, s.window, s.causal ? 1 : 0,
+                                             split, part),
                   "attention_rows_quantized");
 }
 

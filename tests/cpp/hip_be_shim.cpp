@@ -133,9 +133,9 @@ int hipbe_dequantize_kv_f16(void* q, const void* codes, const void* scales, void
     });
 }
 
-// attention_rows<half> (the Float format at f16) and attention_rows_quantized (int8) with the split the launcher
-// suggests and its scratch.
-int hipbe_attention(void* q, int f16_rows, const float* qp, const void* k, const void* k_scales, const void* v,
+// attention_rows<half> (k_format 0: the Float format at f16) or attention_rows_quantized over keys and values in
+// k_format / v_format (KvFormat's values), with the split the launcher suggests and its scratch.
+int hipbe_attention(void* q, int k_format, int v_format, const float* qp, const void* k, const void* k_scales, const void* v,
                     const void* v_scales, float* out, int64_t tokens, int64_t q_heads, int64_t kv_heads,
                     int64_t head_dim, int64_t kv_len, float scale) {
     return guarded([&] {
@@ -148,12 +148,14 @@ int hipbe_attention(void* q, int f16_rows, const float* qp, const void* k, const
         s.scale = scale;
         const int64_t split = hb::attention_split(s);
         hb::DeviceBuffer part(hb::attention_scratch(s, split));
-        if (f16_rows) {
+        if (k_format == 0) {
             hb::attention_rows(q, qp, static_cast<const hb::half*>(k), static_cast<const hb::half*>(v), out, s, split,
                                static_cast<float*>(part.get()));
         } else {
-            hb::KvQuantized kv{{hb::KvFormat::I8, static_cast<const uint8_t*>(k), static_cast<const uint8_t*>(k_scales)},
-                               {hb::KvFormat::I8, static_cast<const uint8_t*>(v), static_cast<const uint8_t*>(v_scales)}};
+            hb::KvQuantized kv{{static_cast<hb::KvFormat>(k_format), static_cast<const uint8_t*>(k),
+                                static_cast<const uint8_t*>(k_scales)},
+                               {static_cast<hb::KvFormat>(v_format), static_cast<const uint8_t*>(v),
+                                static_cast<const uint8_t*>(v_scales)}};
             hb::attention_rows_quantized(q, qp, kv, out, s, split, static_cast<float*>(part.get()));
         }
         if (xs_hip_stream_synchronize(q) != XS_HIP_OK) throw hb::Error(xs_hip_last_error());

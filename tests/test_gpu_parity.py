@@ -1433,6 +1433,20 @@ def test_turbo_rotate(ora):
     d = dev(x)
     X.call("xs_hip_kv_rotate", None, C.c_void_p(d.ptr), C.c_void_p(d.ptr), 77, 256, 0)
     assert_exact(d.numpy(), ora.turbo_rotate(x), "rotate in place")
+    # Exact cancellations: signed zeros as IEEE arithmetic gives them (a zero row, a row of -0, small integers, and
+    # decoded turbo2 groups, whose few distinct values cancel often).
+    z = rng.integers(-1, 2, (64, 128)).astype(np.float32)
+    z[0] = 0.0
+    z[1] = -0.0
+    z[2, ::2] = -0.0
+    c2, n2 = ora.turbo_quantize(rng.standard_normal((64, 128)).astype(np.float32), 2)
+    z = np.concatenate([z, ora.turbo_decode(c2, n2, 2)])
+    for inverse in (False, True):
+        step(f"kv_rotate signed zeros, inverse {inverse}")
+        got = X.kv_rotate(dev(z), inverse=inverse).numpy()
+        want = ora.turbo_rotate(z, inverse=inverse)
+        assert (want == 0).any() and np.signbit(want[want == 0]).any()
+        assert_exact(got, want, f"rotate signed zeros, inverse {inverse}")
 
 
 def test_turbo4_full_size(ora):

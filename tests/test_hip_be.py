@@ -40,7 +40,7 @@ def shim():
         "hipbe_dequantize_kv_f16": [_P, _P, _P, _P, _L, _L],
         "hipbe_binary_n_mismatch": [],
         "hipbe_quantize_kv_turbo": [],
-        "hipbe_attention": [_P, _I, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, C.c_float],
+        "hipbe_attention": [_P, _I, _I, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, C.c_float],
     }
     for name, args in sigs.items():
         getattr(L, name).argtypes = args
@@ -228,7 +228,7 @@ def test_hip_be_attention(shim, ora):
     out = X.DeviceTensor.empty(F32, (t, hq, d))
     scale = 1.0 / np.sqrt(d)
     print("[gpu] hip_be attention_rows<half> [1, 16, 128] over 3000 keys", flush=True)
-    run(shim, "hipbe_attention", None, 1, qd.ptr, kd.ptr, None, vd.ptr, None, out.ptr, t, hq, hkv, d, n,
+    run(shim, "hipbe_attention", None, 0, 0, qd.ptr, kd.ptr, None, vd.ptr, None, out.ptr, t, hq, hkv, d, n,
         C.c_float(scale))
     want = ora.attention(q, ora.widen(k, F16), ora.widen(v, F16), scale)
     err = np.abs(out.numpy().astype(np.float64) - want)
@@ -236,9 +236,19 @@ def test_hip_be_attention(shim, ora):
     kc, ks = X.quantize_kv(X.DeviceTensor.from_numpy(ora.widen(k, F16).reshape(n * hkv, d)))
     vc, vs = X.quantize_kv(X.DeviceTensor.from_numpy(ora.widen(v, F16).reshape(n * hkv, d)))
     print("[gpu] hip_be attention_rows_quantized int8", flush=True)
-    run(shim, "hipbe_attention", None, 0, qd.ptr, kc.ptr, ks.ptr, vc.ptr, vs.ptr, out.ptr, t, hq, hkv, d, n,
+    run(shim, "hipbe_attention", None, X.KV_I8, X.KV_I8, qd.ptr, kc.ptr, ks.ptr, vc.ptr, vs.ptr, out.ptr, t, hq, hkv, d, n,
         C.c_float(scale))
     want = ora.attention(q, ora.dequantize_kv(kc.numpy(), ks.numpy()).reshape(n, hkv, d),
                          ora.dequantize_kv(vc.numpy(), vs.numpy()).reshape(n, hkv, d), scale)
     err = np.abs(out.numpy().astype(np.float64) - want)
     assert (err <= 1e-4 + 1e-4 * np.abs(want)).all(), "hip_be attention_rows_quantized"
+    # int8 keys with turbo3 values
+    tc, tn = X.turbo_quantize(X.DeviceTensor.from_numpy(ora.widen(v, F16).reshape(n * hkv, d)), 3)
+    print("[gpu] hip_be attention_rows_quantized i8:turbo3", flush=True)
+    run(shim, "hipbe_attention", None, X.KV_I8, X.KV_TURBO3, qd.ptr, kc.ptr, ks.ptr, tc.ptr, tn.ptr, out.ptr, t, hq,
+        hkv, d, n, C.c_float(scale))
+    v_rt = ora.turbo_rotate(ora.turbo_decode(tc.numpy(), tn.numpy().view(np.uint16), 3), inverse=True)
+    want = ora.attention(q, ora.dequantize_kv(kc.numpy(), ks.numpy()).reshape(n, hkv, d), v_rt.reshape(n, hkv, d),
+                         scale)
+    err = np.abs(out.numpy().astype(np.float64) - want)
+    assert (err <= 1e-4 + 1e-4 * np.abs(want)).all(), "hip_be attention_rows_quantized i8:turbo3"

@@ -26,6 +26,7 @@
 #include <mutex>
 
 #include "common.h"
+#include "kv_turbo.h"
 
 namespace xs_hip {
 namespace {
@@ -785,6 +786,295 @@ int launch_float(hipStream_t s, const AttnArgs& a, const void* k, const void* v)
     }
 }
 
+// ---- Decode attention over TurboQuant values, with TurboQuant or int8 keys ---------------------------------------
+//
+// The readers of the pairs of quantized formats other than int8/int8 that the reference attends over: keys and values
+// in the same TurboQuant format, or int8 keys with TurboQuant values (reference src/backend/sycl/sycl_kernels.h:
+// 209-212, 238; sycl_kernels.cpp attention_rows_quantized; rows read as sycl_kv_rows.h's I8Rows and TurboRows).
+// Semantics: cpu_ref::attention over the values the cache stores (quant::round_trip_kv: a TurboQuant row's decoded
+// values rotated back, an int8 row's fl32(code * scale)), computed where the rows are stored: a TurboQuant format keeps
+// its rows rotated (each group of 128 values: sign flips, Walsh-Hadamard, 1 / sqrt(128), sign flips), an orthogonal
+// map, so the query rotated the same way has the originals' dot products with the stored keys, and the weighted sum of
+// stored values, rotated back, is the weighted sum of the originals (up to f32 rounding: the reference's device
+// tolerance for a quantized cache, tests/unit/backend/device_attention.cpp:23-27).
+//
+// Layout: as the float reader above -- one 256-thread workgroup per (token, KV head, key split) for all G query heads,
+// tiles of 256 keys with thread i scoring key i, an online softmax per head -- with these readers:
+//  - keys, TurboQuant: a row's groups of 128 codes (16 * bits bytes each, 16-byte loads) and their f16 norms; a
+//    group's dot product with the rotated query sums q_r[d] * centroid[code_d], times the group's norm;
+//  - keys, int8: 16 codes a 16-byte load, the dot product with the query times the row's scale;
+//  - values, TurboQuant: thread t holds 8 dims of every head, the 8 values lane t % 16 of a group stores (one 32-bit
+//    word of nibbles, or a 16-bit word of 2-bit codes and for turbo3 one byte of third bits), over the tile's keys
+//    t / (D / 8) + k (2048 / D), k = 0, 1, ...; centroid[code] * norm.
+// The centroids sit in LDS. At the end each head's sums add up over the key subsets, and 16 threads a group of 128
+// rotate them back (the butterflies across 16 lanes) before the output or the partial row is written.
+constexpr int kTurboTile = 256;
+
+// KB: 8 for int8 keys, else the keys' TurboQuant bits; VB: the values' TurboQuant bits.
+template <int KB, int VB, int G, int D, bool CAP>
+__global__ __launch_bounds__(256) void attention_turbo_rows(AttnArgs a, const uint8_t* kc, const void* ks,
+                                                            const uint8_t* vc, const uint16_t* vn) {
+    using namespace turbo;
+    static_assert(KB == 8 || KB == VB, "keys int8 or in the values' format");
+    static_assert(D % kGroup == 0, "TurboQuant rows are whole groups of 128");
+    constexpr int kNG = D / kGroup;        // groups a row
+    constexpr int kD8 = D / kLaneValues;   // 8-dim slices a row
+    constexpr int kS = 256 / kD8;          // key subsets of the weighted sum
+    constexpr int kVGB = group_bytes(VB);  // bytes of a value group's codes
+    __shared__ __align__(16) float q_s[G][D];
+    __shared__ float p_s[G][kTurboTile];
+    __shared__ float red[2][4][G];
+    __shared__ __align__(16) float acc_s[kS][D];
+    __shared__ float cent[1 << VB];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t t = blockIdx.y / a.kv_heads;
+    const int64_t kvh = blockIdx.y - t * a.kv_heads;
+    const int sp = blockIdx.x;
+
+    if (tid < (1 << VB)) cent[tid] = centroid<VB>(tid);
+    for (int i = tid; i < G * D; i += 256) q_s[i / D][i % D] = a.q[(t * a.q_heads + kvh * G + i / D) * D + i % D];
+    if constexpr (KB != 8) {
+        // The query into the keys' rotated domain: 16 threads a group of 128, 8 values each (G * D / 8 is a multiple
+        // of 16, so whole groups of 16 lanes take part).
+        __syncthreads();
+        for (int i = tid; i < G * kD8; i += 256) {
+            float* qv = &q_s[i / kD8][(i % kD8) * kLaneValues];
+            float v[kLaneValues];
+#pragma unroll
+            for (int e = 0; e < kLaneValues; ++e) v[e] = qv[e];
+            rotate8(v, i % kLanes, false);
+#pragma unroll
+            for (int e = 0; e < kLaneValues; ++e) qv[e] = v[e];
+        }
+    }
+
+    int64_t first, last;
+    key_range(a, keys_of(a), t, first, last);
+    const int64_t len = last >= first ? last - first + 1 : 0;
+    const int64_t per = (len + a.split - 1) / a.split;
+    const int64_t k0 = first + sp * per;
+    const int64_t k1 = k0 + per - 1 < last ? k0 + per - 1 : last;
+    float m[G], l[G], acc[G][kLaneValues];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < kLaneValues; ++e) acc[g][e] = 0.0f;
+    }
+    const int dg = tid % kD8, sub = tid / kD8;
+    const int vgi = dg / kLanes, vlane = dg % kLanes;  // the value group and lane this thread's 8 dims are
+    __syncthreads();
+    for (int64_t j0 = k0; j0 <= k1; j0 += kTurboTile) {
+        // Scores of key j0 + tid for every head.
+        const int64_t j = j0 + tid;
+        float s[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) s[g] = 0.0f;
+        if (j <= k1) {
+            const int64_t row = j * a.kv_heads + kvh;
+            // The row in chunks of 32 values (4 lanes' worth of a group): decoded into registers once, then one dot
+            // product per head.
+            float factor = 1.0f;
+#pragma unroll 1
+            for (int c = 0; c < D / 32; ++c) {
+                float x[32];
+                float part_norm = 1.0f;
+                if constexpr (KB == 8) {
+                    const uint8_t* r = kc + row * D + 32 * c;
+                    const u32x4 w0 = ld128(r), w1 = ld128(r + 16);
+#pragma unroll
+                    for (int b = 0; b < 16; ++b) {
+                        x[b] = byte_f32(w0[b / 4], b % 4);
+                        x[16 + b] = byte_f32(w1[b / 4], b % 4);
+                    }
+                } else {
+                    constexpr int kChunks = kGroup / 32;  // chunks a group
+                    const int gi = c / kChunks, cc = c % kChunks;
+                    const int64_t group = row * kNG + gi;
+                    const uint8_t* gc = kc + group * group_bytes(KB);
+                    uint32_t low[4], high = 0;
+                    if constexpr (KB == 4) {
+                        const u32x4 w = ld128(gc + 16 * cc);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) low[i] = w[i];
+                    } else {
+                        const uint2 w = *reinterpret_cast<const uint2*>(gc + 8 * cc);
+                        low[0] = w.x & 0xffffu;
+                        low[1] = w.x >> 16;
+                        low[2] = w.y & 0xffffu;
+                        low[3] = w.y >> 16;
+                        if constexpr (KB == 3) high = *reinterpret_cast<const uint32_t*>(gc + kGroup / 4 + 4 * cc);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        LaneCodes<KB> lc;
+                        lc.low = low[i];
+                        lc.high = (high >> (8 * i)) & 0xffu;
+#pragma unroll
+                        for (int e = 0; e < kLaneValues; ++e) x[8 * i + e] = cent[lc.code(e)];
+                    }
+                    part_norm = f16_to_f32(static_cast<const uint16_t*>(ks)[group]);
+                }
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const float* qg = &q_s[g][32 * c];
+                    float dot = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 32; e += 4) {
+                        const float4 q4 = *reinterpret_cast<const float4*>(qg + e);
+                        dot = fmaf(q4.x, x[e], dot);
+                        dot = fmaf(q4.y, x[e + 1], dot);
+                        dot = fmaf(q4.z, x[e + 2], dot);
+                        dot = fmaf(q4.w, x[e + 3], dot);
+                    }
+                    if constexpr (KB == 8) s[g] += dot;
+                    else s[g] = fmaf(dot, part_norm, s[g]);
+                }
+            }
+            if constexpr (KB == 8) factor = static_cast<const float*>(ks)[row];
+#pragma unroll
+            for (int g = 0; g < G; ++g) s[g] *= factor;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float x = s[g] * a.scale;
+                if constexpr (CAP) x = a.softcap * tanhf(x / a.softcap);
+                s[g] = x;
+            }
+        } else {
+#pragma unroll
+            for (int g = 0; g < G; ++g) s[g] = -INFINITY;
+        }
+        // The tile's max per head, then exponentials and their sum.
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float w = wave_reduce<OpMax>(s[g], -INFINITY);
+            if (lane == 0) red[0][wave][g] = w;
+        }
+        __syncthreads();
+        float c[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float mt = fmaxf(fmaxf(red[0][0][g], red[0][1][g]), fmaxf(red[0][2][g], red[0][3][g]));
+            const float mn = fmaxf(m[g], mt);
+            c[g] = m[g] == -INFINITY ? 0.0f : __expf(m[g] - mn);
+            m[g] = mn;
+            const float p = s[g] == -INFINITY ? 0.0f : __expf(s[g] - mn);
+            p_s[g][tid] = p;
+            const float w = wave_reduce<OpSum>(p, 0.0f);
+            if (lane == 0) red[1][wave][g] = w;
+        }
+        __syncthreads();
+        // The weighted sum of the tile's stored (rotated) value rows.
+        const int64_t n = k1 - j0 + 1 < kTurboTile ? k1 - j0 + 1 : kTurboTile;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            l[g] = l[g] * c[g] + ((red[1][0][g] + red[1][1][g]) + (red[1][2][g] + red[1][3][g]));
+#pragma unroll
+            for (int e = 0; e < kLaneValues; ++e) acc[g][e] *= c[g];
+        }
+        for (int k = sub; k < n; k += kS) {
+            const int64_t group = ((j0 + k) * a.kv_heads + kvh) * kNG + vgi;
+            LaneCodes<VB> lc;
+            lc.load(vc + group * kVGB, vlane);
+            const float norm = f16_to_f32(vn[group]);
+            float vf[kLaneValues];
+#pragma unroll
+            for (int e = 0; e < kLaneValues; ++e) vf[e] = cent[lc.code(e)] * norm;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float p = p_s[g][k];
+#pragma unroll
+                for (int e = 0; e < kLaneValues; ++e) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
+            }
+        }
+        __syncthreads();  // p_s and red are rewritten by the next tile
+    }
+    // Per head: the key subsets' sums add up, 16 threads a group rotate them back, then the output or the partial row
+    // with its (max, sum).
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        *reinterpret_cast<u32x4*>(&acc_s[sub][kLaneValues * dg]) =
+            u32x4{__float_as_uint(acc[g][0]), __float_as_uint(acc[g][1]), __float_as_uint(acc[g][2]),
+                  __float_as_uint(acc[g][3])};
+        *reinterpret_cast<u32x4*>(&acc_s[sub][kLaneValues * dg + 4]) =
+            u32x4{__float_as_uint(acc[g][4]), __float_as_uint(acc[g][5]), __float_as_uint(acc[g][6]),
+                  __float_as_uint(acc[g][7])};
+        __syncthreads();
+        if (tid < kD8) {  // kD8 is a multiple of 16: whole groups of 16 lanes
+            float v[kLaneValues];
+#pragma unroll
+            for (int e = 0; e < kLaneValues; ++e) {
+                float sum = 0.0f;
+#pragma unroll
+                for (int q = 0; q < kS; ++q) sum += acc_s[q][kLaneValues * tid + e];
+                v[e] = sum;
+            }
+            rotate8(v, tid % kLanes, true);
+            const int64_t hh = kvh * G + g;
+            if (a.part == nullptr) {
+                float* o = a.out + (t * a.q_heads + hh) * D + kLaneValues * tid;
+#pragma unroll
+                for (int e = 0; e < kLaneValues; ++e) o[e] = v[e] / l[g];
+            } else {
+                const int64_t pi = (t * a.q_heads + hh) * a.split + sp;
+                float* o = a.part + pi * D + kLaneValues * tid;
+#pragma unroll
+                for (int e = 0; e < kLaneValues; ++e) o[e] = v[e];
+                if (tid == 0) {
+                    float* ml = a.part + a.tokens * a.q_heads * a.split * D + 2 * pi;
+                    ml[0] = m[g];
+                    ml[1] = l[g];
+                }
+            }
+        }
+        __syncthreads();  // acc_s is rewritten for the next head
+    }
+}
+
+template <int KB, int VB, int G>
+int launch_turbo_g(hipStream_t s, const AttnArgs& a, const uint8_t* kc, const void* ks, const uint8_t* vc,
+                   const uint16_t* vn, const char* what) {
+    const dim3 grid(static_cast<unsigned>(a.split), static_cast<unsigned>(a.tokens * a.kv_heads));
+    const bool cap = a.softcap > 0.0f;
+    switch (a.head_dim) {
+        case 128:
+            if (cap) attention_turbo_rows<KB, VB, G, 128, true><<<grid, 256, 0, s>>>(a, kc, ks, vc, vn);
+            else attention_turbo_rows<KB, VB, G, 128, false><<<grid, 256, 0, s>>>(a, kc, ks, vc, vn);
+            break;
+        case 256:
+            if (cap) attention_turbo_rows<KB, VB, G, 256, true><<<grid, 256, 0, s>>>(a, kc, ks, vc, vn);
+            else attention_turbo_rows<KB, VB, G, 256, false><<<grid, 256, 0, s>>>(a, kc, ks, vc, vn);
+            break;
+        case 512:
+            if (cap) attention_turbo_rows<KB, VB, G, 512, true><<<grid, 256, 0, s>>>(a, kc, ks, vc, vn);
+            else attention_turbo_rows<KB, VB, G, 512, false><<<grid, 256, 0, s>>>(a, kc, ks, vc, vn);
+            break;
+        default:
+            return fail(XS_HIP_EUNSUPPORTED, std::string(what) + ": head_dim " + std::to_string(a.head_dim) +
+                                                 " with TurboQuant values (supported: 128, 256, 512)");
+    }
+    return check_launch(what);
+}
+
+template <int KB, int VB>
+int launch_turbo(hipStream_t s, const AttnArgs& a, const uint8_t* kc, const void* ks, const uint8_t* vc,
+                 const uint16_t* vn, const char* what) {
+    switch (a.q_heads / a.kv_heads) {
+        case 1: return launch_turbo_g<KB, VB, 1>(s, a, kc, ks, vc, vn, what);
+        case 2: return launch_turbo_g<KB, VB, 2>(s, a, kc, ks, vc, vn, what);
+        case 3: return launch_turbo_g<KB, VB, 3>(s, a, kc, ks, vc, vn, what);
+        case 4: return launch_turbo_g<KB, VB, 4>(s, a, kc, ks, vc, vn, what);
+        case 5: return launch_turbo_g<KB, VB, 5>(s, a, kc, ks, vc, vn, what);
+        case 6: return launch_turbo_g<KB, VB, 6>(s, a, kc, ks, vc, vn, what);
+        case 7: return launch_turbo_g<KB, VB, 7>(s, a, kc, ks, vc, vn, what);
+        case 8: return launch_turbo_g<KB, VB, 8>(s, a, kc, ks, vc, vn, what);
+        default:
+            return fail(XS_HIP_EUNSUPPORTED, std::string(what) + ": " + std::to_string(a.q_heads / a.kv_heads) +
+                                                 " query heads per KV head (supported: 1 to 8)");
+    }
+}
+
 // KV heads a workgroup of `waves` waves: the largest power of two up to `waves` dividing kv_heads.
 int heads_per_group(int64_t kv_heads, int waves) {
     int hg = waves;
@@ -978,6 +1268,85 @@ int attention_float(void* stream, xs_dtype kv_dtype, const float* q, const void*
     return check_launch(what);
 }
 
+// The format's name as quant::kv_format_name gives it (src/quant/kv_format.cpp:22-31).
+const char* kv_format_name(xs_kv_format f) {
+    switch (f) {
+        case XS_KV_FLOAT: return "auto";
+        case XS_KV_I8: return "i8";
+        case XS_KV_TURBO4: return "turbo4";
+        case XS_KV_TURBO3: return "turbo3";
+        case XS_KV_TURBO2: return "turbo2";
+    }
+    return "?";
+}
+
+// Both quantized entry points: the formats' pair checked, int8/int8 to the matrix-core reader, the others to the
+// TurboQuant reader.
+int attention_quantized(void* stream, xs_kv_format kf, xs_kv_format vf, const float* q, const void* k_codes,
+                        const void* k_scales, const void* v_codes, const void* v_scales, float* out, int64_t tokens,
+                        int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t kv_len,
+                        const int64_t* kv_len_dev, float scale, float softcap, int64_t window, int causal,
+                        int64_t split, void* scratch, const char* what) {
+    const auto turbo_bits = [](xs_kv_format f) {
+        return f == XS_KV_TURBO4 ? 4 : f == XS_KV_TURBO3 ? 3 : f == XS_KV_TURBO2 ? 2 : 0;
+    };
+    const int kb = kf == XS_KV_I8 ? 8 : turbo_bits(kf), vb = vf == XS_KV_I8 ? 8 : turbo_bits(vf);
+    // The pairs kv_formats_supported admits besides float/float: int8/int8, a TurboQuant format for both, int8 keys
+    // with TurboQuant values (sycl_kernels.h:209-212).
+    if (kb == 0 || vb == 0 || !(kb == vb || (kb == 8 && vb != 8)))
+        return fail(XS_HIP_EUNSUPPORTED, std::string(what) + ": keys in " + kv_format_name(kf) + " with values in " +
+                                             kv_format_name(vf));
+    if (vb == 8)
+        return attention_i8(stream, q, k_codes, k_scales, v_codes, v_scales, out, tokens, q_heads, kv_heads, head_dim,
+                            kv_len, kv_len_dev, scale, softcap, window, causal, split, scratch, what);
+    if (tokens < 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || kv_len < 0 || window < 0 || split < 1 ||
+        q_heads % kv_heads != 0)
+        return fail(XS_HIP_EINVAL, std::string(what) + ": q [" + std::to_string(tokens) + ", " +
+                                       std::to_string(q_heads) + ", " + std::to_string(head_dim) + "] over " +
+                                       std::to_string(kv_len) + " keys of " + std::to_string(kv_heads) +
+                                       " KV heads, split " + std::to_string(split));
+    if (head_dim % 128 != 0)
+        return fail(XS_HIP_EINVAL, std::string(what) + ": a TurboQuant KV format needs a head_dim that is a multiple "
+                                                       "of 128, got " + std::to_string(head_dim));
+    if (tokens == 0) return XS_HIP_OK;
+    if ((causal || window > 0) && kv_len < tokens)
+        return fail(XS_HIP_EINVAL, std::string(what) + ": " + std::to_string(kv_len) + " keys for " +
+                                       std::to_string(tokens) + " queries");
+    if (kv_len == 0) return fail(XS_HIP_EINVAL, std::string(what) + ": no keys");
+    if (q == nullptr || k_codes == nullptr || k_scales == nullptr || v_codes == nullptr || v_scales == nullptr ||
+        out == nullptr)
+        return fail(XS_HIP_EINVAL, std::string(what) + ": null buffer");
+    if (split > 1 && scratch == nullptr)
+        return fail(XS_HIP_EINVAL, std::string(what) + ": split " + std::to_string(split) +
+                                       " needs xs_hip_attention_i8_scratch bytes of scratch");
+    if (split > kMaxSplit || tokens * kv_heads > 65535)
+        return fail(XS_HIP_EUNSUPPORTED, std::string(what) + ": launch too large");
+    if (!aligned16(q) || !aligned16(out) || !aligned16(k_codes) || !aligned16(v_codes) ||
+        reinterpret_cast<uintptr_t>(k_scales) % (kb == 8 ? 4 : 2) != 0 ||
+        reinterpret_cast<uintptr_t>(v_scales) % 2 != 0 ||
+        (split > 1 && reinterpret_cast<uintptr_t>(scratch) % 16 != 0))
+        return fail(XS_HIP_EINVAL, std::string(what) + ": q, out, codes and scratch must be 16-byte aligned, f32 "
+                                                       "scales 4-byte and f16 norms 2-byte aligned");
+    AttnArgs a{q, nullptr, nullptr, nullptr, nullptr, out, split > 1 ? static_cast<float*>(scratch) : nullptr, tokens,
+               q_heads, kv_heads, head_dim, kv_len, window, scale, softcap, causal ? 1 : 0, static_cast<int>(split), 1,
+               kv_len_dev};
+    const hipStream_t s = as_stream(stream);
+    const auto* kc = static_cast<const uint8_t*>(k_codes);
+    const auto* vc = static_cast<const uint8_t*>(v_codes);
+    const auto* vn = static_cast<const uint16_t*>(v_scales);
+    int rc;
+    if (vb == 4) rc = kb == 8 ? launch_turbo<8, 4>(s, a, kc, k_scales, vc, vn, what)
+                              : launch_turbo<4, 4>(s, a, kc, k_scales, vc, vn, what);
+    else if (vb == 3) rc = kb == 8 ? launch_turbo<8, 3>(s, a, kc, k_scales, vc, vn, what)
+                                   : launch_turbo<3, 3>(s, a, kc, k_scales, vc, vn, what);
+    else rc = kb == 8 ? launch_turbo<8, 2>(s, a, kc, k_scales, vc, vn, what)
+                      : launch_turbo<2, 2>(s, a, kc, k_scales, vc, vn, what);
+    if (rc != XS_HIP_OK || split == 1) return rc;
+    attention_combine_rows<<<static_cast<unsigned>(tokens * q_heads * (head_dim / kCombineDims)), 256, 0, s>>>(
+        static_cast<const float*>(scratch), out, static_cast<int>(split), head_dim, tokens * q_heads);
+    return check_launch(what);
+}
+
 }  // namespace
 
 extern "C" {
@@ -1036,6 +1405,28 @@ int xs_hip_attention_i8_noalloc(void* stream, const float* q, const void* k_code
     }
     return attention_i8(stream, q, k_codes, k_scales, v_codes, v_scales, out, tokens, q_heads, kv_heads, head_dim,
                         kv_len, nullptr, scale, softcap, window, causal, split, buf, what);
+}
+
+int xs_hip_attention_quantized(void* stream, xs_kv_format k_format, xs_kv_format v_format, const float* q,
+                               const void* k_codes, const void* k_scales, const void* v_codes, const void* v_scales,
+                               float* out, int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                               int64_t kv_len, float scale, float softcap, int64_t window, int causal, int64_t split,
+                               void* scratch) {
+    return attention_quantized(stream, k_format, v_format, q, k_codes, k_scales, v_codes, v_scales, out, tokens,
+                               q_heads, kv_heads, head_dim, kv_len, nullptr, scale, softcap, window, causal, split,
+                               scratch, "xs_hip_attention_quantized");
+}
+
+int xs_hip_attention_quantized_at(void* stream, xs_kv_format k_format, xs_kv_format v_format, const float* q,
+                                  const void* k_codes, const void* k_scales, const void* v_codes,
+                                  const void* v_scales, float* out, int64_t tokens, int64_t q_heads, int64_t kv_heads,
+                                  int64_t head_dim, int64_t kv_capacity, const int64_t* kv_len, float scale,
+                                  float softcap, int64_t window, int causal, int64_t split, void* scratch) {
+    if (kv_len == nullptr || reinterpret_cast<uintptr_t>(kv_len) % 8 != 0)
+        return fail(XS_HIP_EINVAL, "xs_hip_attention_quantized_at: kv_len must be an 8-byte aligned device int64");
+    return attention_quantized(stream, k_format, v_format, q, k_codes, k_scales, v_codes, v_scales, out, tokens,
+                               q_heads, kv_heads, head_dim, kv_capacity, kv_len, scale, softcap, window, causal, split,
+                               scratch, "xs_hip_attention_quantized_at");
 }
 
 }  // extern "C"

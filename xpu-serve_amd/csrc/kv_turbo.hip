@@ -26,103 +26,9 @@
 namespace xs_hip {
 namespace {
 
-constexpr int kGroup = 128;
-constexpr int kLanes = 16;       // lanes a group
-constexpr int kLaneValues = 8;   // values a lane
+using namespace turbo;
+
 constexpr int kGroupsPerBlock = kBlock / kLanes;
-
-// The rotation's sign flips before and after the transform: bit i % 64 of word i / 64 flips value i
-// (kv_turbo.h:27-28; format constants).
-constexpr uint64_t kSignsBefore[2] = {0x42f85949e46a0359ull, 0x49f250a9a4c63bbbull};
-constexpr uint64_t kSignsAfter[2] = {0x3f628fdc16acee90ull, 0xbea56562b7a5357aull};
-
-// The codebooks: Lloyd-Max magnitudes for a Gaussian of variance 1 / 128 and the borders between neighbours
-// (kv_turbo.h:39-56; format constants).
-template <int Bits>
-struct Book;
-template <>
-struct Book<2> {
-    static constexpr float mags[2] = {0.039994f, 0.133462f};
-    static constexpr float edges[1] = {0.086728f};
-};
-template <>
-struct Book<3> {
-    static constexpr float mags[4] = {0.021663f, 0.066822f, 0.118786f, 0.190207f};
-    static constexpr float edges[3] = {0.044243f, 0.092804f, 0.154496f};
-};
-template <>
-struct Book<4> {
-    static constexpr float mags[8] = {0.011349f, 0.034299f, 0.058050f, 0.083292f,
-                                      0.111036f, 0.143016f, 0.182877f, 0.241529f};
-    static constexpr float edges[7] = {0.022824f, 0.046174f, 0.070671f, 0.097164f, 0.127026f, 0.162947f, 0.212203f};
-};
-
-template <int Bits>
-constexpr int kMagnitudes = 1 << (Bits - 1);
-
-// fl32(e_j^2 * 128), squared in f64 (kv_turbo.h:57-62).
-template <int Bits>
-constexpr float edge_sq(int j) {
-    const double e = Book<Bits>::edges[j];
-    return static_cast<float>(e * e * kGroup);
-}
-
-// Sign masks (bit 31) of lane `lane`'s 8 values.
-__device__ __forceinline__ void sign_masks(const uint64_t* signs, int lane, uint32_t* mask) {
-    const uint32_t bits = static_cast<uint32_t>((lane < 8 ? signs[0] : signs[1]) >> (8 * (lane % 8))) & 0xffu;
-#pragma unroll
-    for (int e = 0; e < kLaneValues; ++e) mask[e] = ((bits >> e) & 1u) << 31;
-}
-
-__device__ __forceinline__ float flip(float v, uint32_t mask) { return __uint_as_float(__float_as_uint(v) ^ mask); }
-
-// The value of lane l ^ M of this lane's 16 (M = 1, 2, 4, 8).
-template <int M>
-__device__ __forceinline__ float xlane(float v) {
-    // The quad permutations as plain DPP moves (no old value to keep), which the compiler folds into their user.
-    if constexpr (M == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), dpp::kQuadXor1, 0xF, 0xF, true));
-    else if constexpr (M == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), dpp::kQuadXor2, 0xF, 0xF, true));
-    else return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1f | (M << 10)));  // bit mode, xor M
-}
-
-// The 16 lanes' values added pairwise, 1, 2, 4, 8 lanes apart: every lane ends with the same sum.
-__device__ __forceinline__ float sum_lanes(float s) {
-    s = s + xlane<1>(s);
-    s = s + xlane<2>(s);
-    s = s + xlane<4>(s);
-    return s + xlane<8>(s);
-}
-
-// Span 8 M of the butterflies: the lower lane of a pair takes a + b, the upper a - b (a the lower's value, b the
-// upper's). Each lane computes own + t * partner with t = +1 (lower) or -1 (upper) in one fused multiply-add, exact
-// since t * partner is: the upper lane so holds b - a = -(a - b), its value negated (round to nearest even commutes
-// with negation). A lane's values thus come out of the four spans negated when an odd number of its lane bits is set;
-// the caller folds that sign into the flips after the transform.
-template <int M>
-__device__ __forceinline__ void cross_span(float* v, float t) {
-#pragma unroll
-    for (int e = 0; e < kLaneValues; ++e) v[e] = fmaf(xlane<M>(v[e]), t, v[e]);
-}
-
-// The unnormalized Walsh-Hadamard transform of a group, on this lane's 8 values; returns the sign mask (bit 31) the
-// cross-lane spans left on them.
-__device__ __forceinline__ uint32_t butterflies(float* v, int lane) {
-#pragma unroll
-    for (int h = 1; h < kLaneValues; h *= 2) {
-#pragma unroll
-        for (int e = 0; e < kLaneValues; ++e) {
-            if (e & h) continue;
-            const float a = v[e], b = v[e + h];
-            v[e] = a + b;
-            v[e + h] = a - b;
-        }
-    }
-    cross_span<1>(v, (lane & 1) ? -1.0f : 1.0f);
-    cross_span<2>(v, (lane & 2) ? -1.0f : 1.0f);
-    cross_span<4>(v, (lane & 4) ? -1.0f : 1.0f);
-    cross_span<8>(v, (lane & 8) ? -1.0f : 1.0f);
-    return static_cast<uint32_t>(__builtin_popcount(lane & 15) & 1) << 31;
-}
 
 template <typename X>
 __device__ __forceinline__ void load_lane(const typename X::storage* x, float* v) {
@@ -226,8 +132,7 @@ __global__ __launch_bounds__(kDecBlock) void turbo_decode_kernel(const uint8_t* 
                                                               const uint16_t* __restrict__ norms,
                                                               typename Y::storage* __restrict__ out, int64_t groups) {
     constexpr int NC = 1 << Bits;
-    constexpr int NM = kMagnitudes<Bits>;
-    __shared__ float centroid[NC];
+    __shared__ float centroid_s[NC];
     const int lane = threadIdx.x % kLanes;
     const int64_t g0 = static_cast<int64_t>(blockIdx.x) * kDecGroupsPerBlock * kDecU + threadIdx.x / kLanes;
     // The groups' codes and norms are requested first, so their latency overlaps the codebook's staging.
@@ -250,8 +155,7 @@ __global__ __launch_bounds__(kDecBlock) void turbo_decode_kernel(const uint8_t* 
         }
     }
     if (threadIdx.x < NC) {
-        const int c = static_cast<int>(threadIdx.x);
-        centroid[c] = c >= NM ? Book<Bits>::mags[c - NM] : -Book<Bits>::mags[NM - 1 - c];
+        centroid_s[threadIdx.x] = centroid<Bits>(static_cast<int>(threadIdx.x));
     }
     __syncthreads();
 #pragma unroll
@@ -265,7 +169,7 @@ __global__ __launch_bounds__(kDecBlock) void turbo_decode_kernel(const uint8_t* 
             uint32_t code;
             if constexpr (Bits == 4) code = (packed[u] >> (4 * e)) & 15u;
             else code = ((packed[u] >> (2 * e)) & 3u) | (Bits == 3 ? ((high[u] >> e) & 1u) << 2 : 0u);
-            v[e] = centroid[code] * norm;
+            v[e] = centroid_s[code] * norm;
         }
         typename Y::storage* o = out + g * kGroup + lane * kLaneValues;
         if constexpr (sizeof(typename Y::storage) == 4) {
@@ -288,14 +192,7 @@ __global__ __launch_bounds__(kBlock) void turbo_rotate_kernel(const float* __res
     const float* xl = x + g * kGroup + lane * kLaneValues;
     unpack<F32>(ld128(xl), v);
     unpack<F32>(ld128(xl + 4), v + 4);
-    uint32_t mask[kLaneValues];
-    sign_masks(inverse ? kSignsAfter : kSignsBefore, lane, mask);
-#pragma unroll
-    for (int e = 0; e < kLaneValues; ++e) v[e] = flip(v[e], mask[e]);
-    const uint32_t parity = butterflies(v, lane);
-    sign_masks(inverse ? kSignsBefore : kSignsAfter, lane, mask);
-#pragma unroll
-    for (int e = 0; e < kLaneValues; ++e) v[e] = flip(v[e] * 0.08838834764831845f, mask[e] ^ parity);
+    rotate8(v, lane, inverse);
     float* yl = y + g * kGroup + lane * kLaneValues;
     st128(yl, pack<F32>(v));
     st128(yl + 4, pack<F32>(v + 4));

@@ -124,6 +124,10 @@ _SIGS = {
     "xs_hip_kv_store_pair": [_P, _INT, _P, _P, _INT, _P, _P, _I64, _I64, _P, _I64, _I64],
     "xs_hip_attention": [_P, _INT, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _F, _I64, _INT, _I64, _P],
     "xs_hip_attention_at": [_P, _INT, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _F, _F, _I64, _INT, _I64, _P],
+    "xs_hip_attention_quantized": [_P, _INT, _INT, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _F, _I64,
+                                   _INT, _I64, _P],
+    "xs_hip_attention_quantized_at": [_P, _INT, _INT, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _F,
+                                      _F, _I64, _INT, _I64, _P],
     "xs_hip_attention_i8_split": [_I64, _I64, _I64],
     "xs_hip_attention_i8_scratch": [_I64, _I64, _I64, _I64],
 }
@@ -389,6 +393,27 @@ def attention(q: DeviceTensor, k: DeviceTensor, v: DeviceTensor, kv_heads: int, 
     call("xs_hip_attention", stream, k.dtype, C.c_void_p(q.ptr), C.c_void_p(k.ptr), C.c_void_p(v.ptr),
          C.c_void_p(out.ptr), tokens, q_heads, kv_heads, d, kv_len, C.c_float(scale), C.c_float(softcap), window,
          int(causal), split, C.c_void_p(scratch.ptr) if scratch else None)
+    if scratch is not None:
+        synchronize()  # the scratch is freed when this returns
+    return out
+
+
+def attention_quantized(q: DeviceTensor, k_format: int, k_codes: DeviceTensor, k_scales: DeviceTensor,
+                        v_format: int, v_codes: DeviceTensor, v_scales: DeviceTensor, kv_heads: int, kv_len: int,
+                        scale: float, softcap: float = 0.0, window: int = 0, causal: bool = True, split: int = 0,
+                        stream=None) -> DeviceTensor:
+    """Decode attention of q [T, Hq, D] (f32) over a quantized cache of kv_len keys, each stream (codes, scales or
+    norms) as quantize_kv writes it in its format (xs_hip_attention_quantized). split 0: the library's suggestion."""
+    tokens, q_heads, d = q.shape
+    if split <= 0:
+        split = int(lib().xs_hip_attention_i8_split(tokens, kv_heads, kv_len))
+    out = DeviceTensor.empty(F32, q.shape)
+    nbytes = int(lib().xs_hip_attention_i8_scratch(tokens, q_heads, d, split))
+    scratch = DeviceBuffer(nbytes) if nbytes else None
+    call("xs_hip_attention_quantized", stream, k_format, v_format, C.c_void_p(q.ptr), C.c_void_p(k_codes.ptr),
+         C.c_void_p(k_scales.ptr), C.c_void_p(v_codes.ptr), C.c_void_p(v_scales.ptr), C.c_void_p(out.ptr), tokens,
+         q_heads, kv_heads, d, kv_len, C.c_float(scale), C.c_float(softcap), window, int(causal), split,
+         C.c_void_p(scratch.ptr) if scratch else None)
     if scratch is not None:
         synchronize()  # the scratch is freed when this returns
     return out
