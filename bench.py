@@ -491,6 +491,59 @@ def op_attention_i8(inputs):
               2, "attention_i8_rows")
 
 
+def op_attention_f16(inputs):
+    """The same decode step over config 4's K and V held as f16 rows (the Float KV format at f16 precision), through
+    xs_hip_attention."""
+    rows, dim, k0, v0 = inputs
+    kv_heads, q_heads = 8, 32
+    kv_len = rows // kv_heads
+    rng = np.random.default_rng(0x5EED0005)
+    q0 = X.DeviceTensor.from_numpy(rng.standard_normal((1, q_heads, dim)).astype(np.float32))
+    split = int(X.lib().xs_hip_attention_i8_split(1, kv_heads, kv_len))
+    nscratch = int(X.lib().xs_hip_attention_i8_scratch(1, q_heads, dim, split))
+
+    def mk():
+        s = (dcopy(k0), dcopy(v0), dcopy(q0), X.DeviceTensor.empty(X.F32, (1, q_heads, dim)), X.DeviceBuffer(nscratch))
+        need(s[0], rows * dim * 2, "attention f16 keys")
+        return s
+
+    def go(s, stream):
+        k, v, q, out, scratch = s
+        X.call("xs_hip_attention", stream, X.F16, vp(q), vp(k), vp(v), vp(out), 1, q_heads, kv_heads, dim, kv_len,
+               C.c_float(1.0 / math.sqrt(dim)), C.c_float(0.0), 0, 1, split, C.c_void_p(scratch.ptr))
+    return Op("attention_f16_decode", W.ALGO_BYTES["attention_f16_decode"], W.ALGO_BYTES["attention_f16_decode"], mk,
+              go, 2, "attention_float_rows")
+
+
+def op_attention_turbo(inputs, int8_keys=False):
+    """The same decode step over config 4's K and V as turbo4 (or int8 keys with turbo4 values), through
+    xs_hip_attention_quantized."""
+    rows, dim, k0, v0 = inputs
+    kv_heads, q_heads = 8, 32
+    kv_len = rows // kv_heads
+    kc0, ks0 = X.quantize_kv(k0) if int8_keys else X.turbo_quantize(k0, 4)
+    vc0, vs0 = X.turbo_quantize(v0, 4)
+    rng = np.random.default_rng(0x5EED0005)
+    q0 = X.DeviceTensor.from_numpy(rng.standard_normal((1, q_heads, dim)).astype(np.float32))
+    split = int(X.lib().xs_hip_attention_i8_split(1, kv_heads, kv_len))
+    nscratch = int(X.lib().xs_hip_attention_i8_scratch(1, q_heads, dim, split))
+    kf = X.KV_I8 if int8_keys else X.KV_TURBO4
+    name = "attention_i8_turbo4_decode" if int8_keys else "attention_turbo4_decode"
+
+    def mk():
+        s = (dcopy(kc0), dcopy(ks0), dcopy(vc0), dcopy(vs0), dcopy(q0), X.DeviceTensor.empty(X.F32, (1, q_heads, dim)),
+             X.DeviceBuffer(nscratch))
+        need(s[2], rows * dim // 2, "attention v codes")
+        return s
+
+    def go(s, stream):
+        kc, ks, vc, vs, q, out, scratch = s
+        X.call("xs_hip_attention_quantized", stream, kf, X.KV_TURBO4, vp(q), vp(kc), vp(ks), vp(vc), vp(vs), vp(out),
+               1, q_heads, kv_heads, dim, kv_len, C.c_float(1.0 / math.sqrt(dim)), C.c_float(0.0), 0, 1, split,
+               C.c_void_p(scratch.ptr))
+    return Op(name, W.ALGO_BYTES[name], W.ALGO_BYTES[name], mk, go, 2, "attention_turbo_rows")
+
+
 def op_copy(n=256 << 20, name="copy"):
     """Bytes per call n (default 256 MiB): the kernel the hardware byte counters are calibrated against, and, at
     other sizes (`--only copy_10MiB` etc.), the ceiling a streaming op of that size can reach."""
@@ -509,7 +562,8 @@ def op_copy(n=256 << 20, name="copy"):
 
 
 OP_ORDER = ["swiglu_bias", "swiglu_bias_strided", "rmsnorm_residual", "rmsnorm_residual_separate", "softmax_masked",
-            "argmax", "argmax_one_launch", "rope_qk", "rope_qk_separate", "kv_quantize", "kv_dequantize", "attention_i8_decode", "layer_norm", "l2_clip",
+            "argmax", "argmax_one_launch", "rope_qk", "rope_qk_separate", "kv_quantize", "kv_dequantize", "attention_i8_decode",
+            "attention_f16_decode", "attention_turbo4_decode", "attention_i8_turbo4_decode", "layer_norm", "l2_clip",
             "reduce_sum_rows", "reduce_sum_cols", "unary_softcap", "kv_turbo4_quantize", "kv_turbo4_dequantize",
             "topk_shortlist", "topk_moe_router", "topk_draft_candidates"]
 
@@ -522,7 +576,9 @@ def build_ops(only):
         yield op_copy(int(m.group(1)) << (10 if m.group(2) == "KiB" else 20), name)
     kv = None
     for name in names:
-        if name in ("kv_quantize", "kv_dequantize", "attention_i8_decode", "kv_turbo4_quantize",
+        if name in ("kv_quantize", "kv_dequantize", "attention_i8_decode", "attention_f16_decode",
+                    "attention_turbo4_decode",
+                    "attention_i8_turbo4_decode", "kv_turbo4_quantize",
                     "kv_turbo4_dequantize") and kv is None:
             kv = _kv_inputs()
         yield {"swiglu_bias": op_swiglu, "swiglu_bias_strided": op_swiglu_strided, "rmsnorm_residual": op_rmsnorm,
@@ -531,7 +587,10 @@ def build_ops(only):
                "argmax_one_launch": op_argmax_one_launch, "rope_qk": op_rope,
                "rope_qk_separate": lambda: op_rope(True), "copy": op_copy,
                "kv_quantize": lambda: op_kv_quantize(kv), "kv_dequantize": lambda: op_kv_dequantize(kv),
-               "attention_i8_decode": lambda: op_attention_i8(kv), "unary_softcap": op_unary_softcap,
+               "attention_i8_decode": lambda: op_attention_i8(kv),
+               "attention_f16_decode": lambda: op_attention_f16(kv),
+               "attention_turbo4_decode": lambda: op_attention_turbo(kv),
+               "attention_i8_turbo4_decode": lambda: op_attention_turbo(kv, True), "unary_softcap": op_unary_softcap,
                "layer_norm": lambda: op_row_norms("layer_norm"), "l2_clip": lambda: op_row_norms("l2_clip"),
                "reduce_sum_rows": lambda: op_row_norms("reduce_sum_rows"),
                "reduce_sum_cols": lambda: op_row_norms("reduce_sum_cols"),

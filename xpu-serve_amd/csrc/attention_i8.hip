@@ -592,248 +592,229 @@ __global__ __launch_bounds__(256) void attention_combine_rows(const float* part,
     }
 }
 
-// ---- Decode attention over a float cache (f16 or f32 rows) --------------------------------------------------------
+// ---- Decode attention over float and TurboQuant caches ------------------------------------------------------------
 //
-// The reader of the float KV format (SessionOptions::kv Float: f16 rows at f16 precision, f32 at f32; reference
-// src/quant/kv_format.h:12, sycl_backend.cpp:2224-2228): keys and values [N, Hkv, D] of T. Semantics as the int8
-// reader above over the values the rows hold. Launcher replaced: sycl_be::attention_rows<KV> with attention_combine
-// (src/backend/sycl/sycl_kernels.h, attention_rows / attention_combine), KV = half or float.
+// One reader for the pairs of formats the int8 reader above does not take (reference src/backend/sycl/
+// sycl_kernels.h:209-212, 236-240; rows as sycl_kv_rows.h's FloatRows, I8Rows and TurboRows):
+//  - the Float KV format (SessionOptions::kv Float: f16 rows at f16 precision, f32 at f32; src/quant/kv_format.h:12,
+//    sycl_backend.cpp:2224-2228): keys and values [N, Hkv, D] of f16 or f32, sycl_be::attention_rows<KV>;
+//  - keys and values in the same TurboQuant format, or int8 keys with TurboQuant values: sycl_be::
+//    attention_rows_quantized.
+// Semantics: cpu_ref::attention over the values the cache stores (the rows as they are; quant::round_trip_kv: a
+// TurboQuant row's decoded values rotated back, an int8 row's fl32(code * scale)). A TurboQuant format keeps its rows
+// rotated (each group of 128 values: sign flips, Walsh-Hadamard, 1 / sqrt(128), sign flips), an orthogonal map: the
+// query rotated the same way has the originals' dot products with the stored keys, and the weighted sum of stored
+// values, rotated back, is the weighted sum of the originals (up to f32 rounding: the reference's device tolerance for
+// a quantized cache, tests/unit/backend/device_attention.cpp:23-27).
 //
-// Layout: one 256-thread workgroup per (token, KV head, key split), for all G query heads of that KV head, so each key
-// and value row is read once for them. The split's keys go in tiles of 256: thread i scores key i of the tile for the
-// G heads (its row's dot products with q, which sits in LDS, f32 fused multiply-adds), the tile's max and sum of
-// exponentials per head come from wave reductions and one LDS stage, and the weighted sum runs with thread t holding
-// four dims of every head over the tile's keys t / (D / 4) + k (1024 / D), k = 0, 1, ...: the value rows' loads of a
-// wave cover whole rows. One online softmax per head; the partial sums of the 1024 / D key subsets add up in LDS at the
-// end. With one split the workgroup writes the output; with several, partial rows as the int8 reader writes them.
-constexpr int kFloatTile = 256;
+// Layout: one 256-thread workgroup per (token, KV head, key split) for all G query heads, so each key and value row is
+// read once for them; the split's keys in tiles of 256, one online softmax per head.
+//  - Scores: 8 lanes a key, lane l the LV values LV l .. LV l + LV - 1 of each group of 8 LV values of the row (LV =
+//    16, or 8 for head_dim 64; for TurboQuant two of the format's 8-value lanes), 8 keys at once a wave, each lane's
+//    loads contiguous. A lane's dot products with the (rotated) query, held in registers where it fits, sum
+//    q[d] * x_d over its values (x: the row's value, an int8 code, or a TurboQuant centroid, times the group's norm);
+//    int8 keys take the row's scale at the end; 3 DPP steps add the 8 lanes' sums. The scores go through LDS to
+//    thread-per-key form for the tile's max and exponentials.
+//  - Weighted sum: thread t holds 8 dims of every head (for TurboQuant, the 8 values format lane t % 16 of a group
+//    stores) over the tile's keys t / (D / 8) + kS u (kS = 2048 / D key subsets), u = 0, 1, ...: acc += (p * f) * x
+//    with f the group's norm (1 for float rows).
+//  - TurboQuant codes become centroids through an LDS table indexed by a byte of codes (turbo4: a byte is 2 codes, one
+//    64-bit read; turbo2: 4 codes, one 128-bit read; turbo3: 2 low-bit pairs and their 2 third bits, 6 bits, one 64-bit
+//    read).
+// The value rows a thread adds up are loaded 16 (f32: 8) at a time, the first of them before the scores so that their
+// latency overlaps that work. At the end each head's sums add up over the key subsets (and, for TurboQuant values, 16
+// threads a group of 128 rotate them back); with one split the workgroup writes the output, with several the partial
+// rows with their (max, sum) as the int8 reader writes them.
+constexpr int kRowsTile = 256;
 
-template <typename KV, int G, int D, bool CAP>
-__global__ __launch_bounds__(256) void attention_float_rows(AttnArgs a, const void* kp, const void* vp) {
-    constexpr int kS = 1024 / D;   // key subsets of the weighted sum
-    constexpr int kD4 = D / 4;     // 4-dim groups a row
-    constexpr int kEl = 16 / sizeof(typename KV::storage);  // elements of one 128-bit load
-    __shared__ __align__(16) float q_s[G][D];
-    __shared__ float p_s[G][kFloatTile];
-    __shared__ float red[2][4][G];
-    __shared__ __align__(16) float acc_s[kS][G][D];
-    const auto* kr = static_cast<const typename KV::storage*>(kp);
-    const auto* vr = static_cast<const typename KV::storage*>(vp);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t t = blockIdx.y / a.kv_heads;
-    const int64_t kvh = blockIdx.y - t * a.kv_heads;
-    const int sp = blockIdx.x;
+// The storage formats, as template arguments: TurboQuant bits 2, 3, 4; 8: int8 codes; 16: f16; 32: f32.
+constexpr bool is_turbo(int f) { return f <= 4; }
+// Bytes of 8 LV values of a row in format f (one group: 128 values for TurboQuant).
+constexpr int group_bytes_of(int f, int lv) { return is_turbo(f) ? turbo::group_bytes(f) : 8 * lv * f / 8; }
 
-    for (int i = tid; i < G * D; i += 256) q_s[i / D][i % D] = a.q[(t * a.q_heads + kvh * G + i / D) * D + i % D];
-
-    int64_t first, last;
-    key_range(a, keys_of(a), t, first, last);
-    const int64_t len = last >= first ? last - first + 1 : 0;
-    const int64_t per = (len + a.split - 1) / a.split;
-    const int64_t k0 = first + sp * per;
-    const int64_t k1 = k0 + per - 1 < last ? k0 + per - 1 : last;
-    float m[G], l[G], acc[G][4];
+// The byte-indexed decode table of a TurboQuant format in LDS (entry i: the centroids of the codes byte i holds, as
+// above), filled by the workgroup.
+template <int Bits>
+struct TurboTable {
+    static constexpr int kEntries = Bits == 3 ? 64 : 256;
+    static constexpr int kWidth = Bits == 2 ? 4 : 2;  // centroids an entry
+    __device__ static void fill(float* t, int tid) {
+        for (int i = tid; i < kEntries; i += 256) {
+            if constexpr (Bits == 4) {
+                t[2 * i] = turbo::centroid<4>(i & 15);
+                t[2 * i + 1] = turbo::centroid<4>(i >> 4);
+            } else if constexpr (Bits == 2) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        m[g] = -INFINITY;
-        l[g] = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[g][e] = 0.0f;
-    }
-    const int dg = tid % kD4, sub = tid / kD4;
-    __syncthreads();
-    for (int64_t j0 = k0; j0 <= k1; j0 += kFloatTile) {
-        // Scores of key j0 + tid for every head.
-        const int64_t j = j0 + tid;
-        float s[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) s[g] = 0.0f;
-        if (j <= k1) {
-            const auto* row = kr + (j * a.kv_heads + kvh) * D;
-#pragma unroll 4
-            for (int c = 0; c < D; c += kEl) {
-                float kf[kEl];
-                unpack<KV>(ld128(row + c), kf);
-#pragma unroll
-                for (int g = 0; g < G; ++g)
-#pragma unroll
-                    for (int e = 0; e < kEl; ++e) s[g] = fmaf(q_s[g][c + e], kf[e], s[g]);
-            }
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float x = s[g] * a.scale;
-                if constexpr (CAP) x = a.softcap * tanhf(x / a.softcap);
-                s[g] = x;
-            }
-        } else {
-#pragma unroll
-            for (int g = 0; g < G; ++g) s[g] = -INFINITY;
-        }
-        // The tile's max per head, then exponentials and their sum.
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float w = wave_reduce<OpMax>(s[g], -INFINITY);
-            if (lane == 0) red[0][wave][g] = w;
-        }
-        __syncthreads();
-        float c[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float mt = fmaxf(fmaxf(red[0][0][g], red[0][1][g]), fmaxf(red[0][2][g], red[0][3][g]));
-            const float mn = fmaxf(m[g], mt);
-            c[g] = m[g] == -INFINITY ? 0.0f : __expf(m[g] - mn);
-            m[g] = mn;
-            const float p = s[g] == -INFINITY ? 0.0f : __expf(s[g] - mn);
-            p_s[g][tid] = p;
-            const float w = wave_reduce<OpSum>(p, 0.0f);
-            if (lane == 0) red[1][wave][g] = w;
-        }
-        __syncthreads();
-        // The weighted sum of the tile's value rows.
-        const int64_t n = k1 - j0 + 1 < kFloatTile ? k1 - j0 + 1 : kFloatTile;
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            l[g] = l[g] * c[g] + ((red[1][0][g] + red[1][1][g]) + (red[1][2][g] + red[1][3][g]));
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[g][e] *= c[g];
-        }
-        for (int k = sub; k < n; k += kS) {
-            const auto* row = vr + ((j0 + k) * a.kv_heads + kvh) * D + 4 * dg;
-            float vf[4];
-            if constexpr (sizeof(typename KV::storage) == 4) {
-                unpack<KV>(ld128(row), vf);
+                for (int e = 0; e < 4; ++e) t[4 * i + e] = turbo::centroid<2>((i >> (2 * e)) & 3);
             } else {
-                const uint2 w2 = *reinterpret_cast<const uint2*>(row);
-                vf[0] = KV::load(static_cast<uint16_t>(w2.x & 0xffffu));
-                vf[1] = KV::load(static_cast<uint16_t>(w2.x >> 16));
-                vf[2] = KV::load(static_cast<uint16_t>(w2.y & 0xffffu));
-                vf[3] = KV::load(static_cast<uint16_t>(w2.y >> 16));
-            }
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float p = p_s[g][k];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
+                t[2 * i] = turbo::centroid<3>((i & 3) | (((i >> 4) & 1) << 2));
+                t[2 * i + 1] = turbo::centroid<3>(((i >> 2) & 3) | (((i >> 5) & 1) << 2));
             }
         }
-        __syncthreads();  // p_s and red are rewritten by the next tile
     }
-    // The key subsets' sums add up; then the output, or the partial row with its (max, sum).
+    // The 8 centroids of one format lane's codes (turbo::LaneCodes' low and high words).
+    __device__ static void decode8(const float* t, uint32_t low, uint32_t high, float* x) {
+        if constexpr (Bits == 4) {
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-        *reinterpret_cast<u32x4*>(&acc_s[sub][g][4 * dg]) =
-            u32x4{__float_as_uint(acc[g][0]), __float_as_uint(acc[g][1]), __float_as_uint(acc[g][2]),
-                  __float_as_uint(acc[g][3])};
-    __syncthreads();
-    for (int i = tid; i < G * D; i += 256) {
-        const int g = i / D, d = i % D;
-        float sum = 0.0f;
+            for (int i = 0; i < 4; ++i) {
+                const float2 v = reinterpret_cast<const float2*>(t)[(low >> (8 * i)) & 0xffu];
+                x[2 * i] = v.x;
+                x[2 * i + 1] = v.y;
+            }
+        } else if constexpr (Bits == 2) {
 #pragma unroll
-        for (int q = 0; q < kS; ++q) sum += acc_s[q][g][d];
-        const int64_t hh = kvh * G + g;
-        if (a.part == nullptr) {
-            a.out[(t * a.q_heads + hh) * D + d] = sum / l[g];
+            for (int i = 0; i < 2; ++i) {
+                const float4 v = reinterpret_cast<const float4*>(t)[(low >> (8 * i)) & 0xffu];
+                x[4 * i] = v.x;
+                x[4 * i + 1] = v.y;
+                x[4 * i + 2] = v.z;
+                x[4 * i + 3] = v.w;
+            }
         } else {
-            const int64_t pi = (t * a.q_heads + hh) * a.split + sp;
-            a.part[pi * D + d] = sum;
-            if (d == 0) {
-                float* ml = a.part + a.tokens * a.q_heads * a.split * D + 2 * pi;
-                ml[0] = m[g];
-                ml[1] = l[g];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t idx = ((low >> (4 * i)) & 15u) | (((high >> (2 * i)) & 3u) << 4);
+                const float2 v = reinterpret_cast<const float2*>(t)[idx];
+                x[2 * i] = v.x;
+                x[2 * i + 1] = v.y;
             }
         }
     }
-}
+};
 
-template <typename KV, int G>
-int launch_float_g(hipStream_t s, const AttnArgs& a, const void* k, const void* v) {
-    const dim3 grid(static_cast<unsigned>(a.split), static_cast<unsigned>(a.tokens * a.kv_heads));
-    const bool cap = a.softcap > 0.0f;
-    switch (a.head_dim) {
-        case 64:
-            if (cap) attention_float_rows<KV, G, 64, true><<<grid, 256, 0, s>>>(a, k, v);
-            else attention_float_rows<KV, G, 64, false><<<grid, 256, 0, s>>>(a, k, v);
-            break;
-        case 128:
-            if (cap) attention_float_rows<KV, G, 128, true><<<grid, 256, 0, s>>>(a, k, v);
-            else attention_float_rows<KV, G, 128, false><<<grid, 256, 0, s>>>(a, k, v);
-            break;
-        case 256:
-            if (cap) attention_float_rows<KV, G, 256, true><<<grid, 256, 0, s>>>(a, k, v);
-            else attention_float_rows<KV, G, 256, false><<<grid, 256, 0, s>>>(a, k, v);
-            break;
-        default:
-            return fail(XS_HIP_EUNSUPPORTED, "xs_hip_attention: head_dim " + std::to_string(a.head_dim) +
-                                                 " (supported: 64, 128, 256)");
-    }
-    return check_launch("xs_hip_attention");
-}
-
-template <typename KV>
-int launch_float(hipStream_t s, const AttnArgs& a, const void* k, const void* v) {
-    switch (a.q_heads / a.kv_heads) {
-        case 1: return launch_float_g<KV, 1>(s, a, k, v);
-        case 2: return launch_float_g<KV, 2>(s, a, k, v);
-        case 3: return launch_float_g<KV, 3>(s, a, k, v);
-        case 4: return launch_float_g<KV, 4>(s, a, k, v);
-        case 5: return launch_float_g<KV, 5>(s, a, k, v);
-        case 6: return launch_float_g<KV, 6>(s, a, k, v);
-        case 7: return launch_float_g<KV, 7>(s, a, k, v);
-        case 8: return launch_float_g<KV, 8>(s, a, k, v);
-        default:
-            return fail(XS_HIP_EUNSUPPORTED, "xs_hip_attention: " + std::to_string(a.q_heads / a.kv_heads) +
-                                                 " query heads per KV head (supported: 1 to 8)");
+// Widens n 16-bit or 32-bit float values held in raw words.
+template <int F>
+__device__ __forceinline__ void widen_words(const uint32_t* w, float* x, int n) {
+#pragma unroll
+    for (int i = 0; i < n; ++i) {
+        if constexpr (F == 16) x[i] = f16_to_f32(static_cast<uint16_t>((w[i / 2] >> (16 * (i & 1))) & 0xffffu));
+        else x[i] = __uint_as_float(w[i]);
     }
 }
 
-// ---- Decode attention over TurboQuant values, with TurboQuant or int8 keys ---------------------------------------
-//
-// The readers of the pairs of quantized formats other than int8/int8 that the reference attends over: keys and values
-// in the same TurboQuant format, or int8 keys with TurboQuant values (reference src/backend/sycl/sycl_kernels.h:
-// 209-212, 238; sycl_kernels.cpp attention_rows_quantized; rows read as sycl_kv_rows.h's I8Rows and TurboRows).
-// Semantics: cpu_ref::attention over the values the cache stores (quant::round_trip_kv: a TurboQuant row's decoded
-// values rotated back, an int8 row's fl32(code * scale)), computed where the rows are stored: a TurboQuant format keeps
-// its rows rotated (each group of 128 values: sign flips, Walsh-Hadamard, 1 / sqrt(128), sign flips), an orthogonal
-// map, so the query rotated the same way has the originals' dot products with the stored keys, and the weighted sum of
-// stored values, rotated back, is the weighted sum of the originals (up to f32 rounding: the reference's device
-// tolerance for a quantized cache, tests/unit/backend/device_attention.cpp:23-27).
-//
-// Layout: as the float reader above -- one 256-thread workgroup per (token, KV head, key split) for all G query heads,
-// tiles of 256 keys with thread i scoring key i, an online softmax per head -- with these readers:
-//  - keys, TurboQuant: a row's groups of 128 codes (16 * bits bytes each, 16-byte loads) and their f16 norms; a
-//    group's dot product with the rotated query sums q_r[d] * centroid[code_d], times the group's norm;
-//  - keys, int8: 16 codes a 16-byte load, the dot product with the query times the row's scale;
-//  - values, TurboQuant: thread t holds 8 dims of every head, the 8 values lane t % 16 of a group stores (one 32-bit
-//    word of nibbles, or a 16-bit word of 2-bit codes and for turbo3 one byte of third bits), over the tile's keys
-//    t / (D / 8) + k (2048 / D), k = 0, 1, ...; centroid[code] * norm.
-// The centroids sit in LDS. At the end each head's sums add up over the key subsets, and 16 threads a group of 128
-// rotate them back (the butterflies across 16 lanes) before the output or the partial row is written.
-constexpr int kTurboTile = 256;
+// A key lane's LV values of one group, as stored: TurboQuant format lanes 2 l and 2 l + 1 (turbo4: 8 bytes; turbo2:
+// 4 bytes; turbo3: those 4 low-bit bytes and 2 third-bit bytes); int8: LV codes; f16 / f32: LV values.
+template <int F, int LV>
+struct KeyLane {
+    static constexpr int kWords = is_turbo(F) ? 2 : LV * F / 32;
+    uint32_t w[kWords];
+    __device__ __forceinline__ void load(const uint8_t* gc, int l8) {
+        if constexpr (F == 4) {
+            const uint2 v = *reinterpret_cast<const uint2*>(gc + 8 * l8);
+            w[0] = v.x;
+            w[1] = v.y;
+        } else if constexpr (F == 3 || F == 2) {
+            w[0] = *reinterpret_cast<const uint32_t*>(gc + 4 * l8);
+            w[1] = F == 3 ? *reinterpret_cast<const uint16_t*>(gc + turbo::kGroup / 4 + 2 * l8) : 0u;
+        } else if constexpr (kWords == 2) {
+            const uint2 v = *reinterpret_cast<const uint2*>(gc + 8 * l8);
+            w[0] = v.x;
+            w[1] = v.y;
+        } else {
+#pragma unroll
+            for (int i = 0; i < kWords / 4; ++i) {
+                const u32x4 v = ld128(gc + 4 * kWords * l8 + 16 * i);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) w[4 * i + j] = v[j];
+            }
+        }
+    }
+    // The lane's LV values (centroids, int8 codes as floats, or the floats).
+    __device__ __forceinline__ void decode(const float* t, float* x) const {
+        if constexpr (F == 8) {
+#pragma unroll
+            for (int b = 0; b < LV; ++b) x[b] = byte_f32(w[b / 4], b % 4);
+        } else if constexpr (F == 16 || F == 32) {
+            widen_words<F>(w, x, LV);
+        } else if constexpr (F == 4) {
+            TurboTable<4>::decode8(t, w[0], 0, x);
+            TurboTable<4>::decode8(t, w[1], 0, x + 8);
+        } else if constexpr (F == 2) {
+            TurboTable<2>::decode8(t, w[0] & 0xffffu, 0, x);
+            TurboTable<2>::decode8(t, w[0] >> 16, 0, x + 8);
+        } else {
+            TurboTable<3>::decode8(t, w[0] & 0xffffu, w[1] & 0xffu, x);
+            TurboTable<3>::decode8(t, w[0] >> 16, w[1] >> 8, x + 8);
+        }
+    }
+};
 
-// KB: 8 for int8 keys, else the keys' TurboQuant bits; VB: the values' TurboQuant bits.
-template <int KB, int VB, int G, int D, bool CAP>
-__global__ __launch_bounds__(256) void attention_turbo_rows(AttnArgs a, const uint8_t* kc, const void* ks,
-                                                            const uint8_t* vc, const uint16_t* vn) {
+// A value thread's 8 dims of one row, as stored: a TurboQuant format lane's codes and the group's f16 norm, or 8 f16 /
+// f32 values.
+template <int F>
+struct ValueSlice {
+    static constexpr int kWords = is_turbo(F) ? 2 : F / 4;
+    uint32_t w[kWords];
+    uint32_t norm = 0;
+    // gc: the row's group of this thread's dims; vlane: their slice of it; nb: the group's norm.
+    __device__ __forceinline__ void load(const uint8_t* gc, int vlane, const uint16_t* nb) {
+        if constexpr (is_turbo(F)) {
+            turbo::LaneCodes<F> lc;
+            lc.load(gc, vlane);
+            w[0] = lc.low;
+            w[1] = lc.high;
+            norm = *nb;
+        } else {
+#pragma unroll
+            for (int i = 0; i < kWords / 4; ++i) {
+                const u32x4 v = ld128(gc + 4 * kWords * vlane + 16 * i);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) w[4 * i + j] = v[j];
+            }
+        }
+    }
+    // The 8 values, to be multiplied by factor().
+    __device__ __forceinline__ void decode(const float* t, float* x) const {
+        if constexpr (is_turbo(F)) TurboTable<F>::decode8(t, w[0], w[1], x);
+        else widen_words<F>(w, x, 8);
+    }
+    __device__ __forceinline__ float factor() const {
+        if constexpr (is_turbo(F)) return f16_to_f32(static_cast<uint16_t>(norm));
+        else return 1.0f;
+    }
+};
+
+// KF, VF: the keys' and the values' formats (both 16 or both 32; or VF TurboQuant with KF the same or 8).
+template <int KF, int VF, int G, int D, bool CAP>
+__global__ __launch_bounds__(256) void attention_rows_kernel(AttnArgs a, const uint8_t* kc, const void* ks,
+                                                             const uint8_t* vc, const uint16_t* vn) {
     using namespace turbo;
-    static_assert(KB == 8 || KB == VB, "keys int8 or in the values' format");
-    static_assert(D % kGroup == 0, "TurboQuant rows are whole groups of 128");
-    constexpr int kNG = D / kGroup;        // groups a row
-    constexpr int kD8 = D / kLaneValues;   // 8-dim slices a row
-    constexpr int kS = 256 / kD8;          // key subsets of the weighted sum
-    constexpr int kVGB = group_bytes(VB);  // bytes of a value group's codes
+    static_assert((KF == VF && !is_turbo(KF) && KF != 8) || (is_turbo(VF) && (KF == VF || KF == 8)), "format pair");
+    static_assert(!is_turbo(VF) || D % kGroup == 0, "TurboQuant rows are whole groups of 128");
+    constexpr int kLV = D == 64 ? 8 : 16;   // values a key lane takes of each group
+    constexpr int kGV = 8 * kLV;            // values a group
+    constexpr int kNG = D / kGV;            // groups a row
+    constexpr int kD8 = D / kLaneValues;    // 8-dim slices a row
+    constexpr int kS = 256 / kD8;           // key subsets of the weighted sum
+    constexpr int kRowsPerThread = kRowsTile / kS;  // value rows a thread adds up a tile (8 to 64)
+    // Of them, loaded together: about 32 words of registers.
+    constexpr int kVB = 32 / ValueSlice<VF>::kWords < 16 ? 32 / ValueSlice<VF>::kWords : 16;
+    constexpr int kVPref = kVB < kRowsPerThread ? kVB : kRowsPerThread;
+    constexpr int kSets = 256 / 8;          // 8-lane sets that score keys
+    constexpr int kKeysPerSet = kRowsTile / kSets;
+    // Keys a set loads at once: about 32 words of registers.
+    constexpr int kKW = kNG * KeyLane<KF, kLV>::kWords;
+    constexpr int kKB = kKW >= 32 ? 1 : 32 / kKW < 8 ? 32 / kKW : 8;
+    constexpr bool kQReg = G * kNG * kLV <= 64;  // the query values a key lane needs, in registers
+    constexpr int kKGB = group_bytes_of(KF, kLV);
+    constexpr int kVGB = group_bytes_of(VF, kLV);
+    constexpr int kTab = is_turbo(VF) ? TurboTable<(is_turbo(VF) ? VF : 4)>::kEntries *
+                                            TurboTable<(is_turbo(VF) ? VF : 4)>::kWidth
+                                      : 1;
     __shared__ __align__(16) float q_s[G][D];
-    __shared__ float p_s[G][kTurboTile];
+    __shared__ float p_s[G][kRowsTile];
+    __shared__ float s_s[G][kRowsTile];
     __shared__ float red[2][4][G];
     __shared__ __align__(16) float acc_s[kS][D];
-    __shared__ float cent[1 << VB];
+    __shared__ __align__(16) float tab[kTab];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t t = blockIdx.y / a.kv_heads;
     const int64_t kvh = blockIdx.y - t * a.kv_heads;
     const int sp = blockIdx.x;
 
-    if (tid < (1 << VB)) cent[tid] = centroid<VB>(tid);
+    if constexpr (is_turbo(VF)) TurboTable<VF>::fill(tab, tid);
     for (int i = tid; i < G * D; i += 256) q_s[i / D][i % D] = a.q[(t * a.q_heads + kvh * G + i / D) * D + i % D];
-    if constexpr (KB != 8) {
+    if constexpr (is_turbo(KF)) {
         // The query into the keys' rotated domain: 16 threads a group of 128, 8 values each (G * D / 8 is a multiple
         // of 16, so whole groups of 16 lanes take part).
         __syncthreads();
@@ -863,88 +844,95 @@ __global__ __launch_bounds__(256) void attention_turbo_rows(AttnArgs a, const ui
         for (int e = 0; e < kLaneValues; ++e) acc[g][e] = 0.0f;
     }
     const int dg = tid % kD8, sub = tid / kD8;
-    const int vgi = dg / kLanes, vlane = dg % kLanes;  // the value group and lane this thread's 8 dims are
+    // The group of this thread's 8 value dims and their slice of it (for TurboQuant, the format lane).
+    const int vgi = dg / (kGV / kLaneValues), vlane = dg % (kGV / kLaneValues);
+    const int set = tid / 8, l8 = tid % 8;  // the 8-lane set and lane that score keys
     __syncthreads();
-    for (int64_t j0 = k0; j0 <= k1; j0 += kTurboTile) {
-        // Scores of key j0 + tid for every head.
-        const int64_t j = j0 + tid;
-        float s[G];
+    float qreg[kQReg ? G : 1][kQReg ? kNG : 1][kLV];
+    if constexpr (kQReg) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) s[g] = 0.0f;
-        if (j <= k1) {
-            const int64_t row = j * a.kv_heads + kvh;
-            // The row in chunks of 32 values (4 lanes' worth of a group): decoded into registers once, then one dot
-            // product per head.
-            float factor = 1.0f;
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int gi = 0; gi < kNG; ++gi)
+#pragma unroll
+                for (int e = 0; e < kLV; ++e) qreg[g][gi][e] = q_s[g][gi * kGV + kLV * l8 + e];
+    }
+    const uint16_t* knorm = static_cast<const uint16_t*>(ks);
+    for (int64_t j0 = k0; j0 <= k1; j0 += kRowsTile) {
+        const int64_t n = k1 - j0 + 1 < kRowsTile ? k1 - j0 + 1 : kRowsTile;
+        // The value rows this thread adds up in this tile are keys sub + kS u; the first kVPref are requested before
+        // the scores.
+        ValueSlice<VF> vs[kVPref];
+        const auto load_values = [&](int u0) {
+#pragma unroll
+            for (int u = 0; u < kVPref; ++u) {
+                const int k = sub + (u0 + u) * kS;
+                const int64_t group = ((j0 + (k < n ? k : 0)) * a.kv_heads + kvh) * kNG + vgi;
+                vs[u].load(vc + group * kVGB, vlane, vn + group);
+            }
+        };
+        load_values(0);
+        // Scores of keys set + 32 u (u < 8), kKB at a time.
 #pragma unroll 1
-            for (int c = 0; c < D / 32; ++c) {
-                float x[32];
-                float part_norm = 1.0f;
-                if constexpr (KB == 8) {
-                    const uint8_t* r = kc + row * D + 32 * c;
-                    const u32x4 w0 = ld128(r), w1 = ld128(r + 16);
+        for (int ub = 0; ub < kKeysPerSet; ub += kKB) {
+            KeyLane<KF, kLV> kl[kKB][kNG];
+            float kf[kKB][kNG];
 #pragma unroll
-                    for (int b = 0; b < 16; ++b) {
-                        x[b] = byte_f32(w0[b / 4], b % 4);
-                        x[16 + b] = byte_f32(w1[b / 4], b % 4);
-                    }
-                } else {
-                    constexpr int kChunks = kGroup / 32;  // chunks a group
-                    const int gi = c / kChunks, cc = c % kChunks;
-                    const int64_t group = row * kNG + gi;
-                    const uint8_t* gc = kc + group * group_bytes(KB);
-                    uint32_t low[4], high = 0;
-                    if constexpr (KB == 4) {
-                        const u32x4 w = ld128(gc + 16 * cc);
+            for (int u = 0; u < kKB; ++u) {
+                const int kk = set + kSets * (ub + u);
+                const int64_t row = (j0 + (kk < n ? kk : 0)) * a.kv_heads + kvh;
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) low[i] = w[i];
-                    } else {
-                        const uint2 w = *reinterpret_cast<const uint2*>(gc + 8 * cc);
-                        low[0] = w.x & 0xffffu;
-                        low[1] = w.x >> 16;
-                        low[2] = w.y & 0xffffu;
-                        low[3] = w.y >> 16;
-                        if constexpr (KB == 3) high = *reinterpret_cast<const uint32_t*>(gc + kGroup / 4 + 4 * cc);
-                    }
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        LaneCodes<KB> lc;
-                        lc.low = low[i];
-                        lc.high = (high >> (8 * i)) & 0xffu;
-#pragma unroll
-                        for (int e = 0; e < kLaneValues; ++e) x[8 * i + e] = cent[lc.code(e)];
-                    }
-                    part_norm = f16_to_f32(static_cast<const uint16_t*>(ks)[group]);
+                for (int gi = 0; gi < kNG; ++gi) {
+                    kl[u][gi].load(kc + (row * kNG + gi) * kKGB, l8);
+                    if constexpr (is_turbo(KF)) kf[u][gi] = f16_to_f32(knorm[row * kNG + gi]);
                 }
+                if constexpr (KF == 8) kf[u][0] = static_cast<const float*>(ks)[row];
+            }
+#pragma unroll
+            for (int u = 0; u < kKB; ++u) {
+                float dot[G];
+#pragma unroll
+                for (int g = 0; g < G; ++g) dot[g] = 0.0f;
+#pragma unroll
+                for (int gi = 0; gi < kNG; ++gi) {
+                    float x[kLV];
+                    kl[u][gi].decode(tab, x);
+#pragma unroll
+                    for (int g = 0; g < G; ++g) {
+                        float part = 0.0f;
+                        if constexpr (kQReg) {
+#pragma unroll
+                            for (int e = 0; e < kLV; ++e) part = fmaf(qreg[g][gi][e], x[e], part);
+                        } else {
+                            const float* qg = &q_s[g][gi * kGV + kLV * l8];
+#pragma unroll
+                            for (int e = 0; e < kLV; e += 4) {
+                                const float4 q4 = *reinterpret_cast<const float4*>(qg + e);
+                                part = fmaf(q4.x, x[e], part);
+                                part = fmaf(q4.y, x[e + 1], part);
+                                part = fmaf(q4.z, x[e + 2], part);
+                                part = fmaf(q4.w, x[e + 3], part);
+                            }
+                        }
+                        if constexpr (is_turbo(KF)) dot[g] = fmaf(part, kf[u][gi], dot[g]);
+                        else dot[g] += part;
+                    }
+                }
+                const int kk = set + kSets * (ub + u);
 #pragma unroll
                 for (int g = 0; g < G; ++g) {
-                    const float* qg = &q_s[g][32 * c];
-                    float dot = 0.0f;
-#pragma unroll
-                    for (int e = 0; e < 32; e += 4) {
-                        const float4 q4 = *reinterpret_cast<const float4*>(qg + e);
-                        dot = fmaf(q4.x, x[e], dot);
-                        dot = fmaf(q4.y, x[e + 1], dot);
-                        dot = fmaf(q4.z, x[e + 2], dot);
-                        dot = fmaf(q4.w, x[e + 3], dot);
-                    }
-                    if constexpr (KB == 8) s[g] += dot;
-                    else s[g] = fmaf(dot, part_norm, s[g]);
+                    float x = group_reduce<8, OpSum>(dot[g]);
+                    if constexpr (KF == 8) x *= kf[u][0];
+                    x *= a.scale;
+                    if constexpr (CAP) x = a.softcap * tanhf(x / a.softcap);
+                    if (l8 == 0) s_s[g][kk] = kk < n ? x : -INFINITY;
                 }
             }
-            if constexpr (KB == 8) factor = static_cast<const float*>(ks)[row];
-#pragma unroll
-            for (int g = 0; g < G; ++g) s[g] *= factor;
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float x = s[g] * a.scale;
-                if constexpr (CAP) x = a.softcap * tanhf(x / a.softcap);
-                s[g] = x;
-            }
-        } else {
-#pragma unroll
-            for (int g = 0; g < G; ++g) s[g] = -INFINITY;
         }
+        __syncthreads();
+        float s[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) s[g] = s_s[g][tid];
         // The tile's max per head, then exponentials and their sum.
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -965,33 +953,38 @@ __global__ __launch_bounds__(256) void attention_turbo_rows(AttnArgs a, const ui
             if (lane == 0) red[1][wave][g] = w;
         }
         __syncthreads();
-        // The weighted sum of the tile's stored (rotated) value rows.
-        const int64_t n = k1 - j0 + 1 < kTurboTile ? k1 - j0 + 1 : kTurboTile;
+        // The weighted sum of the tile's stored value rows.
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             l[g] = l[g] * c[g] + ((red[1][0][g] + red[1][1][g]) + (red[1][2][g] + red[1][3][g]));
 #pragma unroll
             for (int e = 0; e < kLaneValues; ++e) acc[g][e] *= c[g];
         }
-        for (int k = sub; k < n; k += kS) {
-            const int64_t group = ((j0 + k) * a.kv_heads + kvh) * kNG + vgi;
-            LaneCodes<VB> lc;
-            lc.load(vc + group * kVGB, vlane);
-            const float norm = f16_to_f32(vn[group]);
-            float vf[kLaneValues];
+#pragma unroll 1
+        for (int u0 = 0; u0 < kRowsPerThread; u0 += kVPref) {
+            if (u0 > 0) {
+                if (sub + u0 * kS >= n) break;
+                load_values(u0);
+            }
 #pragma unroll
-            for (int e = 0; e < kLaneValues; ++e) vf[e] = cent[lc.code(e)] * norm;
+            for (int u = 0; u < kVPref; ++u) {
+                const int k = sub + (u0 + u) * kS;
+                if (k >= n) break;
+                float x[kLaneValues];
+                vs[u].decode(tab, x);
+                const float f = vs[u].factor();
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float p = p_s[g][k];
+                for (int g = 0; g < G; ++g) {
+                    const float pf = is_turbo(VF) ? p_s[g][k] * f : p_s[g][k];
 #pragma unroll
-                for (int e = 0; e < kLaneValues; ++e) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
+                    for (int e = 0; e < kLaneValues; ++e) acc[g][e] = fmaf(pf, x[e], acc[g][e]);
+                }
             }
         }
-        __syncthreads();  // p_s and red are rewritten by the next tile
+        __syncthreads();  // s_s, p_s and red are rewritten by the next tile
     }
-    // Per head: the key subsets' sums add up, 16 threads a group rotate them back, then the output or the partial row
-    // with its (max, sum).
+    // Per head: the key subsets' sums add up (TurboQuant values: 16 threads a group rotate them back), then the output
+    // or the partial row with its (max, sum).
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         *reinterpret_cast<u32x4*>(&acc_s[sub][kLaneValues * dg]) =
@@ -1001,7 +994,7 @@ __global__ __launch_bounds__(256) void attention_turbo_rows(AttnArgs a, const ui
             u32x4{__float_as_uint(acc[g][4]), __float_as_uint(acc[g][5]), __float_as_uint(acc[g][6]),
                   __float_as_uint(acc[g][7])};
         __syncthreads();
-        if (tid < kD8) {  // kD8 is a multiple of 16: whole groups of 16 lanes
+        if (tid < kD8) {  // for TurboQuant kD8 is a multiple of 16: whole groups of 16 lanes
             float v[kLaneValues];
 #pragma unroll
             for (int e = 0; e < kLaneValues; ++e) {
@@ -1010,7 +1003,7 @@ __global__ __launch_bounds__(256) void attention_turbo_rows(AttnArgs a, const ui
                 for (int q = 0; q < kS; ++q) sum += acc_s[q][kLaneValues * tid + e];
                 v[e] = sum;
             }
-            rotate8(v, tid % kLanes, true);
+            if constexpr (is_turbo(VF)) rotate8(v, tid % kLanes, true);
             const int64_t hh = kvh * G + g;
             if (a.part == nullptr) {
                 float* o = a.out + (t * a.q_heads + hh) * D + kLaneValues * tid;
@@ -1032,43 +1025,53 @@ __global__ __launch_bounds__(256) void attention_turbo_rows(AttnArgs a, const ui
     }
 }
 
-template <int KB, int VB, int G>
-int launch_turbo_g(hipStream_t s, const AttnArgs& a, const uint8_t* kc, const void* ks, const uint8_t* vc,
-                   const uint16_t* vn, const char* what) {
+template <int KF, int VF, int G>
+int launch_kv_rows_g(hipStream_t s, const AttnArgs& a, const void* k, const void* ks, const void* v,
+                  const uint16_t* vn, const char* what) {
     const dim3 grid(static_cast<unsigned>(a.split), static_cast<unsigned>(a.tokens * a.kv_heads));
     const bool cap = a.softcap > 0.0f;
-    switch (a.head_dim) {
-        case 128:
-            if (cap) attention_turbo_rows<KB, VB, G, 128, true><<<grid, 256, 0, s>>>(a, kc, ks, vc, vn);
-            else attention_turbo_rows<KB, VB, G, 128, false><<<grid, 256, 0, s>>>(a, kc, ks, vc, vn);
-            break;
-        case 256:
-            if (cap) attention_turbo_rows<KB, VB, G, 256, true><<<grid, 256, 0, s>>>(a, kc, ks, vc, vn);
-            else attention_turbo_rows<KB, VB, G, 256, false><<<grid, 256, 0, s>>>(a, kc, ks, vc, vn);
-            break;
-        case 512:
-            if (cap) attention_turbo_rows<KB, VB, G, 512, true><<<grid, 256, 0, s>>>(a, kc, ks, vc, vn);
-            else attention_turbo_rows<KB, VB, G, 512, false><<<grid, 256, 0, s>>>(a, kc, ks, vc, vn);
-            break;
-        default:
-            return fail(XS_HIP_EUNSUPPORTED, std::string(what) + ": head_dim " + std::to_string(a.head_dim) +
-                                                 " with TurboQuant values (supported: 128, 256, 512)");
+    const auto* kc = static_cast<const uint8_t*>(k);
+    const auto* vc = static_cast<const uint8_t*>(v);
+#define XS_ROWS_CASE(DIM)                                                                                             \
+    case DIM:                                                                                                         \
+        if (cap) attention_rows_kernel<KF, VF, G, DIM, true><<<grid, 256, 0, s>>>(a, kc, ks, vc, vn);                 \
+        else attention_rows_kernel<KF, VF, G, DIM, false><<<grid, 256, 0, s>>>(a, kc, ks, vc, vn);                    \
+        break;
+    if constexpr (is_turbo(VF)) {
+        switch (a.head_dim) {
+            XS_ROWS_CASE(128)
+            XS_ROWS_CASE(256)
+            XS_ROWS_CASE(512)
+            default:
+                return fail(XS_HIP_EUNSUPPORTED, std::string(what) + ": head_dim " + std::to_string(a.head_dim) +
+                                                     " with TurboQuant values (supported: 128, 256, 512)");
+        }
+    } else {
+        switch (a.head_dim) {
+            XS_ROWS_CASE(64)
+            XS_ROWS_CASE(128)
+            XS_ROWS_CASE(256)
+            default:
+                return fail(XS_HIP_EUNSUPPORTED, std::string(what) + ": head_dim " + std::to_string(a.head_dim) +
+                                                     " (supported: 64, 128, 256)");
+        }
     }
+#undef XS_ROWS_CASE
     return check_launch(what);
 }
 
-template <int KB, int VB>
-int launch_turbo(hipStream_t s, const AttnArgs& a, const uint8_t* kc, const void* ks, const uint8_t* vc,
-                 const uint16_t* vn, const char* what) {
+template <int KF, int VF>
+int launch_kv_rows(hipStream_t s, const AttnArgs& a, const void* k, const void* ks, const void* v, const uint16_t* vn,
+                const char* what) {
     switch (a.q_heads / a.kv_heads) {
-        case 1: return launch_turbo_g<KB, VB, 1>(s, a, kc, ks, vc, vn, what);
-        case 2: return launch_turbo_g<KB, VB, 2>(s, a, kc, ks, vc, vn, what);
-        case 3: return launch_turbo_g<KB, VB, 3>(s, a, kc, ks, vc, vn, what);
-        case 4: return launch_turbo_g<KB, VB, 4>(s, a, kc, ks, vc, vn, what);
-        case 5: return launch_turbo_g<KB, VB, 5>(s, a, kc, ks, vc, vn, what);
-        case 6: return launch_turbo_g<KB, VB, 6>(s, a, kc, ks, vc, vn, what);
-        case 7: return launch_turbo_g<KB, VB, 7>(s, a, kc, ks, vc, vn, what);
-        case 8: return launch_turbo_g<KB, VB, 8>(s, a, kc, ks, vc, vn, what);
+        case 1: return launch_kv_rows_g<KF, VF, 1>(s, a, k, ks, v, vn, what);
+        case 2: return launch_kv_rows_g<KF, VF, 2>(s, a, k, ks, v, vn, what);
+        case 3: return launch_kv_rows_g<KF, VF, 3>(s, a, k, ks, v, vn, what);
+        case 4: return launch_kv_rows_g<KF, VF, 4>(s, a, k, ks, v, vn, what);
+        case 5: return launch_kv_rows_g<KF, VF, 5>(s, a, k, ks, v, vn, what);
+        case 6: return launch_kv_rows_g<KF, VF, 6>(s, a, k, ks, v, vn, what);
+        case 7: return launch_kv_rows_g<KF, VF, 7>(s, a, k, ks, v, vn, what);
+        case 8: return launch_kv_rows_g<KF, VF, 8>(s, a, k, ks, v, vn, what);
         default:
             return fail(XS_HIP_EUNSUPPORTED, std::string(what) + ": " + std::to_string(a.q_heads / a.kv_heads) +
                                                  " query heads per KV head (supported: 1 to 8)");
@@ -1261,7 +1264,8 @@ int attention_float(void* stream, xs_dtype kv_dtype, const float* q, const void*
                q_heads, kv_heads, head_dim, kv_len, window, scale, softcap, causal ? 1 : 0, static_cast<int>(split), 1,
                kv_len_dev};
     const hipStream_t s = as_stream(stream);
-    const int rc = kv_dtype == XS_F16 ? launch_float<F16>(s, a, k, v) : launch_float<F32>(s, a, k, v);
+    const int rc = kv_dtype == XS_F16 ? launch_kv_rows<16, 16>(s, a, k, nullptr, v, nullptr, what)
+                                      : launch_kv_rows<32, 32>(s, a, k, nullptr, v, nullptr, what);
     if (rc != XS_HIP_OK || split == 1) return rc;
     attention_combine_rows<<<static_cast<unsigned>(tokens * q_heads * (head_dim / kCombineDims)), 256, 0, s>>>(
         static_cast<const float*>(scratch), out, static_cast<int>(split), head_dim, tokens * q_heads);
@@ -1331,16 +1335,14 @@ int attention_quantized(void* stream, xs_kv_format kf, xs_kv_format vf, const fl
                q_heads, kv_heads, head_dim, kv_len, window, scale, softcap, causal ? 1 : 0, static_cast<int>(split), 1,
                kv_len_dev};
     const hipStream_t s = as_stream(stream);
-    const auto* kc = static_cast<const uint8_t*>(k_codes);
-    const auto* vc = static_cast<const uint8_t*>(v_codes);
     const auto* vn = static_cast<const uint16_t*>(v_scales);
     int rc;
-    if (vb == 4) rc = kb == 8 ? launch_turbo<8, 4>(s, a, kc, k_scales, vc, vn, what)
-                              : launch_turbo<4, 4>(s, a, kc, k_scales, vc, vn, what);
-    else if (vb == 3) rc = kb == 8 ? launch_turbo<8, 3>(s, a, kc, k_scales, vc, vn, what)
-                                   : launch_turbo<3, 3>(s, a, kc, k_scales, vc, vn, what);
-    else rc = kb == 8 ? launch_turbo<8, 2>(s, a, kc, k_scales, vc, vn, what)
-                      : launch_turbo<2, 2>(s, a, kc, k_scales, vc, vn, what);
+    if (vb == 4) rc = kb == 8 ? launch_kv_rows<8, 4>(s, a, k_codes, k_scales, v_codes, vn, what)
+                              : launch_kv_rows<4, 4>(s, a, k_codes, k_scales, v_codes, vn, what);
+    else if (vb == 3) rc = kb == 8 ? launch_kv_rows<8, 3>(s, a, k_codes, k_scales, v_codes, vn, what)
+                                   : launch_kv_rows<3, 3>(s, a, k_codes, k_scales, v_codes, vn, what);
+    else rc = kb == 8 ? launch_kv_rows<8, 2>(s, a, k_codes, k_scales, v_codes, vn, what)
+                      : launch_kv_rows<2, 2>(s, a, k_codes, k_scales, v_codes, vn, what);
     if (rc != XS_HIP_OK || split == 1) return rc;
     attention_combine_rows<<<static_cast<unsigned>(tokens * q_heads * (head_dim / kCombineDims)), 256, 0, s>>>(
         static_cast<const float*>(scratch), out, static_cast<int>(split), head_dim, tokens * q_heads);

@@ -99,6 +99,11 @@ ALGO_BYTES: Dict[str, int] = {
     # one decode step over config 4's int8 cache: K and V codes [65536, 8, 128] and scales [65536, 8]; q and out
     # [1, 32, 128] f32
     "attention_i8_decode": 2 * (65536 * 8 * 128 + 65536 * 8 * 4) + 2 * 32 * 128 * 4,
+    # the same step over turbo4 keys and values (64 code bytes and a 2-byte norm per 128 values), and over int8 keys
+    # with turbo4 values
+    "attention_f16_decode": 2 * 65536 * 8 * 128 * 2 + 2 * 32 * 128 * 4,
+    "attention_turbo4_decode": 2 * (65536 * 8 * 64 + 65536 * 8 * 2) + 2 * 32 * 128 * 4,
+    "attention_i8_turbo4_decode": 65536 * 8 * (128 + 4) + 65536 * 8 * (64 + 2) + 2 * 32 * 128 * 4,
     "rope_qk": 2 * (8192 * 32 * 128 * 2) + 2 * (8192 * 8 * 128 * 2) + 8192 * 4 + 64 * 4,
     "kv_quantize": 2 * (65536 * 8 * 128 * 2 + 65536 * 8 * 128 + 65536 * 8 * 4),
     "kv_dequantize": 2 * (65536 * 8 * 128 + 65536 * 8 * 4 + 65536 * 8 * 128 * 2),
