@@ -337,6 +337,9 @@ int xs_hip_attention_i8_at(void* stream, const float* q, const void* k_codes, co
                            int64_t kv_heads, int64_t head_dim, int64_t kv_capacity, const int64_t* kv_len,
                            float scale, float softcap, int64_t window, int causal, int64_t split, void* scratch);
 int64_t xs_hip_attention_i8_split(int64_t tokens, int64_t kv_heads, int64_t kv_len);
+/* The split xs_hip_attention and xs_hip_attention_quantized (for pairs other than int8/int8) run best at for this shape:
+ * about two workgroups a CU, each at least 128 keys. Scratch: xs_hip_attention_i8_scratch. */
+int64_t xs_hip_attention_rows_split(int64_t tokens, int64_t kv_heads, int64_t kv_len);
 size_t xs_hip_attention_i8_scratch(int64_t tokens, int64_t q_heads, int64_t head_dim, int64_t split);
 /* Decode attention over a float KV cache: keys and values [kv_len, kv_heads, head_dim] of kv_dtype (XS_F16 or XS_F32;
  * the Float KV format: f16 rows at f16 precision, f32 at f32), q and out as xs_hip_attention_i8, the same key

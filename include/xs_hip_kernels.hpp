@@ -314,6 +314,10 @@ struct AttentionShape {
 inline int64_t attention_split(const AttentionShape& s) {
     return xs_hip_attention_i8_split(s.tokens, s.kv_heads, s.kv_len);
 }
+// The split for attention_rows (float caches) and attention_rows_quantized with TurboQuant values.
+inline int64_t attention_rows_split(const AttentionShape& s) {
+    return xs_hip_attention_rows_split(s.tokens, s.kv_heads, s.kv_len);
+}
 inline size_t attention_scratch(const AttentionShape& s, int64_t split) {
     return xs_hip_attention_i8_scratch(s.tokens, s.q_heads, s.head_dim, split);
 }

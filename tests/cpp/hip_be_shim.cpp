@@ -146,7 +146,9 @@ int hipbe_attention(void* q, int k_format, int v_format, const float* qp, const 
         s.head_dim = head_dim;
         s.kv_len = kv_len;
         s.scale = scale;
-        const int64_t split = hb::attention_split(s);
+        const int64_t split = k_format == static_cast<int>(hb::KvFormat::I8) && v_format == k_format
+                                  ? hb::attention_split(s)
+                                  : hb::attention_rows_split(s);
         hb::DeviceBuffer part(hb::attention_scratch(s, split));
         if (k_format == 0) {
             hb::attention_rows(q, qp, static_cast<const hb::half*>(k), static_cast<const hb::half*>(v), out, s, split,

@@ -774,6 +774,92 @@ struct ValueSlice {
     }
 };
 
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// The scale of the TurboQuant centroids in the f16 key table: 64 c stays a normal f16 in its low part too.
+constexpr float kKeyTableScale = 64.0f;
+
+// The key table of a TurboQuant format for the matrix cores: entry i (indexed as TurboTable) holds the f16 high and
+// low parts of 64 x the centroids byte i holds -- hi = f16(64 c), lo = f16(64 c - hi), 22 significant bits -- as packed
+// pairs: turbo4 / turbo3 {hi pair, lo pair}; turbo2 {hi pair 0, hi pair 1, lo pair 0, lo pair 1}.
+template <int Bits>
+struct TurboKeyTable {
+    static constexpr int kEntries = TurboTable<Bits>::kEntries;
+    static constexpr int kWords = Bits == 2 ? 4 : 2;
+    __device__ static uint32_t pair(float a, float b) {
+        const _Float16 ha = static_cast<_Float16>(a), hb = static_cast<_Float16>(b);
+        return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, ha)) |
+               (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hb)) << 16);
+    }
+    __device__ static void fill(uint32_t* t, int tid) {
+        for (int i = tid; i < kEntries; i += 256) {
+            float c[4];
+            if constexpr (Bits == 4) {
+                c[0] = turbo::centroid<4>(i & 15);
+                c[1] = turbo::centroid<4>(i >> 4);
+            } else if constexpr (Bits == 2) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) c[e] = turbo::centroid<2>((i >> (2 * e)) & 3);
+            } else {
+                c[0] = turbo::centroid<3>((i & 3) | (((i >> 4) & 1) << 2));
+                c[1] = turbo::centroid<3>(((i >> 2) & 3) | (((i >> 5) & 1) << 2));
+            }
+            constexpr int kN = Bits == 2 ? 4 : 2;
+            float hi[4], lo[4];
+#pragma unroll
+            for (int e = 0; e < kN; ++e) {
+                const float v = c[e] * kKeyTableScale;
+                hi[e] = static_cast<float>(static_cast<_Float16>(v));
+                lo[e] = v - hi[e];
+            }
+            if constexpr (Bits == 2) {
+                t[4 * i] = pair(hi[0], hi[1]);
+                t[4 * i + 1] = pair(hi[2], hi[3]);
+                t[4 * i + 2] = pair(lo[0], lo[1]);
+                t[4 * i + 3] = pair(lo[2], lo[3]);
+            } else {
+                t[2 * i] = pair(hi[0], hi[1]);
+                t[2 * i + 1] = pair(lo[0], lo[1]);
+            }
+        }
+    }
+    // One format lane's 8 codes (low and high words as turbo::LaneCodes) as the f16 high and low parts of 64 x their
+    // centroids, in the matrix-core operand layout (value e in half e).
+    __device__ static void decode8(const uint32_t* t, uint32_t low, uint32_t high, uint32_t* hi, uint32_t* lo) {
+        if constexpr (Bits == 4) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint2 v = reinterpret_cast<const uint2*>(t)[(low >> (8 * i)) & 0xffu];
+                hi[i] = v.x;
+                lo[i] = v.y;
+            }
+        } else if constexpr (Bits == 2) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint4 v = reinterpret_cast<const uint4*>(t)[(low >> (8 * i)) & 0xffu];
+                hi[2 * i] = v.x;
+                hi[2 * i + 1] = v.y;
+                lo[2 * i] = v.z;
+                lo[2 * i + 1] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t idx = ((low >> (4 * i)) & 15u) | (((high >> (2 * i)) & 3u) << 4);
+                const uint2 v = reinterpret_cast<const uint2*>(t)[idx];
+                hi[i] = v.x;
+                lo[i] = v.y;
+            }
+        }
+    }
+};
+
+__device__ __forceinline__ half8_t as_half8(const uint32_t* w) {
+    u32x4 v = {w[0], w[1], w[2], w[3]};
+    return __builtin_bit_cast(half8_t, v);
+}
+
 // KF, VF: the keys' and the values' formats (both 16 or both 32; or VF TurboQuant with KF the same or 8).
 template <int KF, int VF, int G, int D, bool CAP>
 __global__ __launch_bounds__(256) void attention_rows_kernel(AttnArgs a, const uint8_t* kc, const void* ks,
@@ -795,7 +881,14 @@ __global__ __launch_bounds__(256) void attention_rows_kernel(AttnArgs a, const u
     // Keys a set loads at once: about 32 words of registers.
     constexpr int kKW = kNG * KeyLane<KF, kLV>::kWords;
     constexpr int kKB = kKW >= 32 ? 1 : 32 / kKW < 8 ? 32 / kKW : 8;
-    constexpr bool kQReg = G * kNG * kLV <= 64;  // the query values a key lane needs, in registers
+    // Scores on the matrix cores (v_mfma_f32_16x16x32_f16) for f16 and int8 keys up to head_dim 256; f32 and TurboQuant
+    // keys, and head_dim 512, take the lanes' fused multiply-adds (measured on MI355X: TurboQuant keys decoded into
+    // the matrix operands' f16 high and low parts ran slower than the lanes' decode and multiply-adds).
+    constexpr bool kMfma = (KF == 16 || KF == 8) && D <= 256;
+    constexpr bool kQReg = !kMfma && G * kNG * kLV <= 64;  // the query values a key lane needs, in registers
+    constexpr int kSteps = D / 32;  // 32-dim steps of a key row
+    constexpr int kAW = KF == 16 ? 4 : KF == 8 ? 2 : KF == 3 ? 2 : 1;  // words of a lane's A operand a step, as stored
+    constexpr int kABlk = kSteps * kAW * 4 <= 64 ? 4 : 2;              // 16-key blocks whose keys are loaded together
     constexpr int kKGB = group_bytes_of(KF, kLV);
     constexpr int kVGB = group_bytes_of(VF, kLV);
     constexpr int kTab = is_turbo(VF) ? TurboTable<(is_turbo(VF) ? VF : 4)>::kEntries *
@@ -807,12 +900,16 @@ __global__ __launch_bounds__(256) void attention_rows_kernel(AttnArgs a, const u
     __shared__ float red[2][4][G];
     __shared__ __align__(16) float acc_s[kS][D];
     __shared__ __align__(16) float tab[kTab];
+    __shared__ __align__(16) uint32_t ktab[kMfma && is_turbo(KF) ? TurboKeyTable<(is_turbo(KF) ? KF : 4)>::kEntries *
+                                                                        TurboKeyTable<(is_turbo(KF) ? KF : 4)>::kWords
+                                                                  : 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t t = blockIdx.y / a.kv_heads;
     const int64_t kvh = blockIdx.y - t * a.kv_heads;
     const int sp = blockIdx.x;
 
     if constexpr (is_turbo(VF)) TurboTable<VF>::fill(tab, tid);
+    if constexpr (kMfma && is_turbo(KF)) TurboKeyTable<KF>::fill(ktab, tid);
     for (int i = tid; i < G * D; i += 256) q_s[i / D][i % D] = a.q[(t * a.q_heads + kvh * G + i / D) * D + i % D];
     if constexpr (is_turbo(KF)) {
         // The query into the keys' rotated domain: 16 threads a group of 128, 8 values each (G * D / 8 is a multiple
@@ -858,6 +955,40 @@ __global__ __launch_bounds__(256) void attention_rows_kernel(AttnArgs a, const u
                 for (int e = 0; e < kLV; ++e) qreg[g][gi][e] = q_s[g][gi * kGV + kLV * l8 + e];
     }
     const uint16_t* knorm = static_cast<const uint16_t*>(ks);
+    // The matrix cores' B operand: column n = lane % 16 is query head n (zero past G), rows 8 (lane / 16) + e of each
+    // 32-dim step; the query times a power of two qs that brings max |q| just under 2^14, as f16 high and low parts
+    // (22 significant bits; qs is undone, exactly, on the scores).
+    uint32_t qb_hi[kMfma ? kSteps : 1][4], qb_lo[kMfma ? kSteps : 1][4];
+    float q_unscale = 1.0f;
+    if constexpr (kMfma) {
+        float amax = 0.0f;
+        for (int i = tid; i < G * D; i += 256) amax = fmaxf(amax, fabsf(q_s[i / D][i % D]));
+        amax = wave_reduce<OpMax>(amax, 0.0f);
+        if (lane == 0) red[0][wave][0] = amax;
+        __syncthreads();
+        amax = fmaxf(fmaxf(red[0][0][0], red[0][1][0]), fmaxf(red[0][2][0], red[0][3][0]));
+        int e2 = 0;
+        frexpf(amax, &e2);  // amax < 2^e2
+        const float qs = amax > 0.0f && amax <= 3.0e38f ? ldexpf(1.0f, 14 - e2) : 1.0f;
+        q_unscale = 1.0f / qs;  // a power of two: exact
+        const int hn = lane % 16, kq = 8 * (lane / 16);
+#pragma unroll
+        for (int st = 0; st < kSteps; ++st) {
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                float h[2], lo2[2];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const float v = hn < G ? q_s[hn < G ? hn : 0][32 * st + kq + e + j] * qs : 0.0f;
+                    h[j] = static_cast<float>(static_cast<_Float16>(v));
+                    lo2[j] = v - h[j];
+                }
+                qb_hi[st][e / 2] = TurboKeyTable<4>::pair(h[0], h[1]);
+                qb_lo[st][e / 2] = TurboKeyTable<4>::pair(lo2[0], lo2[1]);
+            }
+        }
+        __syncthreads();  // red is rewritten by the first tile
+    }
     for (int64_t j0 = k0; j0 <= k1; j0 += kRowsTile) {
         const int64_t n = k1 - j0 + 1 < kRowsTile ? k1 - j0 + 1 : kRowsTile;
         // The value rows this thread adds up in this tile are keys sub + kS u; the first kVPref are requested before
@@ -872,6 +1003,97 @@ __global__ __launch_bounds__(256) void attention_rows_kernel(AttnArgs a, const u
             }
         };
         load_values(0);
+        if constexpr (kMfma) {
+            // Scores on the matrix cores: wave w takes keys 64 w .. 64 w + 63 of the tile, 16 a block; lane l loads
+            // the A operand of key 16 b + l % 16 (8 values of each 32-dim step from 8 (l / 16)) and receives the
+            // scores of keys 16 b + 4 (l / 16) + i for query head l % 16.
+            const int kq = 8 * (lane / 16);
+#pragma unroll 1
+            for (int b0 = 0; b0 < 4; b0 += kABlk) {
+                uint32_t araw[kABlk][kSteps][kAW];
+#pragma unroll
+                for (int bb = 0; bb < kABlk; ++bb) {
+                    const int kr = 64 * wave + 16 * (b0 + bb) + lane % 16;
+                    const int64_t row = (j0 + (kr < n ? kr : 0)) * a.kv_heads + kvh;
+#pragma unroll
+                    for (int st = 0; st < kSteps; ++st) {
+                        if constexpr (KF == 16) {
+                            const u32x4 v = ld128(kc + 2 * (row * D + 32 * st + kq));
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) araw[bb][st][i] = v[i];
+                        } else if constexpr (KF == 8) {
+                            const uint2 v = *reinterpret_cast<const uint2*>(kc + row * D + 32 * st + kq);
+                            araw[bb][st][0] = v.x;
+                            araw[bb][st][1] = v.y;
+                        } else {
+                            const int gi = st / 4, fl = 4 * (st % 4) + lane / 16;  // group, format lane
+                            LaneCodes<KF> lc;
+                            lc.load(kc + (row * kNG + gi) * group_bytes(KF), fl);
+                            araw[bb][st][0] = lc.low;
+                            if constexpr (KF == 3) araw[bb][st][1] = lc.high;
+                        }
+                    }
+                }
+#pragma unroll
+                for (int bb = 0; bb < kABlk; ++bb) {
+                    constexpr int kAcc = is_turbo(KF) ? kNG : 1;  // TurboQuant: one accumulator a group (its norm)
+                    f32x4_t cacc[kAcc];
+#pragma unroll
+                    for (int gi = 0; gi < kAcc; ++gi) cacc[gi] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int st = 0; st < kSteps; ++st) {
+                        const int gi = is_turbo(KF) ? st / 4 : 0;
+                        const half8_t bh = as_half8(qb_hi[st]), bl = as_half8(qb_lo[st]);
+                        if constexpr (KF == 16) {
+                            const half8_t ah = as_half8(araw[bb][st]);
+                            cacc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, cacc[gi], 0, 0, 0);
+                            cacc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, cacc[gi], 0, 0, 0);
+                        } else if constexpr (KF == 8) {
+                            uint32_t w[4];
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                const uint32_t src = araw[bb][st][i / 2];
+                                const int s0 = 16 * (i % 2);
+                                w[i] = TurboKeyTable<4>::pair(
+                                    static_cast<float>(static_cast<int8_t>((src >> s0) & 0xffu)),
+                                    static_cast<float>(static_cast<int8_t>((src >> (s0 + 8)) & 0xffu)));
+                            }
+                            const half8_t ah = as_half8(w);  // the codes, exact in f16
+                            cacc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, cacc[gi], 0, 0, 0);
+                            cacc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, cacc[gi], 0, 0, 0);
+                        } else {
+                            uint32_t hi[4], lo[4];
+                            TurboKeyTable<KF>::decode8(ktab, araw[bb][st][0], KF == 3 ? araw[bb][st][kAW - 1] : 0u,
+                                                       hi, lo);
+                            const half8_t ah = as_half8(hi), al = as_half8(lo);
+                            cacc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, cacc[gi], 0, 0, 0);
+                            cacc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, cacc[gi], 0, 0, 0);
+                            cacc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, cacc[gi], 0, 0, 0);
+                        }
+                    }
+                    const int hn = lane % 16;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int kk = 64 * wave + 16 * (b0 + bb) + 4 * (lane / 16) + i;
+                        const int64_t row = (j0 + (kk < n ? kk : 0)) * a.kv_heads + kvh;
+                        float x;
+                        if constexpr (is_turbo(KF)) {
+                            x = 0.0f;
+#pragma unroll
+                            for (int gi = 0; gi < kAcc; ++gi) x = fmaf(cacc[gi][i], f16_to_f32(knorm[row * kNG + gi]), x);
+                            x *= q_unscale * (1.0f / kKeyTableScale);
+                        } else if constexpr (KF == 8) {
+                            x = cacc[0][i] * q_unscale * static_cast<const float*>(ks)[row];
+                        } else {
+                            x = cacc[0][i] * q_unscale;
+                        }
+                        x *= a.scale;
+                        if constexpr (CAP) x = a.softcap * tanhf(x / a.softcap);
+                        if (hn < G) s_s[hn < G ? hn : 0][kk] = kk < n ? x : -INFINITY;
+                    }
+                }
+            }
+        } else {
         // Scores of keys set + 32 u (u < 8), kKB at a time.
 #pragma unroll 1
         for (int ub = 0; ub < kKeysPerSet; ub += kKB) {
@@ -928,6 +1150,7 @@ __global__ __launch_bounds__(256) void attention_rows_kernel(AttnArgs a, const u
                     if (l8 == 0) s_s[g][kk] = kk < n ? x : -INFINITY;
                 }
             }
+        }
         }
         __syncthreads();
         float s[G];
@@ -1126,6 +1349,19 @@ int64_t xs_hip_attention_i8_split(int64_t tokens, int64_t kv_heads, int64_t kv_l
     const int64_t groups = tokens * (kv_heads / hg);
     int64_t split = (static_cast<int64_t>(device_cus()) + groups - 1) / groups;
     const int64_t by_len = kv_len <= 2 * kTile * (kMaxWaves / hg) ? 1 : kv_len / kTile;
+    if (split > by_len) split = by_len;
+    if (split > kMaxSplit) split = kMaxSplit;
+    return split < 1 ? 1 : split;
+}
+
+int64_t xs_hip_attention_rows_split(int64_t tokens, int64_t kv_heads, int64_t kv_len) {
+    if (tokens <= 0 || kv_heads <= 0 || kv_len <= 0) return 1;
+    // About two workgroups a CU, each at least half a tile of keys. Measured on MI355X, one query token, 32 query and 8
+    // KV heads, head_dim 128, f16 rows: 65536 keys 54 us at split 64 (68 at 256, 64 at 32), 16384 keys 23 us at 64,
+    // 4096 keys 14 us at 32, 1024 keys 14 us at 8 or 16.
+    const int64_t units = tokens * kv_heads;
+    int64_t split = (2 * static_cast<int64_t>(device_cus()) + units - 1) / units;
+    const int64_t by_len = (kv_len + kRowsTile / 2 - 1) / (kRowsTile / 2);
     if (split > by_len) split = by_len;
     if (split > kMaxSplit) split = kMaxSplit;
     return split < 1 ? 1 : split;

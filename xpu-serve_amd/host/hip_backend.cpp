@@ -988,8 +988,10 @@ Program::RunPlan& Program::plan_for(int64_t T, std::span<const std::string> only
         } else if (plan_[i].op == Op::Attention) {
             const Dims& q = p.shapes[i][0];
             const Dims& k = g_.type(nd.inputs[1]).shape;
-            // The split grows with the keys: sized for max_context, enough for every L of the session.
-            const int64_t split = xs_hip_attention_i8_split(q[0], k[1], max_len);
+            // The split grows with the keys: sized for max_context, enough for every L of the session, whichever
+            // reader (int8 or float rows) runs.
+            const int64_t split = std::max(xs_hip_attention_i8_split(q[0], k[1], max_len),
+                                           xs_hip_attention_rows_split(q[0], k[1], max_len));
             bytes = xs_hip_attention_i8_scratch(q[0], q[1], q[2], split);
         }
         if (bytes == 0) continue;
@@ -1319,7 +1321,9 @@ void Program::launch(size_t i, const RunPlan& p, int64_t T, int64_t L, int64_t r
             const Loc& kl = p.locs[static_cast<size_t>(np.reads[1].node)][0];
             KvState& kv = s_.kv()[static_cast<size_t>(kl.id)];
             const Dims& qs = in_shape(q);
-            const int64_t split = xs_hip_attention_i8_split(qs[0], kv.heads, replay_cap > 0 ? replay_cap : L);
+            const int64_t keys = replay_cap > 0 ? replay_cap : L;
+            const int64_t split = kv.rows == DType::I8 ? xs_hip_attention_i8_split(qs[0], kv.heads, keys)
+                                                       : xs_hip_attention_rows_split(qs[0], kv.heads, keys);
             auto* out_p = reinterpret_cast<float*>(ptr(p, Value{static_cast<int32_t>(i), 0}));
             char* scratch = split > 1 ? s_.arena().get() + p.block_offset[static_cast<size_t>(p.scratch[i])] : nullptr;
             if (kv.rows != DType::I8) {  // the Float format's rows
