@@ -14,7 +14,7 @@ F32, F16, BF16, I64, I32 = 0, 1, 2, 3, 4
 NP = {F32: np.float32, F16: np.float16, BF16: np.uint16, I64: np.int64, I32: np.int32}
 # xs::graph::OpKind values of the unary ops.
 SCALE, TANH, GELU_TANH, SOFTCAP, SIGMOID, SILU, SOFTPLUS, CLAMP, GELU = 7, 8, 9, 10, 11, 12, 13, 14, 34
-KV_FLOAT, KV_I8, KV_TURBO4 = 0, 1, 2
+KV_FLOAT, KV_I8, KV_TURBO4, KV_TURBO3, KV_TURBO2 = 0, 1, 2, 3, 4
 SLICE_END = (1 << 63) - 1
 T, L = -1, -2
 

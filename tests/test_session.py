@@ -116,8 +116,13 @@ def _kv_graph(extra=None):
 
 
 def test_refuses_unsupported_kv_formats_and_precisions():
-    _refusal(_kv_graph(), "KV cache format i8:auto", kv=(S.KV_I8, S.KV_FLOAT))
-    _refusal(_kv_graph(), "KV cache format turbo4", kv=(S.KV_TURBO4, S.KV_TURBO4))
+    # The pairs the reference's device refuses (sycl_backend.cpp:2662-2664), and TurboQuant over rows that are not
+    # whole groups of 128 (kv_format.cpp:50-51).
+    _refusal(_kv_graph(), "keys in i8 and values in auto is not supported", kv=(S.KV_I8, S.KV_FLOAT))
+    _refusal(_kv_graph(), "keys in turbo4 and values in i8 is not supported", kv=(S.KV_TURBO4, S.KV_I8))
+    _refusal(_kv_graph(), "keys in turbo4 and values in turbo2 is not supported", kv=(S.KV_TURBO4, S.KV_TURBO2))
+    _refusal(_kv_graph(), "TurboQuant KV format needs a head_dim that is a multiple of 128, got 64",
+             kv=(S.KV_TURBO4, S.KV_TURBO4))
     with pytest.raises(S.BackendError, match="precision must be f16 or f32, got bf16"):
         S.Session(_kv_graph(), kv=(S.KV_FLOAT, S.KV_FLOAT), precision=S.BF16)
 
@@ -394,6 +399,66 @@ def test_kv_decode_steps(ora, hq, hkv, d, window, softcap):
     s.reset()
     cache.truncate(0)
     assert s.num_cached() == 0
+    one(4)
+
+
+class _TurboCache(_Cache):
+    """cpu-ref's cache of round-tripped rows for a pair of formats (quant::round_trip_kv, kv_format.cpp:57-61): a
+    TurboQuant stream's rows quantized, decoded and rotated back (quant::turbo::round_trip) on the oracle; an int8
+    stream's as _Cache."""
+
+    def __init__(self, ora, hkv, d, kbits, vbits):
+        super().__init__(ora, hkv, d)
+        self.kbits, self.vbits = kbits, vbits
+
+    def rt_bits(self, x, bits):
+        return super().rt(x) if bits == 8 else self.ora.turbo_round_trip(x, bits).reshape(x.shape)
+
+    def append(self, k, v):
+        self.k = np.concatenate([self.k, self.rt_bits(k, self.kbits)])
+        self.v = np.concatenate([self.v, self.rt_bits(v, self.vbits)])
+
+
+TURBO_KV = {4: S.KV_TURBO4, 3: S.KV_TURBO3, 2: S.KV_TURBO2, 8: S.KV_I8}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kbits,vbits", [(4, 4), (3, 3), (2, 2), (8, 4), (8, 3), (8, 2)])
+@pytest.mark.parametrize("hq,hkv,d,window,softcap", [(32, 8, 128, 0, 0.0), (8, 2, 256, 6, 30.0)])
+def test_turbo_kv_decode_steps(ora, kbits, vbits, hq, hkv, d, window, softcap):
+    """TurboQuant KV formats (keys and values in one, or int8 keys with TurboQuant values): a prefill, decode steps, a
+    KvRead program, truncate and reset, against the oracle over the rows cpu-ref's cache holds (each row quantized,
+    decoded and rotated back), at the reference's quantized-cache bar (device_attention.cpp:23-27)."""
+    rng = np.random.default_rng(40 + kbits + vbits + d)
+    prefill, reader = _kv_programs(hq, hkv, d, window, softcap)
+    step(f"session kv {kbits}:{vbits} H{hq}/{hkv} D{d} w{window} cap{softcap}")
+    s = S.Session([prefill, reader], max_context=64, kv=(TURBO_KV[kbits], TURBO_KV[vbits]))
+    cache = _TurboCache(ora, hkv, d, kbits, vbits)
+    scale = 1 / math.sqrt(d)
+
+    def one(tokens, program=0):
+        q = rng.standard_normal((tokens, hq, d)).astype(np.float32)
+        inputs = {"q": (q, S.F32)}
+        if program == 0:
+            k = rng.standard_normal((tokens, hkv, d)).astype(np.float32)
+            v = rng.standard_normal((tokens, hkv, d)).astype(np.float32)
+            inputs.update({"k": (k, S.F32), "v": (v, S.F32)})
+            cache.append(k, v)
+        o = s.run(inputs, program=program)["o"]
+        attention_close(o, ora.attention(q, cache.k, cache.v, scale, softcap, window, True),
+                        f"program {program}, {tokens} tokens at L {len(cache.k)}", atol=1e-4, rtol=1e-4)
+
+    one(7)
+    for _ in range(3):
+        one(1)
+    one(2, program=1)
+    s.truncate(6)
+    cache.truncate(6)
+    one(1)
+    one(3)
+    assert s.num_cached() == 10
+    s.reset()
+    cache.truncate(0)
     one(4)
 
 

@@ -222,12 +222,25 @@ struct Loc {
     int64_t row_stride = 0;  // strided views: bytes between rows (0: contiguous)
 };
 
+// Bytes of one row (a token's head of `dim` values) of a quantized format: its codes, and the scales beside them
+// (quant::kv_row_bytes, reference src/quant/kv_format.cpp:45-55).
+int64_t kv_code_bytes(quant::KvFormat f, int64_t dim) {
+    const int bits = quant::turbo_bits(f);
+    return bits == 0 ? dim : dim / 128 * 16 * bits;
+}
+int64_t kv_scale_bytes(quant::KvFormat f, int64_t dim) { return quant::turbo_bits(f) == 0 ? 4 : dim / 128 * 2; }
+xs_kv_format kv_abi(quant::KvFormat f) { return static_cast<xs_kv_format>(static_cast<int>(f)); }
+
 struct KvState {
     int64_t heads = 0, dim = 0, cap = 0;
     int64_t len = 0;
-    // What the slot stores (SessionOptions::kv): I8 -- codes int8 [cap, heads, dim] in kc / vc and scales f32
-    // [cap, heads] in ks / vs; or the Float format's rows [cap, heads, dim] of F16 (f16 precision) or F32 in kc / vc.
+    // What the slot stores (SessionOptions::kv), for the keys (kc, ks) and the values (vc, vs): I8 -- codes int8
+    // [cap, heads, dim] and scales f32 [cap, heads]; a TurboQuant format -- codes [cap * heads * dim / 128, 16 bits]
+    // bytes and f16 norms [cap * heads * dim / 128]; or, both streams alike, the Float format's rows [cap, heads,
+    // dim] of F16 (f16 precision) or F32 in kc / vc. `rows` is the Float format's row type, I8 for the others.
     DType rows = DType::I8;
+    quant::KvFormat kf = quant::KvFormat::I8, vf = quant::KvFormat::I8;
+    bool both_i8() const { return kf == quant::KvFormat::I8 && vf == quant::KvFormat::I8; }
     DeviceMemory kc, ks, vc, vs;
     std::string label;
 };
@@ -345,7 +358,11 @@ public:
         ++arena_gen_;
     }
     // HIP-graph replay of repeated steps: the "graphs" backend option ("1", the default, or "0").
-    bool graphs() const { return graphs_; }
+    // Steps replay from captured HIP graphs unless the graphs option is off or a KV stream is TurboQuant (whose
+    // append takes its first row from the host).
+    bool graphs() const {
+        return graphs_ && quant::turbo_bits(options_.kv.k) == 0 && quant::turbo_bits(options_.kv.v) == 0;
+    }
     // The step record a replayed step reads from device memory: [first token the step appends, keys held]. Its host
     // copy is the first 16 bytes of the staging.
     const int64_t* step_record() const { return reinterpret_cast<const int64_t*>(step_.get()); }
@@ -374,7 +391,12 @@ public:
         k.dim = s.head_dim;
         k.cap = options_.max_context;
         k.label = s.label;
-        k.rows = options_.kv.k == quant::KvFormat::I8 ? DType::I8 : options_.precision;
+        k.kf = options_.kv.k;
+        k.vf = options_.kv.v;
+        k.rows = options_.kv.k == quant::KvFormat::Float ? options_.precision : DType::I8;
+        XS_CHECK((quant::turbo_bits(k.kf) == 0 && quant::turbo_bits(k.vf) == 0) || k.dim % 128 == 0,
+                 "hip: kv slot '", s.label, "': a TurboQuant KV format needs a head_dim that is a multiple of 128, got ",
+                 k.dim);
         kv_.push_back(std::move(k));
         return static_cast<int>(kv_.size() - 1);
     }
@@ -533,9 +555,12 @@ Program::Program(const Graph& g, HipSession& s, size_t index) : g_(g), s_(s), in
     }
     if (!g_.kv_slots().empty()) {
         const auto& kv = s_.options().kv;
-        XS_CHECK(kv.k == kv.v && (kv.k == quant::KvFormat::I8 || kv.k == quant::KvFormat::Float),
-                 "hip: the KV cache format ", quant::kv_format_name(kv.k), ":", quant::kv_format_name(kv.v),
-                 " is not supported; this backend stores keys and values as i8, or as the precision's float (auto)");
+        // The pairs the reference's device reads (sycl_kernels.h:209-212): one format for both, or int8 keys with
+        // TurboQuant values.
+        XS_CHECK(kv.k == kv.v || (kv.k == quant::KvFormat::I8 && quant::turbo_bits(kv.v) != 0),
+                 "hip: a KV cache with keys in ", quant::kv_format_name(kv.k), " and values in ",
+                 quant::kv_format_name(kv.v),
+                 " is not supported: both take one format, or the keys i8 and the values a turbo format");
         for (const auto& slot : g_.kv_slots()) slot_of_.push_back(s_.slot_for(slot));
     }
     for (const Node& nd : nodes) {
@@ -1289,6 +1314,20 @@ void Program::launch(size_t i, const RunPlan& p, int64_t T, int64_t L, int64_t r
                 }
                 return;
             }
+            if (!kv.both_i8()) {  // a TurboQuant stream (never replayed from a captured graph: see replayable)
+                XS_CHECK(replay_cap == 0, "hip: a TurboQuant KV cache is appended outside captured graphs");
+                for (int which = 0; which < 2; ++which) {
+                    const quant::KvFormat f = which == 0 ? kv.kf : kv.vf;
+                    const Value x = np.reads[static_cast<size_t>(which)];
+                    const int64_t cb = kv_code_bytes(f, kv.dim), sb = kv_scale_bytes(f, kv.dim);
+                    check(xs_hip_quantize_kv(st, kv_abi(f), abi(dtype(x)), ptr(p, x),
+                                             (which == 0 ? kv.kc : kv.vc).get() + first * kv.heads * cb,
+                                             (which == 0 ? kv.ks : kv.vs).get() + first * kv.heads * sb, T * kv.heads,
+                                             kv.dim),
+                          "KvCache");
+                }
+                return;
+            }
             if (dtype(k) == dtype(v)) {  // keys and values in one launch
                 const bool at = replay_cap > 0;  // the first token read from the step record at replay
                 const int64_t skip = at ? 0 : first * kv.heads;
@@ -1322,8 +1361,8 @@ void Program::launch(size_t i, const RunPlan& p, int64_t T, int64_t L, int64_t r
             KvState& kv = s_.kv()[static_cast<size_t>(kl.id)];
             const Dims& qs = in_shape(q);
             const int64_t keys = replay_cap > 0 ? replay_cap : L;
-            const int64_t split = kv.rows == DType::I8 ? xs_hip_attention_i8_split(qs[0], kv.heads, keys)
-                                                       : xs_hip_attention_rows_split(qs[0], kv.heads, keys);
+            const int64_t split = kv.both_i8() ? xs_hip_attention_i8_split(qs[0], kv.heads, keys)
+                                               : xs_hip_attention_rows_split(qs[0], kv.heads, keys);
             auto* out_p = reinterpret_cast<float*>(ptr(p, Value{static_cast<int32_t>(i), 0}));
             char* scratch = split > 1 ? s_.arena().get() + p.block_offset[static_cast<size_t>(p.scratch[i])] : nullptr;
             if (kv.rows != DType::I8) {  // the Float format's rows
@@ -1338,6 +1377,14 @@ void Program::launch(size_t i, const RunPlan& p, int64_t T, int64_t L, int64_t r
                                            split, scratch),
                           what);
                 }
+                return;
+            }
+            if (!kv.both_i8()) {  // TurboQuant values, with keys in the same format or in int8
+                check(xs_hip_attention_quantized(st, kv_abi(kv.kf), kv_abi(kv.vf), f32(0), kv.kc.get(), kv.ks.get(),
+                                                 kv.vc.get(), kv.vs.get(), out_p, qs[0], qs[1], kv.heads, qs[2], L,
+                                                 a.scale, a.softcap, a.sliding_window, a.causal ? 1 : 0, split,
+                                                 scratch),
+                      what);
                 return;
             }
             if (replay_cap > 0) {  // the key count read from the step record at replay
@@ -1576,12 +1623,15 @@ HipSession::HipSession(std::span<const Graph* const> programs, const WeightStore
     try {
         for (KvState& k : kv_) {
             const auto rows = static_cast<size_t>(k.cap * k.heads);
-            const size_t width = static_cast<size_t>(k.dim) * dtype_size(k.rows);
-            k.kc.grow(rows * width);
-            k.vc.grow(rows * width);
-            if (k.rows == DType::I8) {
-                k.ks.grow(rows * 4);
-                k.vs.grow(rows * 4);
+            if (k.kf == quant::KvFormat::Float) {
+                const size_t width = static_cast<size_t>(k.dim) * dtype_size(k.rows);
+                k.kc.grow(rows * width);
+                k.vc.grow(rows * width);
+            } else {
+                k.kc.grow(rows * static_cast<size_t>(kv_code_bytes(k.kf, k.dim)));
+                k.ks.grow(rows * static_cast<size_t>(kv_scale_bytes(k.kf, k.dim)));
+                k.vc.grow(rows * static_cast<size_t>(kv_code_bytes(k.vf, k.dim)));
+                k.vs.grow(rows * static_cast<size_t>(kv_scale_bytes(k.vf, k.dim)));
             }
         }
         step_.grow(2 * sizeof(int64_t));
