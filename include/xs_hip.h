@@ -73,7 +73,8 @@ typedef enum {
 typedef enum { XS_BINARY_ADD = 0, XS_BINARY_MUL = 1, XS_BINARY_DIV = 2 } xs_binary_op;
 
 /* `xs::quant::KvFormat` (src/quant/kv_format.h:11-17). xs_hip_quantize_kv / xs_hip_dequantize_kv take XS_KV_I8 and
- * the TurboQuant formats; the Float format's rows are written by xs_hip_kv_store_pair and read by xs_hip_attention. */
+ * the TurboQuant formats, read by xs_hip_attention_i8 and xs_hip_attention_quantized; the Float format's rows are
+ * written by xs_hip_kv_store_pair and read by xs_hip_attention. */
 typedef enum { XS_KV_FLOAT = 0, XS_KV_I8 = 1, XS_KV_TURBO4 = 2, XS_KV_TURBO3 = 3, XS_KV_TURBO2 = 4 } xs_kv_format;
 
 /* numpy broadcasting over at most XS_MAX_RANK dims: the out shape and the element strides of a, b and y per out dim.

@@ -1,4 +1,5 @@
-// Decode attention over an int8 KV cache for gfx950: the reader of the codes and scales xs_hip_quantize_kv writes.
+// Decode attention for gfx950 over the KV caches: the int8 reader of the codes and scales xs_hip_quantize_kv writes
+// (this header), and further down one reader for the Float format's rows and the TurboQuant caches.
 //
 // Semantics: cpu_ref::attention / attend_one (reference src/backend/cpu_ref/ops.cpp:113-156, 535-594) over the
 // values the int8 cache stores, fl32(code * scale) (quant::round_trip_kv_i8, src/quant/quant.cpp:269-277; the CPU

@@ -33,14 +33,18 @@
 //  - a KvCache's keys and values, of one dtype: one quantize launch (no reference counterpart).
 // Reshape is a view; Slice is a view when it keeps whole leading rows or only an act-bias-mul reads it, else a copy.
 //
-// KV formats (SessionOptions::kv): i8 keys and values (int8 codes and f32 scales), or the Float format -- rows of the
-// precision's float (f16 at f16 precision, the reference's default; f32 at f32), as the SYCL session stores them.
-// SessionOptions::precision is f16 or f32, as for cpu-ref (cpu_backend.cpp:75-76), and as there the activations are
-// computed and kept in f32 either way (cpu_backend.cpp:611); the precision picks the Float format's row type.
+// KV formats (SessionOptions::kv): every pair the reference's device takes -- the Float format (rows of the
+// precision's float: f16 at f16 precision, the reference's default; f32 at f32), as the SYCL session stores them; i8
+// keys and values (int8 codes and f32 scales); a TurboQuant format for both (codes and f16 norms per 128 values); or i8
+// keys with TurboQuant values. Steps with a TurboQuant stream are launched one by one (their append takes its first
+// row from the host). SessionOptions::precision is f16 or f32, as for cpu-ref (cpu_backend.cpp:75-76), and as there
+// the activations are computed and kept in f32 either way (cpu_backend.cpp:611); the precision picks the Float
+// format's row type.
 //
 // What it refuses: MatMul and the other ops with no kernel here (the GEMM path is outside this library), a precision
-// other than f16 or f32, the TurboQuant KV formats and mixed key/value formats, KV outputs read by anything but
-// Attention, and attention with a key bias, groups, blocks, relative bias or an anchored window.
+// other than f16 or f32, the KV format pairs the reference's device refuses too, a TurboQuant format over a head_dim
+// that is not a multiple of 128, KV outputs read by anything but Attention, and attention with a key bias, groups,
+// blocks, relative bias or an anchored window.
 #include <algorithm>
 #include <cstring>
 #include <limits>
