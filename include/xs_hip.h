@@ -287,6 +287,13 @@ int xs_hip_dequantize_kv(void* stream, xs_kv_format format, const void* codes, c
  * cache writes nothing. */
 int xs_hip_quantize_kv_at(void* stream, xs_dtype x_dtype, const void* x, void* codes, void* scales, int64_t rows,
                           int64_t width, const int64_t* row0, int64_t rows_per_unit, int64_t capacity_rows);
+/* No counterpart in the reference, as xs_hip_quantize_kv_at: the TurboQuant quantize (format XS_KV_TURBO4, 3 or 2) of
+ * `rows` rows, written at rows row0[0] * rows_per_unit + r of a cache of `capacity_rows` rows (codes
+ * [capacity_rows * width / 128, 16 * bits] bytes, f16 norms [capacity_rows * width / 128]); a destination outside the
+ * cache writes nothing. */
+int xs_hip_quantize_kv_turbo_at(void* stream, xs_kv_format format, xs_dtype x_dtype, const void* x, void* codes,
+                                void* norms, int64_t rows, int64_t width, const int64_t* row0, int64_t rows_per_unit,
+                                int64_t capacity_rows);
 /* No counterpart in the reference (it appends keys and values by two launches): the XS_KV_I8 quantize of a step's
  * keys k and values v, both [rows, width] of x_dtype, in one launch, into their own caches -- at rows [0, rows) of
  * k_codes / k_scales and v_codes / v_scales with row0 NULL, or at the device-held row as xs_hip_quantize_kv_at. The

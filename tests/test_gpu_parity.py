@@ -1261,6 +1261,38 @@ def test_quantize_kv_at_device_row(ora):
             assert_exact(gs.view(np.uint32), want_s.view(np.uint32), f"scales at token {tok0}")
 
 
+@pytest.mark.parametrize("bits", [4, 3, 2])
+def test_quantize_kv_turbo_at_device_row(ora, bits):
+    """xs_hip_quantize_kv_turbo_at: the groups land at the rows row0[0] * unit of the cache, bit-exact with
+    xs_hip_quantize_kv in the same format (the oracle's codes and norms), nothing else changes; a destination outside
+    the cache writes nothing."""
+    rng = np.random.default_rng(76 + bits)
+    heads, d, cap_tokens, t = 2, 256, 24, 3
+    gpr = d // 128
+    x = rng.standard_normal((t * heads, d)).astype(np.float32)
+    wc, wn = ora.turbo_quantize(x, bits)
+    for tok0, lands in ((4, True), (cap_tokens - t, True), (cap_tokens - t + 1, False), (-2, False)):
+        step(f"quantize_kv_turbo_at turbo{bits} token {tok0}")
+        codes = X.DeviceTensor.empty(X.U8, (cap_tokens * heads * gpr, 16 * bits))
+        norms = X.DeviceTensor.empty(F16, (cap_tokens * heads * gpr,))
+        X.call("xs_hip_memset", C.c_void_p(codes.ptr), 0x5A, C.c_size_t(codes.nbytes), None)
+        X.call("xs_hip_memset", C.c_void_p(norms.ptr), 0x5A, C.c_size_t(norms.nbytes), None)
+        row0 = _dev_i64(tok0)
+        xd = dev(x)
+        X.call("xs_hip_quantize_kv_turbo_at", None, X.TURBO_FORMAT[bits], F32, C.c_void_p(xd.ptr),
+               C.c_void_p(codes.ptr), C.c_void_p(norms.ptr), t * heads, d, C.c_void_p(row0.ptr), heads,
+               cap_tokens * heads)
+        gc, gn = codes.numpy(), norms.numpy().view(np.uint16)
+        want_c = np.full_like(gc, 0x5A)
+        want_n = np.full(gn.shape, 0x5A5A, np.uint16)
+        if lands:
+            g0 = tok0 * heads * gpr
+            want_c[g0:g0 + t * heads * gpr] = wc
+            want_n[g0:g0 + t * heads * gpr] = wn
+        assert_exact(gc, want_c, f"turbo{bits} codes at token {tok0}")
+        assert_exact(gn, want_n, f"turbo{bits} norms at token {tok0}")
+
+
 @pytest.mark.parametrize("xdt,width", [(F32, 128), (F16, 128), (BF16, 64), (F32, 100)])
 def test_quantize_kv_pair(ora, xdt, width):
     """xs_hip_quantize_kv_pair: keys and values in one launch, each bit-exact with xs_hip_quantize_kv, at the buffers'

@@ -573,6 +573,46 @@ def test_float_kv_many_steps(ora, graphs):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("kbits,vbits", [(4, 4), (8, 3)])
+@pytest.mark.parametrize("graphs", ["1", "0"])
+def test_turbo_kv_many_steps(ora, kbits, vbits, graphs):
+    """Forty decode steps over a TurboQuant cache with the repeated steps replayed from captured graphs (the append's
+    row read from the device step record by xs_hip_quantize_kv_turbo_at, the key count by
+    xs_hip_attention_quantized_at) or launched one by one, against cpu-ref's cache of round-tripped rows."""
+    hq, hkv, d = 8, 2, 128
+    rng = np.random.default_rng(98 + kbits)
+    prefill, reader = _kv_programs(hq, hkv, d)
+    step(f"session kv {kbits}:{vbits} 40 steps graphs={graphs}")
+    s = S.Session([prefill, reader], max_context=64, kv=(TURBO_KV[kbits], TURBO_KV[vbits]), options={"graphs": graphs})
+    cache = _TurboCache(ora, hkv, d, kbits, vbits)
+    scale = 1 / math.sqrt(d)
+
+    def one(tokens, program=0):
+        q = rng.standard_normal((tokens, hq, d)).astype(np.float32)
+        inputs = {"q": (q, S.F32)}
+        if program == 0:
+            k = rng.standard_normal((tokens, hkv, d)).astype(np.float32)
+            v = rng.standard_normal((tokens, hkv, d)).astype(np.float32)
+            inputs.update({"k": (k, S.F32), "v": (v, S.F32)})
+            cache.append(k, v)
+        o = s.run(inputs, program=program)["o"]
+        attention_close(o, ora.attention(q, cache.k, cache.v, scale, 0.0, 0, True),
+                        f"graphs={graphs} program {program}, {tokens} tokens at L {len(cache.k)}", atol=1e-4,
+                        rtol=1e-4)
+
+    one(8)
+    for i in range(40):
+        one(1)
+        if i % 9 == 4:
+            one(1, program=1)
+    s.truncate(20)
+    cache.truncate(20)
+    for _ in range(5):
+        one(1)
+    assert s.num_cached() == 25
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("graphs", ["1", "0"])
 def test_kv_decode_many_steps(ora, graphs):
     """Forty decode steps after a prefill, through key counts 9 .. 49 (length buckets 16, 32 and 64), with the

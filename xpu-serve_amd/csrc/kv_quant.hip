@@ -460,6 +460,22 @@ int xs_hip_quantize_kv_at(void* stream, xs_dtype x_dtype, const void* x, void* c
                        what);
 }
 
+int xs_hip_quantize_kv_turbo_at(void* stream, xs_kv_format format, xs_dtype x_dtype, const void* x, void* codes,
+                                void* norms, int64_t rows, int64_t width, const int64_t* row0, int64_t rows_per_unit,
+                                int64_t capacity_rows) {
+    const char* what = "xs_hip_quantize_kv_turbo_at";
+    if (format < XS_KV_TURBO4 || format > XS_KV_TURBO2)
+        return fail(XS_HIP_EINVAL, std::string(what) + ": format " + std::to_string(static_cast<int>(format)) +
+                                       " is not a TurboQuant format");
+    if (rows < 0 || rows_per_unit < 0 || capacity_rows < 0)
+        return fail(XS_HIP_EINVAL, std::string(what) + ": rows " + std::to_string(rows) + ", " +
+                                       std::to_string(rows_per_unit) + " rows a unit, capacity " +
+                                       std::to_string(capacity_rows));
+    if (row0 == nullptr) return fail(XS_HIP_EINVAL, std::string(what) + ": null row0");
+    return turbo_quantize(as_stream(stream), turbo_bits(format), x_dtype, x, codes, norms, rows, width, row0,
+                          rows_per_unit, capacity_rows);
+}
+
 int xs_hip_dequantize_kv(void* stream, xs_kv_format format, const void* codes, const void* scales, xs_dtype out_dtype,
                          void* out, int64_t rows, int64_t width) {
     int rc = check_kv_format(format, "xs_hip_dequantize_kv");

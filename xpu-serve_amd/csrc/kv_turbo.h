@@ -9,8 +9,11 @@ namespace xs_hip {
 
 // Rows [rows, width] (width a multiple of 128) as codes [rows * width / 128, 16 * bits] bytes and f16 norms
 // [rows * width / 128]; bits 4, 3 or 2.
+// With row0 set, the rows go to row row0[0] * rows_per_unit + r of a cache of capacity_rows rows (read from device
+// memory when the kernel runs); a destination outside the cache writes nothing.
 int turbo_quantize(hipStream_t s, int bits, xs_dtype x_dtype, const void* x, void* codes, void* norms, int64_t rows,
-                   int64_t width);
+                   int64_t width, const int64_t* row0 = nullptr, int64_t rows_per_unit = 0,
+                   int64_t capacity_rows = 0);
 // The rotated values such codes and norms store, in out_dtype.
 int turbo_dequantize(hipStream_t s, int bits, const void* codes, const void* norms, xs_dtype out_dtype, void* out,
                      int64_t rows, int64_t width);

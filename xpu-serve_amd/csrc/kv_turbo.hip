@@ -43,10 +43,20 @@ __device__ __forceinline__ void load_lane(const typename X::storage* x, float* v
 // Groups a 16-lane set quantizes in turn: its sign masks and tables are made once for all of them.
 constexpr int kQuantRounds = 4;
 
+// With `row0` set, the groups go to group row0[0] * unit_groups + g of a cache of cap_groups groups (the destination
+// read from device memory when the kernel runs); a destination outside the cache writes nothing.
 template <int Bits, typename X>
 __global__ __launch_bounds__(kBlock) void turbo_quantize_kernel(const typename X::storage* __restrict__ x,
                                                                 uint8_t* __restrict__ codes,
-                                                                uint16_t* __restrict__ norms, int64_t groups) {
+                                                                uint16_t* __restrict__ norms, int64_t groups,
+                                                                const int64_t* row0 = nullptr, int64_t unit_groups = 0,
+                                                                int64_t cap_groups = 0) {
+    if (row0 != nullptr) {
+        const int64_t off = row0[0] * unit_groups;
+        if (off < 0 || off > cap_groups - groups) return;
+        codes += off * (kGroup * Bits / 8);
+        norms += off;
+    }
     constexpr int NM = kMagnitudes<Bits>;
     __shared__ float mag_sq[NM];
     if (threadIdx.x < NM) mag_sq[threadIdx.x] = Book<Bits>::mags[threadIdx.x] * Book<Bits>::mags[threadIdx.x];
@@ -203,19 +213,21 @@ unsigned blocks_for(int64_t groups, int rounds = 1, int per_block = kGroupsPerBl
 }
 
 template <int Bits>
-int quantize_bits(hipStream_t s, xs_dtype x_dtype, const void* x, uint8_t* codes, uint16_t* norms, int64_t groups) {
+int quantize_bits(hipStream_t s, xs_dtype x_dtype, const void* x, uint8_t* codes, uint16_t* norms, int64_t groups,
+                  const int64_t* row0, int64_t unit_groups, int64_t cap_groups) {
+    const unsigned grid = blocks_for(groups, kQuantRounds);
     switch (x_dtype) {
         case XS_F32:
-            turbo_quantize_kernel<Bits, F32><<<blocks_for(groups, kQuantRounds), kBlock, 0, s>>>(static_cast<const float*>(x), codes,
-                                                                                   norms, groups);
+            turbo_quantize_kernel<Bits, F32><<<grid, kBlock, 0, s>>>(static_cast<const float*>(x), codes, norms, groups,
+                                                                     row0, unit_groups, cap_groups);
             break;
         case XS_F16:
-            turbo_quantize_kernel<Bits, F16><<<blocks_for(groups, kQuantRounds), kBlock, 0, s>>>(static_cast<const uint16_t*>(x),
-                                                                                   codes, norms, groups);
+            turbo_quantize_kernel<Bits, F16><<<grid, kBlock, 0, s>>>(static_cast<const uint16_t*>(x), codes, norms,
+                                                                     groups, row0, unit_groups, cap_groups);
             break;
         case XS_BF16:
-            turbo_quantize_kernel<Bits, BF16><<<blocks_for(groups, kQuantRounds), kBlock, 0, s>>>(static_cast<const uint16_t*>(x),
-                                                                                    codes, norms, groups);
+            turbo_quantize_kernel<Bits, BF16><<<grid, kBlock, 0, s>>>(static_cast<const uint16_t*>(x), codes, norms,
+                                                                      groups, row0, unit_groups, cap_groups);
             break;
         default:
             return fail(XS_HIP_EINVAL, std::string("xs_hip_quantize_kv: x must be f32, f16 or bf16, got ") +
@@ -261,19 +273,23 @@ int check_turbo(const char* op, int64_t rows, int64_t width, const void* a, cons
 }  // namespace
 
 int turbo_quantize(hipStream_t s, int bits, xs_dtype x_dtype, const void* x, void* codes, void* norms, int64_t rows,
-                   int64_t width) {
+                   int64_t width, const int64_t* row0, int64_t rows_per_unit, int64_t capacity_rows) {
     int rc = check_turbo("xs_hip_quantize_kv", rows, width, x, codes, norms);
     if (rc != XS_HIP_OK || rows == 0) return rc;
     if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(codes) % 4 != 0 ||
         reinterpret_cast<uintptr_t>(norms) % 2 != 0)
         return fail(XS_HIP_EINVAL, "xs_hip_quantize_kv: TurboQuant needs x 16-byte, codes 4-byte and norms 2-byte "
                                    "aligned");
-    const int64_t groups = rows * (width / kGroup);
+    if (row0 != nullptr && reinterpret_cast<uintptr_t>(row0) % 8 != 0)
+        return fail(XS_HIP_EINVAL, "xs_hip_quantize_kv: row0 must be 8-byte aligned");
+    const int64_t gpr = width / kGroup;  // groups a row
+    const int64_t groups = rows * gpr;
     auto* c = static_cast<uint8_t*>(codes);
     auto* nm = static_cast<uint16_t*>(norms);
-    if (bits == 4) return quantize_bits<4>(s, x_dtype, x, c, nm, groups);
-    if (bits == 3) return quantize_bits<3>(s, x_dtype, x, c, nm, groups);
-    return quantize_bits<2>(s, x_dtype, x, c, nm, groups);
+    const int64_t ug = rows_per_unit * gpr, cg = capacity_rows * gpr;
+    if (bits == 4) return quantize_bits<4>(s, x_dtype, x, c, nm, groups, row0, ug, cg);
+    if (bits == 3) return quantize_bits<3>(s, x_dtype, x, c, nm, groups, row0, ug, cg);
+    return quantize_bits<2>(s, x_dtype, x, c, nm, groups, row0, ug, cg);
 }
 
 int turbo_dequantize(hipStream_t s, int bits, const void* codes, const void* norms, xs_dtype out_dtype, void* out,

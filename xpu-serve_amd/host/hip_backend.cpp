@@ -36,8 +36,7 @@
 // KV formats (SessionOptions::kv): every pair the reference's device takes -- the Float format (rows of the
 // precision's float: f16 at f16 precision, the reference's default; f32 at f32), as the SYCL session stores them; i8
 // keys and values (int8 codes and f32 scales); a TurboQuant format for both (codes and f16 norms per 128 values); or i8
-// keys with TurboQuant values. Steps with a TurboQuant stream are launched one by one (their append takes its first
-// row from the host). SessionOptions::precision is f16 or f32, as for cpu-ref (cpu_backend.cpp:75-76), and as there
+// keys with TurboQuant values. SessionOptions::precision is f16 or f32, as for cpu-ref (cpu_backend.cpp:75-76), and as there
 // the activations are computed and kept in f32 either way (cpu_backend.cpp:611); the precision picks the Float
 // format's row type.
 //
@@ -362,11 +361,7 @@ public:
         ++arena_gen_;
     }
     // HIP-graph replay of repeated steps: the "graphs" backend option ("1", the default, or "0").
-    // Steps replay from captured HIP graphs unless the graphs option is off or a KV stream is TurboQuant (whose
-    // append takes its first row from the host).
-    bool graphs() const {
-        return graphs_ && quant::turbo_bits(options_.kv.k) == 0 && quant::turbo_bits(options_.kv.v) == 0;
-    }
+    bool graphs() const { return graphs_; }
     // The step record a replayed step reads from device memory: [first token the step appends, keys held]. Its host
     // copy is the first 16 bytes of the staging.
     const int64_t* step_record() const { return reinterpret_cast<const int64_t*>(step_.get()); }
@@ -1318,17 +1313,29 @@ void Program::launch(size_t i, const RunPlan& p, int64_t T, int64_t L, int64_t r
                 }
                 return;
             }
-            if (!kv.both_i8()) {  // a TurboQuant stream (never replayed from a captured graph: see replayable)
-                XS_CHECK(replay_cap == 0, "hip: a TurboQuant KV cache is appended outside captured graphs");
+            if (!kv.both_i8()) {  // a TurboQuant stream: keys and values by a launch each
                 for (int which = 0; which < 2; ++which) {
                     const quant::KvFormat f = which == 0 ? kv.kf : kv.vf;
                     const Value x = np.reads[static_cast<size_t>(which)];
-                    const int64_t cb = kv_code_bytes(f, kv.dim), sb = kv_scale_bytes(f, kv.dim);
-                    check(xs_hip_quantize_kv(st, kv_abi(f), abi(dtype(x)), ptr(p, x),
-                                             (which == 0 ? kv.kc : kv.vc).get() + first * kv.heads * cb,
-                                             (which == 0 ? kv.ks : kv.vs).get() + first * kv.heads * sb, T * kv.heads,
-                                             kv.dim),
-                          "KvCache");
+                    char* codes = (which == 0 ? kv.kc : kv.vc).get();
+                    char* scales = (which == 0 ? kv.ks : kv.vs).get();
+                    if (replay_cap > 0) {  // the first token read from the step record at replay
+                        if (f == quant::KvFormat::I8)
+                            check(xs_hip_quantize_kv_at(st, abi(dtype(x)), ptr(p, x), codes, scales, T * kv.heads,
+                                                        kv.dim, s_.step_record(), kv.heads, kv.cap * kv.heads),
+                                  "KvCache");
+                        else
+                            check(xs_hip_quantize_kv_turbo_at(st, kv_abi(f), abi(dtype(x)), ptr(p, x), codes, scales,
+                                                              T * kv.heads, kv.dim, s_.step_record(), kv.heads,
+                                                              kv.cap * kv.heads),
+                                  "KvCache");
+                    } else {
+                        const int64_t cb = kv_code_bytes(f, kv.dim), sb = kv_scale_bytes(f, kv.dim);
+                        check(xs_hip_quantize_kv(st, kv_abi(f), abi(dtype(x)), ptr(p, x),
+                                                 codes + first * kv.heads * cb, scales + first * kv.heads * sb,
+                                                 T * kv.heads, kv.dim),
+                              "KvCache");
+                    }
                 }
                 return;
             }
@@ -1384,11 +1391,19 @@ void Program::launch(size_t i, const RunPlan& p, int64_t T, int64_t L, int64_t r
                 return;
             }
             if (!kv.both_i8()) {  // TurboQuant values, with keys in the same format or in int8
-                check(xs_hip_attention_quantized(st, kv_abi(kv.kf), kv_abi(kv.vf), f32(0), kv.kc.get(), kv.ks.get(),
-                                                 kv.vc.get(), kv.vs.get(), out_p, qs[0], qs[1], kv.heads, qs[2], L,
-                                                 a.scale, a.softcap, a.sliding_window, a.causal ? 1 : 0, split,
-                                                 scratch),
-                      what);
+                if (replay_cap > 0) {  // the key count read from the step record at replay
+                    check(xs_hip_attention_quantized_at(st, kv_abi(kv.kf), kv_abi(kv.vf), f32(0), kv.kc.get(),
+                                                        kv.ks.get(), kv.vc.get(), kv.vs.get(), out_p, qs[0], qs[1],
+                                                        kv.heads, qs[2], kv.cap, s_.step_record() + 1, a.scale,
+                                                        a.softcap, a.sliding_window, a.causal ? 1 : 0, split, scratch),
+                          what);
+                } else {
+                    check(xs_hip_attention_quantized(st, kv_abi(kv.kf), kv_abi(kv.vf), f32(0), kv.kc.get(),
+                                                     kv.ks.get(), kv.vc.get(), kv.vs.get(), out_p, qs[0], qs[1],
+                                                     kv.heads, qs[2], L, a.scale, a.softcap, a.sliding_window,
+                                                     a.causal ? 1 : 0, split, scratch),
+                          what);
+                }
                 return;
             }
             if (replay_cap > 0) {  // the key count read from the step record at replay

@@ -112,6 +112,7 @@ _SIGS = {
     "xs_hip_quantize_kv": [_P, _INT, _INT, _P, _P, _P, _I64, _I64],
     "xs_hip_dequantize_kv": [_P, _INT, _P, _P, _INT, _P, _I64, _I64],
     "xs_hip_quantize_kv_at": [_P, _INT, _P, _P, _P, _I64, _I64, _P, _I64, _I64],
+    "xs_hip_quantize_kv_turbo_at": [_P, _INT, _INT, _P, _P, _P, _I64, _I64, _P, _I64, _I64],
     "xs_hip_quantize_kv_pair": [_P, _INT, _P, _P, _P, _P, _P, _P, _I64, _I64, _P, _I64, _I64],
     "xs_hip_copy": [_P, _P, _P, C.c_size_t],
     "xs_hip_copy_rows": [_P, _P, _I64, _P, _I64, _I64, _I64],
