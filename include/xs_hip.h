@@ -398,6 +398,28 @@ int xs_hip_attention_i8_noalloc(void* stream, const float* q, const void* k_code
                                 int64_t kv_heads, int64_t head_dim, int64_t kv_len, float scale, float softcap,
                                 int64_t window, int causal, int64_t split);
 
+/* ---- Data movement: gather, transpose, concat ------------------------------------------------------------------ */
+
+/* out [n, width] = rows ids[r] of table [rows, width] -- an embedding lookup. table f32, f16 or bf16 gives f32 rows
+ * (f16 / bf16 widened exactly); an i32 table gives its rows' bits as they are (i32 out). ids i32 or i64. An id outside
+ * [0, rows) gives a row of zeros (cpu-ref refuses it by name; the device keeps every access inside the table).
+ * cpu_ref::gather (ops.cpp:157-173, cpu_backend.cpp:370); replaces sycl_be::gather / gather_bits
+ * (sycl_kernels.h:106-110). */
+int xs_hip_gather(void* stream, xs_dtype table_dtype, const void* table, int64_t rows, int64_t width,
+                  xs_dtype ids_dtype, const void* ids, int64_t n, void* out);
+/* y = x with its axes permuted: y.shape[i] = in_shape[perm[i]], elements of elem_bytes (1, 2, 4 or 8) moved as they
+ * are; rank 1 to XS_MAX_RANK. cpu_ref::transpose (ops.cpp:312-340); replaces sycl_be::transpose (sycl_kernels.h:
+ * 121-128). */
+int xs_hip_transpose(void* stream, const void* x, void* y, int64_t elem_bytes, int rank, const int64_t* in_shape,
+                     const int32_t* perm);
+/* The parts joined along an axis: `outer` rows (the product of the dims before the axis), each the parts' rows laid
+ * end to end -- part k contributes part_row_bytes[k] bytes from parts[k] + o * part_row_bytes[k]. 1 to
+ * XS_CONCAT_PARTS parts, any element type. cpu_ref::concat (ops.cpp:616-637); replaces sycl_be::concat
+ * (sycl_kernels.h:95-104, kConcatParts). */
+#define XS_CONCAT_PARTS 8
+int xs_hip_concat(void* stream, int count, const void* const* parts, const int64_t* part_row_bytes, void* out,
+                  int64_t outer);
+
 /* ---- Strided copy -------------------------------------------------------------------------------------------- */
 
 /* y[r, :] = x[r, :] for `rows` rows of `row_bytes` bytes, x rows `x_row_stride` bytes apart and y rows `y_row_stride`

@@ -27,6 +27,7 @@ ORACLE_LIB = os.path.join(HERE, "liboracle.so")
 REF_LIB = os.path.join(HERE, "_ref", "libxsref.so")
 
 F32, F16, BF16 = 0, 1, 2
+I64, I32 = 3, 4
 GELU_TANH, SIGMOID, SILU, GELU = 2, 4, 5, 8
 
 _fp = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
@@ -97,7 +98,29 @@ class _Turbo:
         return self.turbo_rotate(self.turbo_decode(codes, norms, bits), inverse=True).reshape(np.shape(x))
 
 
-class Oracle(_Base, _Turbo):
+class _Movement:
+    """Gather, Transpose and Concat restated on numpy: bytes moved as they are, a float table's rows widened exactly
+    to f32 (cpu_backend.cpp:370 hands cpu_ref::gather the table's f32 view)."""
+
+    def gather(self, table, ids, table_dtype=F32):
+        """cpu_ref::gather (ops.cpp:157-173): rows ids[...] of table [rows, width]; an id outside the table raises."""
+        ids = np.asarray(ids)
+        rows = table.shape[0]
+        if ids.size and (ids.min() < 0 or ids.max() >= rows):
+            raise ValueError(f"gather id outside the table of {rows} rows")
+        t = np.asarray(table, np.int32) if table_dtype == I32 else self.widen(table, table_dtype)
+        return t[ids.astype(np.int64)]
+
+    def transpose(self, x, perm):
+        """cpu_ref::transpose (ops.cpp:312-340): out.shape[i] = x.shape[perm[i]], elements as they are."""
+        return np.ascontiguousarray(np.transpose(x, perm))
+
+    def concat(self, parts, axis):
+        """cpu_ref::concat (ops.cpp:616-637): the parts' rows end to end along `axis`."""
+        return np.ascontiguousarray(np.concatenate(parts, axis=axis))
+
+
+class Oracle(_Base, _Turbo, _Movement):
     """The restatement (oracle/oracle.cpp)."""
 
     def __init__(self, path: str = ORACLE_LIB):
@@ -366,6 +389,9 @@ class Reference(_Base, _Turbo):
         L.xsref_turbo_quantize.argtypes = [_fp, _L, C.c_int, _u8, _u16]
         L.xsref_turbo_decode.argtypes = [_u8, _u16, _L, C.c_int, _fp]
         L.xsref_turbo_rotate.argtypes = [_fp, _L, C.c_int]
+        L.xsref_gather.argtypes = [C.c_int, _P, _L, _L, _P, C.c_int, _L, _P]
+        L.xsref_transpose.argtypes = [C.c_int, _P, _i64, C.c_int, _i32, _P]
+        L.xsref_concat.argtypes = [C.c_int, C.c_int, _P, _i64, C.c_int, C.c_int, _P]
         self.lib = L
 
     def _tq(self, *a):
@@ -447,6 +473,35 @@ class Reference(_Base, _Turbo):
         self._check(self.lib.xsref_attention(qq, k, v, qq.shape[0], q_heads, k.shape[1], d, n, scale, softcap, window,
                                              int(causal), int(kv_i8), out))
         return out[-tokens:] if cached else out
+
+    _INT_DT = {np.dtype(np.int32): I32, np.dtype(np.int64): I64, np.dtype(np.float32): F32}
+
+    def gather(self, table, ids, table_dtype=F32):
+        table = np.ascontiguousarray(table, np.int32 if table_dtype == I32 else storage(table_dtype))
+        ids = np.ascontiguousarray(ids)
+        rows, width = table.shape
+        out = np.empty(ids.shape + (width,), np.int32 if table_dtype == I32 else np.float32)
+        self._check(self.lib.xsref_gather(table_dtype, _ptr(table), rows, width, _ptr(ids),
+                                          int(ids.dtype == np.int64), ids.size, _ptr(out)))
+        return out
+
+    def transpose(self, x, perm):
+        x = np.ascontiguousarray(x)
+        out = np.empty(tuple(x.shape[p] for p in perm), x.dtype)
+        self._check(self.lib.xsref_transpose(self._INT_DT[x.dtype], _ptr(x), np.array(x.shape, np.int64), x.ndim,
+                                             np.array(perm, np.int32), _ptr(out)))
+        return out
+
+    def concat(self, parts, axis):
+        parts = [np.ascontiguousarray(p) for p in parts]
+        shape = list(parts[0].shape)
+        shape[axis] = sum(p.shape[axis] for p in parts)
+        out = np.empty(shape, parts[0].dtype)
+        ptrs = (C.c_void_p * len(parts))(*[p.ctypes.data for p in parts])
+        shapes = np.array([p.shape for p in parts], np.int64).reshape(-1)
+        self._check(self.lib.xsref_concat(self._INT_DT[parts[0].dtype], len(parts), C.cast(ptrs, C.c_void_p), shapes,
+                                          parts[0].ndim, axis, _ptr(out)))
+        return out
 
     def unary_op(self, op, x, a=0.0, b=0.0):
         x = np.ascontiguousarray(x, np.float32)

@@ -90,6 +90,56 @@ extern "C" {
 
 const char* xsref_last_error(void) { return g_error.c_str(); }
 
+// ---- data movement: Gather, Transpose, Concat (cpu_backend.cpp:369-370, 413-414, 479-484) ----
+
+void copy_raw(const HostTensor& t, void* dst) {
+    std::memcpy(dst, t.raw(), static_cast<size_t>(t.numel()) * dtype_size(t.dtype()));
+}
+
+// Rows ids [n] (i32, or i64 with ids_i64) of a table constant [rows, width] of DType table_dtype (F32, F16, BF16 or
+// I32); out f32 [n, width], or i32 for an i32 table.
+int xsref_gather(int table_dtype, const void* table, int64_t rows, int64_t width, const void* ids, int ids_i64,
+                 int64_t n, void* out) {
+    return guarded([&] {
+        const auto td = static_cast<DType>(table_dtype);
+        HostTensor t(td, {rows, width});
+        std::memcpy(t.raw(), table, static_cast<size_t>(rows * width) * dtype_size(td));
+        Graph g;
+        const DType it = ids_i64 ? DType::I64 : DType::I32;
+        g.output("out", g.gather(g.constant(t), g.input("ids", it, {n})));
+        copy_raw(run_graph(g, {{"ids", borrow(it, {n}, ids)}}).at("out"), out);
+    });
+}
+
+// x of DType dtype (F32, I32 or I64) and `shape`, its axes permuted by perm.
+int xsref_transpose(int dtype, const void* x, const int64_t* shape, int rank, const int32_t* perm, void* out) {
+    return guarded([&] {
+        const auto dt = static_cast<DType>(dtype);
+        Graph g;
+        g.output("out", g.transpose(g.input("x", dt, dims(shape, rank)), std::vector<int>(perm, perm + rank)));
+        copy_raw(run_graph(g, {{"x", borrow(dt, dims(shape, rank), x)}}).at("out"), out);
+    });
+}
+
+// `count` parts of DType dtype (F32, I32 or I64), part k of shape shapes[k * rank .. k * rank + rank), joined along
+// `axis`.
+int xsref_concat(int dtype, int count, const void* const* parts, const int64_t* shapes, int rank, int axis,
+                 void* out) {
+    return guarded([&] {
+        const auto dt = static_cast<DType>(dtype);
+        Graph g;
+        std::vector<Value> vs;
+        TensorMap in;
+        for (int k = 0; k < count; ++k) {
+            const std::string name = "p" + std::to_string(k);
+            vs.push_back(g.input(name, dt, dims(shapes + k * rank, rank)));
+            in.emplace(name, borrow(dt, dims(shapes + k * rank, rank), parts[k]));
+        }
+        g.output("out", g.concat(vs, axis));
+        copy_raw(run_graph(g, in).at("out"), out);
+    });
+}
+
 // ---- util/half ----
 void xsref_f32_to_f16(const float* x, uint16_t* y, int64_t n) { convert_f32_to_f16(x, y, static_cast<size_t>(n)); }
 void xsref_f16_to_f32(const uint16_t* x, float* y, int64_t n) { convert_f16_to_f32(x, y, static_cast<size_t>(n)); }

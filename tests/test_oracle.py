@@ -12,7 +12,7 @@ import os
 import numpy as np
 import pytest
 
-from oracle import BF16, F16, F32, GELU, GELU_TANH, SIGMOID, SILU, oracle, reference
+from oracle import BF16, F16, F32, GELU, GELU_TANH, I32, SIGMOID, SILU, oracle, reference
 from tol import assert_exact, assert_f32_close
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -720,3 +720,47 @@ def test_turbo_against_compiled_reference(ora):
         assert_exact(ora.turbo_decode(c1, n1, bits), ref.turbo_decode(c2, n2, bits), f"turbo{bits} decode")
     assert_exact(ora.turbo_rotate(x), ref.turbo_rotate(x), "rotate")
     assert_exact(ora.turbo_rotate(x, inverse=True), ref.turbo_rotate(x, inverse=True), "rotate back")
+
+
+# ---- data movement: Gather, Transpose, Concat ---------------------------------------------------------------------
+
+@pytest.mark.skipif(reference() is None, reason="oracle/_ref not built (no reference tree on this host)")
+def test_movement_restatement_matches_the_reference():
+    """The numpy restatement of cpu_ref::gather / transpose / concat against the compiled reference's cpu-ref run as
+    graph steps, bit for bit: float and i32 tables with i32 and i64 ids; ranks 1 to 6 with f32, i32 and i64 elements;
+    one to eight parts along every axis, empty parts among them. An id outside the table is refused by both."""
+    ora, ref = oracle(), reference()
+    rng = np.random.default_rng(400)
+    for dt in (F32, F16, BF16, I32):
+        table = rng.standard_normal((37, 12)).astype(np.float32)
+        if dt == I32:
+            table = rng.integers(-2 ** 31, 2 ** 31 - 1, (37, 12)).astype(np.int32)
+        elif dt != F32:
+            table = ora.narrow(table, dt)
+        for idt in (np.int32, np.int64):
+            ids = rng.integers(0, 37, (4, 5)).astype(idt)
+            assert_exact(ora.gather(table, ids, dt), ref.gather(table, ids, dt), f"gather table {dt} ids {idt}")
+    for bad in (-1, 37):
+        with pytest.raises(Exception):
+            ref.gather(np.zeros((37, 4), np.float32), np.array([bad], np.int64))
+        with pytest.raises(ValueError):
+            ora.gather(np.zeros((37, 4), np.float32), np.array([bad], np.int64))
+    for rank in range(1, 7):
+        shape = tuple(int(v) for v in rng.integers(1, 5, rank))
+        for dtype in (np.float32, np.int32, np.int64):
+            x = (rng.standard_normal(shape) * 1000).astype(dtype)
+            for _ in range(3):
+                perm = tuple(int(v) for v in rng.permutation(rank))
+                assert_exact(ora.transpose(x, perm), ref.transpose(x, perm), f"transpose {shape} {perm} {dtype}")
+    for rank in (1, 2, 3, 4):
+        for axis in range(rank):
+            for count in (2, 3, 8):
+                base = [int(v) for v in rng.integers(1, 4, rank)]
+                parts = []
+                for k in range(count):
+                    s = list(base)
+                    s[axis] = int(rng.integers(0, 4)) if k != 0 else 2
+                    parts.append((rng.standard_normal(s) * 100).astype(np.float32))
+                assert_exact(ora.concat(parts, axis), ref.concat(parts, axis), f"concat rank {rank} axis {axis}")
+                ip = [p.astype(np.int64) for p in parts]
+                assert_exact(ora.concat(ip, axis), ref.concat(ip, axis), f"concat i64 rank {rank} axis {axis}")

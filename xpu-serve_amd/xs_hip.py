@@ -115,6 +115,9 @@ _SIGS = {
     "xs_hip_quantize_kv_turbo_at": [_P, _INT, _INT, _P, _P, _P, _I64, _I64, _P, _I64, _I64],
     "xs_hip_quantize_kv_pair": [_P, _INT, _P, _P, _P, _P, _P, _P, _I64, _I64, _P, _I64, _I64],
     "xs_hip_copy": [_P, _P, _P, C.c_size_t],
+    "xs_hip_gather": [_P, _INT, _P, _I64, _I64, _INT, _P, _I64, _P],
+    "xs_hip_transpose": [_P, _P, _P, _I64, _INT, _P, _P],
+    "xs_hip_concat": [_P, _INT, _P, _P, _P, _I64],
     "xs_hip_copy_rows": [_P, _P, _I64, _P, _I64, _I64, _I64],
     "xs_hip_kv_rotate": [_P, _P, _P, _I64, _I64, _INT],
     "xs_hip_attention_i8": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _F, _I64, _INT, _I64, _P],
@@ -603,6 +606,39 @@ def kv_rotate(x: DeviceTensor, inverse: bool = False, stream=None) -> DeviceTens
     y = DeviceTensor.empty(F32, x.shape)
     call("xs_hip_kv_rotate", stream, C.c_void_p(x.ptr), C.c_void_p(y.ptr), x.numel // width, width, int(inverse))
     return y
+
+
+def gather(table: DeviceTensor, ids: DeviceTensor, stream=None) -> DeviceTensor:
+    """Rows ids[...] of table [rows, width]: f32 out for a float table (widened), i32 for an i32 table
+    (cpu_ref::gather, ops.cpp:157-173)."""
+    rows, width = table.shape
+    out = DeviceTensor.empty(I32 if table.dtype == I32 else F32, tuple(ids.shape) + (width,))
+    call("xs_hip_gather", stream, table.dtype, C.c_void_p(table.ptr), rows, width, ids.dtype, C.c_void_p(ids.ptr),
+         ids.numel, C.c_void_p(out.ptr))
+    return out
+
+
+def transpose(x: DeviceTensor, perm: Sequence[int], stream=None) -> DeviceTensor:
+    """x with its axes permuted, out.shape[i] = x.shape[perm[i]] (cpu_ref::transpose, ops.cpp:312-340)."""
+    out = DeviceTensor.empty(x.dtype, tuple(x.shape[p] for p in perm))
+    shape = np.array(x.shape, np.int64)
+    pr = np.array(perm, np.int32)
+    call("xs_hip_transpose", stream, C.c_void_p(x.ptr), C.c_void_p(out.ptr), DTYPE_SIZE[x.dtype], len(perm),
+         shape.ctypes.data_as(C.c_void_p), pr.ctypes.data_as(C.c_void_p))
+    return out
+
+
+def concat(parts: Sequence[DeviceTensor], axis: int, stream=None) -> DeviceTensor:
+    """The parts joined along `axis` (cpu_ref::concat, ops.cpp:616-637)."""
+    shape = list(parts[0].shape)
+    shape[axis] = sum(p.shape[axis] for p in parts)
+    out = DeviceTensor.empty(parts[0].dtype, shape)
+    outer = int(np.prod(shape[:axis], dtype=np.int64)) if axis else 1
+    ptrs = (C.c_void_p * len(parts))(*[p.ptr for p in parts])
+    rowb = np.array([p.nbytes // outer if outer else 0 for p in parts], np.int64)
+    call("xs_hip_concat", stream, len(parts), C.cast(ptrs, C.c_void_p), rowb.ctypes.data_as(C.c_void_p),
+         C.c_void_p(out.ptr), outer)
+    return out
 
 
 def convert(x: DeviceTensor, y_dtype: int, stream=None) -> DeviceTensor:
