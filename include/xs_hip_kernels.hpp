@@ -347,6 +347,53 @@ void attention_rows(Stream q, const float* qp, const KV* k, const KV* v, float* 
                   "attention_rows");
 }
 
+// ---- Data movement -------------------------------------------------------------------------------------------------
+
+// out [n, width] = rows ids[r] of table [rows, width] as f32 (sycl_kernels.h:106-107; T float, half or bf16, I int32_t
+// or int64_t). The reference's launcher takes no row count; this device needs it to keep an id outside the table from
+// reading past it (such an id gives a row of zeros).
+template <typename T, typename I>
+void gather(Stream q, const T* table, const I* ids, float* out, int64_t n, int64_t width, int64_t rows) {
+    detail::check(xs_hip_gather(q, detail::dtype_of<T>(), table, rows, width, detail::dtype_of<I>(), ids, n, out),
+                  "gather");
+}
+// Rows of a table of 32-bit integers, copied as they are (sycl_kernels.h:108-110).
+template <typename I>
+void gather_bits(Stream q, const uint32_t* table, const I* ids, uint32_t* out, int64_t n, int64_t width,
+                 int64_t rows) {
+    detail::check(xs_hip_gather(q, XS_I32, table, rows, width, detail::dtype_of<I>(), ids, n, out), "gather_bits");
+}
+
+// For each of `outer` blocks: rows [begin, begin + len) of `dim` rows of `inner` elements of `elem` bytes
+// (sycl_kernels.h:118-120).
+inline void slice(Stream q, const void* x, void* y, size_t elem, int64_t outer, int64_t dim, int64_t begin, int64_t len,
+                  int64_t inner) {
+    const auto row = static_cast<int64_t>(elem) * inner;
+    detail::check(xs_hip_copy_rows(q, static_cast<const char*>(x) + begin * row, dim * row, y, len * row, outer,
+                                   len * row),
+                  "slice");
+}
+
+// y = x with its axes permuted (sycl_kernels.h:121-128): the reference's Permute carries the output shape and x's
+// stride of each output axis; this device takes x's shape and the permutation, from which both follow.
+inline void transpose(Stream q, const void* x, void* y, size_t elem, int rank, const int64_t* in_shape,
+                      const int32_t* perm) {
+    detail::check(xs_hip_transpose(q, x, y, static_cast<int64_t>(elem), rank, in_shape, perm), "transpose");
+}
+
+// Concat as one copy kernel (sycl_kernels.h:95-104): `outer` rows, each the parts' rows laid end to end.
+inline constexpr int kConcatParts = XS_CONCAT_PARTS;
+struct ConcatParts {
+    int count = 0;
+    const void* src[kConcatParts] = {};
+    size_t bytes[kConcatParts] = {};  // per outer row
+};
+inline void concat(Stream q, const ConcatParts& parts, void* out, int64_t outer) {
+    int64_t bytes[kConcatParts] = {};
+    for (int k = 0; k < parts.count && k < kConcatParts; ++k) bytes[k] = static_cast<int64_t>(parts.bytes[k]);
+    detail::check(xs_hip_concat(q, parts.count, parts.src, bytes, out, outer), "concat");
+}
+
 // ---- Device memory -------------------------------------------------------------------------------------------------
 
 // Owns `bytes` of device memory, freed on destruction; the counterpart of the SYCL backend's USM DeviceBuffer

@@ -138,6 +138,18 @@ int64_t xsg_transpose(void* g, int64_t x, int rank, const int32_t* perm) {
     return guard([&] { return enc(static_cast<Graph*>(g)->transpose(dec(x), std::vector<int>(perm, perm + rank))); });
 }
 
+int64_t xsg_gather(void* g, int64_t table, int64_t ids) {
+    return guard([&] { return enc(static_cast<Graph*>(g)->gather(dec(table), dec(ids))); });
+}
+
+int64_t xsg_concat(void* g, int count, const int64_t* parts, int axis) {
+    return guard([&] {
+        std::vector<Value> vs;
+        for (int k = 0; k < count; ++k) vs.push_back(dec(parts[k]));
+        return enc(static_cast<Graph*>(g)->concat(vs, axis));
+    });
+}
+
 int64_t xsg_rope(void* g, int64_t x, int64_t positions, int64_t inv_freq, int64_t rotary, int64_t pair_axes) {
     return guard([&] {
         return enc(static_cast<Graph*>(g)->rope(dec(x), dec(positions), dec(inv_freq), rotary, dec(pair_axes)));

@@ -50,6 +50,8 @@ def lib():
         "xsg_reshape": ([P, I64_, C.c_int, dims], I64_),
         "xsg_slice": ([P, I64_, C.c_int, I64_, I64_], I64_),
         "xsg_transpose": ([P, I64_, C.c_int, C.POINTER(C.c_int32)], I64_),
+        "xsg_gather": ([P, I64_, I64_], I64_),
+        "xsg_concat": ([P, C.c_int, C.POINTER(C.c_int64), C.c_int], I64_),
         "xsg_rope": ([P, I64_, I64_, I64_, I64_, I64_], I64_),
         "xsg_kv_slot": ([P, I64_, I64_, I64_, C.c_char_p], I64_),
         "xsg_kv_cache": ([P, C.c_int, I64_, I64_], I64_),
@@ -174,6 +176,12 @@ class Graph:
 
     def transpose(self, x, perm):
         return _ok(lib().xsg_transpose(self.h, x, len(perm), (C.c_int32 * len(perm))(*perm)))
+
+    def gather(self, table, ids):
+        return _ok(lib().xsg_gather(self.h, table, ids))
+
+    def concat(self, parts, axis):
+        return _ok(lib().xsg_concat(self.h, len(parts), (C.c_int64 * len(parts))(*parts), axis))
 
     def rope(self, x, positions, inv_freq, rotary=0, pair_axes=-1):
         return _ok(lib().xsg_rope(self.h, x, positions, inv_freq, rotary, pair_axes))

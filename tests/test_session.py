@@ -82,6 +82,17 @@ def test_builder_checks():
     slot = g.kv_slot(2, 64, label="a")
     with pytest.raises(S.BackendError, match="appends k and v of"):
         g.kv_cache(slot, q, q)
+    ids = g.input("ids", S.I64, [S.T])
+    with pytest.raises(S.BackendError, match="gather: the table"):
+        g.gather(q, ids)
+    with pytest.raises(S.BackendError, match="gather: ids"):
+        g.gather(x, x)
+    with pytest.raises(S.BackendError, match="joining takes two or more"):
+        g.concat([x], 1)
+    with pytest.raises(S.BackendError, match="symbolic extent along the axis"):
+        g.concat([x, x], 0)
+    with pytest.raises(S.BackendError, match="has extent 5 on axis 1"):
+        g.concat([q, g.input("q5", S.F32, [S.T, 5, 64])], 2)
 
 
 def _refusal(g, match, weights=None, kv=(S.KV_I8, S.KV_I8)):
@@ -96,9 +107,9 @@ def test_refuses_ops_without_kernels():
     g.output("y", g.matmul(x, g.weight(w, "w")))
     _refusal(g, "MatMul.*not supported", w)
     g = S.Graph()
-    x = g.input("x", S.F32, [3, 8])
-    g.output("y", g.transpose(x, [1, 0]))
-    _refusal(g, "Transpose.*not supported")
+    parts = [g.input(f"x{k}", S.F32, [2, 3]) for k in range(9)]
+    g.output("y", g.concat(parts, 1))
+    _refusal(g, "concat of 9 parts")
 
 
 def _kv_graph(extra=None):
@@ -340,6 +351,43 @@ def _kv_programs(hq, hkv, d, window=0, softcap=0.0):
     kr, vr = reader.kv_read(slot2)
     reader.output("o", reader.attention(q2, kr, vr, 1 / math.sqrt(d), window, softcap))
     return prefill, reader
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("table_dtype", [S.F32, S.F16, S.BF16])
+def test_gather_concat_transpose_steps(ora, table_dtype):
+    """An embedding lookup (Gather from a weight table of f32, f16 or bf16 rows) feeding RMSNorm, the rows joined with a
+    second input (Concat on the last axis) and the result's axes swapped (Transpose), over steps of several T; plus an
+    i32 table's rows and a Concat of i64 inputs passed through. Against cpu-ref's semantics on the oracle, bit-exact
+    for the moved values and within the f32 bar for the norm."""
+    rng = np.random.default_rng(700 + table_dtype)
+    vocab, width = 300, 64
+    table = rng.standard_normal((vocab, width)).astype(np.float32)
+    stored = ora.narrow(table, table_dtype) if table_dtype != S.F32 else table
+    norm_w = (1 + 0.1 * rng.standard_normal(width)).astype(np.float32)
+    codes = rng.integers(-2 ** 31, 2 ** 31 - 1, (vocab, 4)).astype(np.int32)
+    w = S.Weights().add("emb", stored, table_dtype).add("norm", norm_w).add("codes", codes, S.I32)
+    g = S.Graph()
+    ids = g.input("ids", S.I64, [S.T])
+    extra = g.input("extra", S.F32, [S.T, 16])
+    tag = g.input("tag", S.I64, [S.T, 2])
+    h = g.rms_norm(g.gather(g.weight(w, "emb"), ids), g.weight(w, "norm"), 1e-6)
+    g.output("h", h)
+    g.output("joined_t", g.transpose(g.concat([h, extra], 1), [1, 0]))
+    g.output("codes", g.gather(g.weight(w, "codes"), ids))
+    g.output("tags", g.concat([tag, tag], 1))
+    s = S.Session(g, w)
+    for t in (5, 1, 3):
+        ii = rng.integers(0, vocab, t).astype(np.int64)
+        ex = rng.standard_normal((t, 16)).astype(np.float32)
+        tg = rng.integers(-5, 5, (t, 2)).astype(np.int64)
+        step(f"session gather/concat/transpose table {table_dtype} T {t}")
+        out = s.run({"ids": (ii, S.I64), "extra": (ex, S.F32), "tag": (tg, S.I64)})
+        rows = ora.gather(stored, ii, table_dtype)
+        assert_f32_close(out["h"], ora.rms_norm(rows, norm_w, 1e-6), what=f"rms_norm of the gathered rows, T {t}")
+        assert_exact(out["joined_t"], ora.transpose(ora.concat([out["h"], ex], 1), (1, 0)), f"concat + transpose T {t}")
+        assert_exact(out["codes"], ora.gather(codes, ii, 4), f"i32 rows T {t}")
+        assert_exact(out["tags"], np.concatenate([tg, tg], 1), f"i64 concat T {t}")
 
 
 class _Cache:

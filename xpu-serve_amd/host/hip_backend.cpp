@@ -201,6 +201,9 @@ enum class Op : uint8_t {
     KvAppend,    // quantizes the step's k, v into the slot
     Attention,   // reads {q, k_all, v_all}
     SliceCopy,   // a Slice that must be contiguous
+    Gather,      // rows of a table by ids; reads {table, ids}
+    Transpose,   // reads {x}
+    Concat,      // reads the parts
 };
 
 struct NodePlan {
@@ -468,6 +471,10 @@ Program::Program(const Graph& g, HipSession& s, size_t index) : g_(g), s_(s), in
             case OpKind::Reshape:
             case OpKind::Slice: dt_[i][0] = dtype(nd.inputs[0]); break;
             case OpKind::TopK: dt_[i][1] = DType::I32; break;
+            // Data movement keeps integers as they are; floats come out f32, as every computed value here.
+            case OpKind::Gather: dt_[i][0] = dtype(nd.inputs[0]) == DType::I32 ? DType::I32 : DType::F32; break;
+            case OpKind::Transpose:
+            case OpKind::Concat: dt_[i][0] = is_float(dtype(nd.inputs[0])) ? DType::F32 : dtype(nd.inputs[0]); break;
             default: break;
         }
     }
@@ -494,6 +501,17 @@ Program::Program(const Graph& g, HipSession& s, size_t index) : g_(g), s_(s), in
             case OpKind::Reshape:
             case OpKind::KvRead: break;
             case OpKind::Slice: p.op = Op::SliceCopy; break;
+            case OpKind::Gather: p.op = Op::Gather; break;
+            case OpKind::Transpose:
+                p.op = Op::Transpose;
+                XS_CHECK(nd.outputs[0].shape.size() <= XS_MAX_RANK, "hip: ", where(i), ": a transpose of rank ",
+                         nd.outputs[0].shape.size(), " (at most ", XS_MAX_RANK, ")");
+                break;
+            case OpKind::Concat:
+                p.op = Op::Concat;
+                XS_CHECK(nd.inputs.size() <= XS_CONCAT_PARTS, "hip: ", where(i), ": a concat of ", nd.inputs.size(),
+                         " parts (at most ", XS_CONCAT_PARTS, " in one launch)");
+                break;
             case OpKind::Add:
             case OpKind::Mul:
             case OpKind::Div: p.op = Op::Binary; break;
@@ -539,7 +557,7 @@ Program::Program(const Graph& g, HipSession& s, size_t index) : g_(g), s_(s), in
             }
             default:
                 fail("hip: ", where(i), " is not supported by the HIP backend (it runs the elementwise, norm, "
-                     "softmax, top-k, reduce, RoPE, int8 KV cache and attention ops)");
+                     "softmax, top-k, reduce, RoPE, gather, transpose, concat, KV cache and attention ops)");
         }
     }
     // KV outputs feed attention only: the slots hold the cache's own format (int8 codes, or f16 / f32 rows).
@@ -833,7 +851,8 @@ bool Program::needs_f32(size_t node, size_t operand) const {
         case Op::Binary:
         case Op::Unary:
         case Op::SliceCopy:
-        case Op::KvAppend: return false;
+        case Op::KvAppend:
+        case Op::Gather: return false;  // the gather widens a 16-bit table's rows itself
         case Op::ActMul: return false;  // x, b and bias share one dtype (checked when fused)
         case Op::RmsNorm:
         case Op::LayerNorm: return operand > 0;
@@ -1417,6 +1436,43 @@ void Program::launch(size_t i, const RunPlan& p, int64_t T, int64_t L, int64_t r
                                           a.causal ? 1 : 0, split, scratch),
                       what);
             }
+            return;
+        }
+        case Op::Gather: {
+            const Value table = np.reads[0], ids = np.reads[1];
+            const Dims& ts = in_shape(table);
+            check(xs_hip_gather(st, abi(dtype(table)), ptr(p, table), ts[0], ts[1], abi(dtype(ids)), ptr(p, ids),
+                                numel(in_shape(ids)), ptr(p, Value{static_cast<int32_t>(i), 0})),
+                  what);
+            return;
+        }
+        case Op::Transpose: {
+            const Value x = np.reads[0];
+            const Dims& xs = in_shape(x);
+            const auto& perm = std::get<graph::TransposeAttrs>(nd.attrs).perm;
+            const std::vector<int32_t> pm(perm.begin(), perm.end());
+            const void* src = is_float(dtype(x)) ? static_cast<const void*>(f32(0)) : ptr(p, x);
+            check(xs_hip_transpose(st, src, ptr(p, Value{static_cast<int32_t>(i), 0}),
+                                   static_cast<int64_t>(dtype_size(dtype(Value{static_cast<int32_t>(i), 0}))),
+                                   static_cast<int>(xs.size()), xs.data(), pm.data()),
+                  what);
+            return;
+        }
+        case Op::Concat: {
+            const int axis = std::get<graph::AxisAttrs>(nd.attrs).axis;
+            int64_t outer = 1;
+            for (int d = 0; d < axis; ++d) outer *= out[static_cast<size_t>(d)];
+            const auto es = static_cast<int64_t>(dtype_size(dtype(Value{static_cast<int32_t>(i), 0})));
+            const void* src[XS_CONCAT_PARTS] = {};
+            int64_t bytes[XS_CONCAT_PARTS] = {};
+            for (size_t k = 0; k < np.reads.size(); ++k) {
+                const Value v = np.reads[k];
+                src[k] = is_float(dtype(v)) ? static_cast<const void*>(f32(k)) : ptr(p, v);
+                bytes[k] = outer > 0 ? numel(in_shape(v)) / outer * es : 0;
+            }
+            check(xs_hip_concat(st, static_cast<int>(np.reads.size()), src, bytes,
+                                ptr(p, Value{static_cast<int32_t>(i), 0}), outer),
+                  what);
             return;
         }
         case Op::SliceCopy: {

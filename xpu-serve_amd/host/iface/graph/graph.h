@@ -134,6 +134,8 @@ public:
     Value reshape(Value x, Dims shape);
     Value slice(Value x, int axis, int64_t begin, int64_t end = kSliceEnd);
     Value transpose(Value x, std::vector<int> perm);
+    Value gather(Value table, Value ids);
+    Value concat(const std::vector<Value>& parts, int axis);
     Value rope(Value x, Value positions, Value inv_freq, int64_t rotary_dim = 0, Value pair_axes = {});
     int add_kv_slot(int64_t num_kv_heads, int64_t head_dim, int64_t sliding_window, std::string label);
     std::pair<Value, Value> kv_cache(int slot, Value k, Value v);
