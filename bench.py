@@ -544,6 +544,63 @@ def op_attention_turbo(inputs, int8_keys=False):
     return Op(name, W.ALGO_BYTES[name], W.ALGO_BYTES[name], mk, go, 2, "attention_turbo_rows")
 
 
+def op_gather_embedding():
+    """2048 token ids (seeded, uniform over the vocabulary) into a [151936, 2560] bf16 embedding table: f32 rows."""
+    vocab, width, n = 151936, 2560, 2048
+    rng = np.random.default_rng(0x5EED0006)
+    table = X.DeviceTensor.empty(X.BF16, (vocab, width))  # read sparsely; one table serves every set
+    X.call("xs_hip_memset", vp(table), 0x3C, C.c_size_t(table.nbytes), None)
+    ids0 = X.DeviceTensor.from_numpy(rng.integers(0, vocab, n).astype(np.int64))
+
+    def mk():
+        s = (dcopy(ids0), X.DeviceTensor.empty(X.F32, (n, width)))
+        need(s[1], n * width * 4, "gather out")
+        return s
+
+    def go(s, stream):
+        ids, out = s
+        X.call("xs_hip_gather", stream, X.BF16, vp(table), vocab, width, X.I64, vp(ids), n, vp(out))
+    return Op("gather_embedding", W.ALGO_BYTES["gather_embedding"], n * width * 4 + n * 8, mk, go, 1, "gather_kernel")
+
+
+def op_transpose_heads():
+    """Config 3's Q [8192, 32, 128] f16 to head-major [32, 8192, 128] (the innermost axis kept: 16-byte runs)."""
+    q0 = X.DeviceTensor.from_numpy(W.config3().arrays["q"], X.F16)
+    shape = np.array(q0.shape, np.int64)
+    perm = np.array([1, 0, 2], np.int32)
+
+    def mk():
+        s = (dcopy(q0), X.DeviceTensor.empty(X.F16, (32, 8192, 128)))
+        need(s[1], q0.nbytes, "transpose out")
+        return s
+
+    def go(s, stream):
+        x, y = s
+        X.call("xs_hip_transpose", stream, vp(x), vp(y), 2, 3, shape.ctypes.data_as(C.c_void_p),
+               perm.ctypes.data_as(C.c_void_p))
+    return Op("transpose_heads", W.ALGO_BYTES["transpose_heads"], W.ALGO_BYTES["transpose_heads"], mk, go, 1,
+              "transpose_kernel")
+
+
+def op_concat_gate_up():
+    """Config 1's gate and up [2048, 9728] bf16 joined along the last axis into [2048, 19456]."""
+    a = W.config1().arrays
+    g0, u0 = X.DeviceTensor.from_numpy(a["gate"], X.BF16), X.DeviceTensor.from_numpy(a["up"], X.BF16)
+    rowb = np.array([9728 * 2, 9728 * 2], np.int64)
+
+    def mk():
+        s = (dcopy(g0), dcopy(u0), X.DeviceTensor.empty(X.BF16, (2048, 19456)))
+        need(s[2], 2048 * 19456 * 2, "concat out")
+        return s
+
+    def go(s, stream):
+        g, u, out = s
+        parts = (C.c_void_p * 2)(g.ptr, u.ptr)
+        X.call("xs_hip_concat", stream, 2, C.cast(parts, C.c_void_p), rowb.ctypes.data_as(C.c_void_p), vp(out), 2048)
+    return Op("concat_gate_up", W.ALGO_BYTES["concat_gate_up"], W.ALGO_BYTES["concat_gate_up"], mk, go, 1,
+              "concat_kernel")
+
+
 def op_copy(n=256 << 20, name="copy"):
     """Bytes per call n (default 256 MiB): the kernel the hardware byte counters are calibrated against, and, at
     other sizes (`--only copy_10MiB` etc.), the ceiling a streaming op of that size can reach."""
@@ -565,7 +622,8 @@ OP_ORDER = ["swiglu_bias", "swiglu_bias_strided", "rmsnorm_residual", "rmsnorm_r
             "argmax", "argmax_one_launch", "rope_qk", "rope_qk_separate", "kv_quantize", "kv_dequantize", "attention_i8_decode",
             "attention_f16_decode", "attention_turbo4_decode", "attention_i8_turbo4_decode", "layer_norm", "l2_clip",
             "reduce_sum_rows", "reduce_sum_cols", "unary_softcap", "kv_turbo4_quantize", "kv_turbo4_dequantize",
-            "topk_shortlist", "topk_moe_router", "topk_draft_candidates"]
+            "topk_shortlist", "topk_moe_router", "topk_draft_candidates", "gather_embedding", "transpose_heads",
+            "concat_gate_up"]
 
 
 def build_ops(only):
@@ -597,7 +655,9 @@ def build_ops(only):
                "kv_turbo4_quantize": lambda: op_kv_turbo(kv), "kv_turbo4_dequantize": lambda: op_kv_turbo(kv, True),
                "topk_shortlist": lambda: op_topk("topk_shortlist"),
                "topk_moe_router": lambda: op_topk("topk_moe_router"),
-               "topk_draft_candidates": lambda: op_topk("topk_draft_candidates")}[name]()
+               "topk_draft_candidates": lambda: op_topk("topk_draft_candidates"),
+               "gather_embedding": op_gather_embedding, "transpose_heads": op_transpose_heads,
+               "concat_gate_up": op_concat_gate_up}[name]()
 
 
 # ---------------------------------------------------------------------------------------------------------------

@@ -94,18 +94,30 @@ struct PermuteArgs {
     int rank;
     int64_t shape[XS_MAX_RANK];   // output shape, the innermost in units
     int64_t stride[XS_MAX_RANK];  // x's unit stride of each output axis
+    FastDiv32 div[XS_MAX_RANK];   // shape[d] as 32-bit divisors (the 32-bit kernel)
 };
 
-template <typename E>
+// W32: fewer than 2^32 units -- the index decomposed with 32-bit multiply-high divisions instead of 64-bit ones.
+template <typename E, bool W32>
 __global__ __launch_bounds__(kMoveBlock) void transpose_kernel(const E* __restrict__ x, E* __restrict__ y, int64_t n,
                                                                PermuteArgs p) {
     const int64_t u = static_cast<int64_t>(blockIdx.x) * kMoveBlock + threadIdx.x;
     if (u >= n) return;
-    int64_t rem = u, off = 0;
-    for (int d = p.rank - 1; d >= 0; --d) {
-        const int64_t q = rem / p.shape[d];
-        off += (rem - q * p.shape[d]) * p.stride[d];
-        rem = q;
+    int64_t off = 0;
+    if constexpr (W32) {
+        uint32_t rem = static_cast<uint32_t>(u);
+        for (int d = p.rank - 1; d >= 0; --d) {
+            const uint32_t q = p.div[d].div(rem);
+            off += static_cast<int64_t>(rem - q * static_cast<uint32_t>(p.shape[d])) * p.stride[d];
+            rem = q;
+        }
+    } else {
+        int64_t rem = u;
+        for (int d = p.rank - 1; d >= 0; --d) {
+            const int64_t q = rem / p.shape[d];
+            off += (rem - q * p.shape[d]) * p.stride[d];
+            rem = q;
+        }
     }
     y[u] = x[off];
 }
@@ -118,13 +130,15 @@ struct ConcatArgs {
     int64_t units[XS_CONCAT_PARTS];  // units of a part's row
     int64_t first[XS_CONCAT_PARTS];  // the part's first unit within an output row
     int64_t row;                     // units of an output row
+    FastDiv32 row_div;               // row as a 32-bit divisor (the 32-bit kernel)
 };
 
-template <typename E>
+template <typename E, bool W32>
 __global__ __launch_bounds__(kMoveBlock) void concat_kernel(ConcatArgs a, E* __restrict__ out, int64_t n) {
     const int64_t u = static_cast<int64_t>(blockIdx.x) * kMoveBlock + threadIdx.x;
     if (u >= n) return;
-    const int64_t o = u / a.row, c = u - o * a.row;
+    const int64_t o = W32 ? static_cast<int64_t>(a.row_div.div(static_cast<uint32_t>(u))) : u / a.row;
+    const int64_t c = u - o * a.row;
     int k = 0;
 #pragma unroll
     for (int j = 1; j < XS_CONCAT_PARTS; ++j)
@@ -228,11 +242,16 @@ int xs_hip_transpose(void* stream, const void* x, void* y, int64_t elem_bytes, i
     }
     const int64_t units = n / per;
     if (units > (int64_t{1} << 40)) return fail(XS_HIP_EUNSUPPORTED, std::string(what) + ": too large");
+    const bool w32 = units < (int64_t{1} << 31);
+    if (w32) {
+        for (int i = 0; i < rank; ++i) p.div[i] = FastDiv32(static_cast<uint32_t>(p.shape[i]));
+    }
     const hipStream_t s = as_stream(stream);
     const unsigned grid = static_cast<unsigned>((units + kMoveBlock - 1) / kMoveBlock);
     by_unit(e, [&](auto tag) {
         using E = decltype(tag);
-        transpose_kernel<E><<<grid, kMoveBlock, 0, s>>>(static_cast<const E*>(x), static_cast<E*>(y), units, p);
+        if (w32) transpose_kernel<E, true><<<grid, kMoveBlock, 0, s>>>(static_cast<const E*>(x), static_cast<E*>(y), units, p);
+        else transpose_kernel<E, false><<<grid, kMoveBlock, 0, s>>>(static_cast<const E*>(x), static_cast<E*>(y), units, p);
     });
     return check_launch(what);
 }
@@ -268,11 +287,14 @@ int xs_hip_concat(void* stream, int count, const void* const* parts, const int64
     a.row = row / e;
     const int64_t units = outer * a.row;
     if (units > (int64_t{1} << 40)) return fail(XS_HIP_EUNSUPPORTED, std::string(what) + ": too large");
+    const bool w32 = units < (int64_t{1} << 31);
+    if (w32) a.row_div = FastDiv32(static_cast<uint32_t>(a.row));
     const hipStream_t s = as_stream(stream);
     const unsigned grid = static_cast<unsigned>((units + kMoveBlock - 1) / kMoveBlock);
     by_unit(e, [&](auto tag) {
         using E = decltype(tag);
-        concat_kernel<E><<<grid, kMoveBlock, 0, s>>>(a, static_cast<E*>(out), units);
+        if (w32) concat_kernel<E, true><<<grid, kMoveBlock, 0, s>>>(a, static_cast<E*>(out), units);
+        else concat_kernel<E, false><<<grid, kMoveBlock, 0, s>>>(a, static_cast<E*>(out), units);
     });
     return check_launch(what);
 }

@@ -101,6 +101,11 @@ ALGO_BYTES: Dict[str, int] = {
     "attention_i8_decode": 2 * (65536 * 8 * 128 + 65536 * 8 * 4) + 2 * 32 * 128 * 4,
     # the same step over turbo4 keys and values (64 code bytes and a 2-byte norm per 128 values), and over int8 keys
     # with turbo4 values
+    # data movement: 2048 token ids into a [151936, 2560] bf16 embedding table (rows read, f32 rows written, the ids);
+    # config 3's Q [8192, 32, 128] f16 to head-major [32, 8192, 128]; config 1's gate and up joined into [2048, 19456]
+    "gather_embedding": 2048 * 2560 * (2 + 4) + 2048 * 8,
+    "transpose_heads": 2 * 8192 * 32 * 128 * 2,
+    "concat_gate_up": 2 * 2 * 2048 * 9728 * 2,
     "attention_f16_decode": 2 * 65536 * 8 * 128 * 2 + 2 * 32 * 128 * 4,
     "attention_turbo4_decode": 2 * (65536 * 8 * 64 + 65536 * 8 * 2) + 2 * 32 * 128 * 4,
     "attention_i8_turbo4_decode": 65536 * 8 * (128 + 4) + 65536 * 8 * (64 + 2) + 2 * 32 * 128 * 4,
