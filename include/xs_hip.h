@@ -398,6 +398,19 @@ int xs_hip_attention_i8_noalloc(void* stream, const float* q, const void* k_code
                                 int64_t kv_heads, int64_t head_dim, int64_t kv_len, float scale, float softcap,
                                 int64_t window, int causal, int64_t split);
 
+/* ---- Split-attention combine and merge (the reference's partial-row layout) ------------------------------------ */
+
+/* part [rows, split, head_dim + 2]: per row and split, head_dim unnormalized weighted sums, the split's max and its sum
+ * of exponentials relative to it (max -inf: a split that saw no key). out [rows, head_dim] = the splits merged and
+ * normalized. Replaces sycl_be::attention_combine (sycl_kernels.h:240; sycl_kernels.cpp:1975-1995). */
+int xs_hip_attention_combine(void* stream, const float* part, float* out, int64_t rows, int64_t split,
+                             int64_t head_dim);
+/* acc [rows, head_dim + 2], a partial row in the same layout, takes in each row's `split` partial rows of `part`;
+ * first != 0 starts acc as their merge alone. xs_hip_attention_combine(acc, split 1) then gives the output. Replaces
+ * sycl_be::attention_merge (sycl_kernels.h:241-244; sycl_kernels.cpp:1997-2030). */
+int xs_hip_attention_merge(void* stream, const float* part, float* acc, int64_t rows, int64_t split, int64_t head_dim,
+                           int first);
+
 /* ---- Data movement: gather, transpose, concat ------------------------------------------------------------------ */
 
 /* out [n, width] = rows ids[r] of table [rows, width] -- an embedding lookup. table f32, f16 or bf16 gives f32 rows

@@ -347,6 +347,17 @@ void attention_rows(Stream q, const float* qp, const KV* k, const KV* v, float* 
                   "attention_rows");
 }
 
+// part [rows, split, D + 2] (D sums, max, denominator per split) merged into out [rows, D] (sycl_kernels.h:240).
+inline void attention_combine(Stream q, const float* part, float* out, int64_t rows, int64_t split, int64_t head_dim) {
+    detail::check(xs_hip_attention_combine(q, part, out, rows, split, head_dim), "attention_combine");
+}
+// acc [rows, D + 2] takes in each row's `split` partial rows; `first`: acc starts as their merge (sycl_kernels.h:
+// 241-244).
+inline void attention_merge(Stream q, const float* part, float* acc, int64_t rows, int64_t split, int64_t head_dim,
+                            bool first) {
+    detail::check(xs_hip_attention_merge(q, part, acc, rows, split, head_dim, first ? 1 : 0), "attention_merge");
+}
+
 // ---- Data movement -------------------------------------------------------------------------------------------------
 
 // out [n, width] = rows ids[r] of table [rows, width] as f32 (sycl_kernels.h:106-107; T float, half or bf16, I int32_t

@@ -218,3 +218,60 @@ def test_attention_quantized_decode_config4_cache(ora):
     step("attention turbo4 decode [1, 32, 128] over 65536 keys")
     y = run(q, 4, 4, streams, hkv, n, 1.0 / math.sqrt(d))
     assert_attention_close(y, ora.attention(q, k_rt, v_rt, 1.0 / math.sqrt(d)), "turbo4 decode full size")
+
+
+# ---- the split combine and merge over the reference's partial-row layout -------------------------------------------
+
+def _partials(scores, v, bounds):
+    """Partial rows [rows, split, D + 2] of an attention with scores [rows, N] over values [N, D], the keys split at
+    `bounds`: per split the weighted sums relative to its own max, the max and the sum of exponentials (f64, rounded
+    to f32); an empty split has max -inf. The layout of sycl_kernels.h:232-244."""
+    rows, n = scores.shape
+    d = v.shape[1]
+    out = np.zeros((rows, len(bounds) - 1, d + 2), np.float64)
+    for s, (a, b) in enumerate(zip(bounds[:-1], bounds[1:])):
+        if a == b:
+            out[:, s, d] = -np.inf
+            continue
+        sc = scores[:, a:b].astype(np.float64)
+        m = sc.max(axis=1)
+        e = np.exp(sc - m[:, None])
+        out[:, s, :d] = e @ v[a:b].astype(np.float64)
+        out[:, s, d] = m
+        out[:, s, d + 1] = e.sum(axis=1)
+    return out.astype(np.float32)
+
+
+def _softmax_out(scores, v):
+    """The closed form the merged partials must give: softmax(scores) @ v, in f64."""
+    sc = scores.astype(np.float64)
+    e = np.exp(sc - sc.max(axis=1, keepdims=True))
+    return (e / e.sum(axis=1, keepdims=True)) @ v.astype(np.float64)
+
+
+@pytest.mark.parametrize("rows,n,d,bounds", [(5, 300, 128, (0, 100, 100, 250, 300)), (64, 40, 64, (0, 40)),
+                                             (3, 1000, 256, (0, 1, 500, 999, 1000)), (7, 64, 80, (0, 0, 64))])
+def test_attention_combine_and_merge(rows, n, d, bounds):
+    """attention_combine of partial rows equals the softmax-weighted sum over all keys (the reference's device bar);
+    attention_merge of the same splits in two calls (first, then the rest), combined with split 1, equals it too."""
+    rng = np.random.default_rng(900 + n)
+    scores = (3 * rng.standard_normal((rows, n))).astype(np.float32)
+    v = rng.standard_normal((n, d)).astype(np.float32)
+    part = _partials(scores, v, bounds)
+    want = _softmax_out(scores, v)
+    split = len(bounds) - 1
+    step(f"attention_combine rows {rows} split {split} D {d}")
+    out = X.DeviceTensor.empty(X.F32, (rows, d))
+    pd = dev(part)
+    X.call("xs_hip_attention_combine", None, C.c_void_p(pd.ptr), C.c_void_p(out.ptr), rows, split, d)
+    assert_attention_close(out.numpy(), want, "combine", atol=1e-5, rtol=1e-4)
+    step(f"attention_merge rows {rows} split {split} D {d}")
+    h = max(split // 2, 1)
+    first, rest = np.ascontiguousarray(part[:, :h]), np.ascontiguousarray(part[:, h:])
+    acc = dev(np.full((rows, d + 2), np.nan, np.float32))  # `first` ignores what acc held
+    fd, rd = dev(first), dev(rest) if rest.shape[1] else None  # kept alive until the launches have run
+    X.call("xs_hip_attention_merge", None, C.c_void_p(fd.ptr), C.c_void_p(acc.ptr), rows, h, d, 1)
+    if rd is not None:
+        X.call("xs_hip_attention_merge", None, C.c_void_p(rd.ptr), C.c_void_p(acc.ptr), rows, rest.shape[1], d, 0)
+    X.call("xs_hip_attention_combine", None, C.c_void_p(acc.ptr), C.c_void_p(out.ptr), rows, 1, d)
+    assert_attention_close(out.numpy(), want, "merge then combine", atol=1e-5, rtol=1e-4)

@@ -115,6 +115,8 @@ _SIGS = {
     "xs_hip_quantize_kv_turbo_at": [_P, _INT, _INT, _P, _P, _P, _I64, _I64, _P, _I64, _I64],
     "xs_hip_quantize_kv_pair": [_P, _INT, _P, _P, _P, _P, _P, _P, _I64, _I64, _P, _I64, _I64],
     "xs_hip_copy": [_P, _P, _P, C.c_size_t],
+    "xs_hip_attention_combine": [_P, _P, _P, _I64, _I64, _I64],
+    "xs_hip_attention_merge": [_P, _P, _P, _I64, _I64, _I64, _INT],
     "xs_hip_gather": [_P, _INT, _P, _I64, _I64, _INT, _P, _I64, _P],
     "xs_hip_transpose": [_P, _P, _P, _I64, _INT, _P, _P],
     "xs_hip_concat": [_P, _INT, _P, _P, _P, _I64],
