@@ -499,7 +499,7 @@ def op_attention_f16(inputs):
     kv_len = rows // kv_heads
     rng = np.random.default_rng(0x5EED0005)
     q0 = X.DeviceTensor.from_numpy(rng.standard_normal((1, q_heads, dim)).astype(np.float32))
-    split = int(X.lib().xs_hip_attention_rows_split(1, kv_heads, kv_len))
+    split = int(X.lib().xs_hip_attention_rows_split_kv(X.KV_FLOAT, X.F16, 1, q_heads, kv_heads, kv_len, dim))
     nscratch = int(X.lib().xs_hip_attention_i8_scratch(1, q_heads, dim, split))
 
     def mk():
@@ -525,9 +525,9 @@ def op_attention_turbo(inputs, int8_keys=False):
     vc0, vs0 = X.turbo_quantize(v0, 4)
     rng = np.random.default_rng(0x5EED0005)
     q0 = X.DeviceTensor.from_numpy(rng.standard_normal((1, q_heads, dim)).astype(np.float32))
-    split = int(X.lib().xs_hip_attention_rows_split(1, kv_heads, kv_len))
-    nscratch = int(X.lib().xs_hip_attention_i8_scratch(1, q_heads, dim, split))
     kf = X.KV_I8 if int8_keys else X.KV_TURBO4
+    split = int(X.lib().xs_hip_attention_rows_split_kv(kf, X.F32, 1, q_heads, kv_heads, kv_len, dim))
+    nscratch = int(X.lib().xs_hip_attention_i8_scratch(1, q_heads, dim, split))
     name = "attention_i8_turbo4_decode" if int8_keys else "attention_turbo4_decode"
 
     def mk():

@@ -348,6 +348,13 @@ int64_t xs_hip_attention_i8_split(int64_t tokens, int64_t kv_heads, int64_t kv_l
 /* The split xs_hip_attention and xs_hip_attention_quantized (for pairs other than int8/int8) run best at for this shape:
  * about two workgroups a CU, each at least 128 keys. Scratch: xs_hip_attention_i8_scratch. */
 int64_t xs_hip_attention_rows_split(int64_t tokens, int64_t kv_heads, int64_t kv_len);
+/* No counterpart in the reference (its dispatch picks no split by format): the split at which the rows kernel for this
+ * key format runs best -- three workgroups a CU for f16 keys (k_format XS_KV_FLOAT, kv_dtype XS_F16) and int8 keys at
+ * head_dim <= 128 with at most 4 query heads a KV head, whose kernels are built for three; two, as
+ * xs_hip_attention_rows_split, otherwise. For callers of
+ * xs_hip_attention and xs_hip_attention_quantized that know the cache's format. */
+int64_t xs_hip_attention_rows_split_kv(xs_kv_format k_format, xs_dtype kv_dtype, int64_t tokens, int64_t q_heads,
+                                       int64_t kv_heads, int64_t kv_len, int64_t head_dim);
 size_t xs_hip_attention_i8_scratch(int64_t tokens, int64_t q_heads, int64_t head_dim, int64_t split);
 /* Decode attention over a float KV cache: keys and values [kv_len, kv_heads, head_dim] of kv_dtype (XS_F16 or XS_F32;
  * the Float KV format: f16 rows at f16 precision, f32 at f32), q and out as xs_hip_attention_i8, the same key

@@ -220,6 +220,38 @@ def test_attention_quantized_decode_config4_cache(ora):
     assert_attention_close(y, ora.attention(q, k_rt, v_rt, 1.0 / math.sqrt(d)), "turbo4 decode full size")
 
 
+def test_attention_quantized_decode_config4_int8_keys_at_suggested_split(ora):
+    """int8 keys with turbo4 values at config 4's shape, at the split xs_hip_attention_rows_split_kv suggests (three
+    workgroups a CU: the three-wave build of the rows kernel)."""
+    rng = np.random.default_rng(108)
+    n, hkv, d, hq = 65536, 8, 128, 32
+    k = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    v = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    q = 2.0 * rng.standard_normal((1, hq, d)).astype(np.float32)
+    streams, k_rt, v_rt = cache(ora, k, v, 8, 4)
+    split = int(X.lib().xs_hip_attention_rows_split_kv(X.KV_I8, X.F32, 1, hq, hkv, n, d))
+    step(f"attention i8:turbo4 decode [1, 32, 128] over 65536 keys, split {split}")
+    y = run(q, 8, 4, streams, hkv, n, 1.0 / math.sqrt(d), split=split)
+    assert_attention_close(y, ora.attention(q, k_rt, v_rt, 1.0 / math.sqrt(d)), "i8:turbo4 decode full size")
+
+
+def test_rows_split_by_key_format():
+    """Three workgroups a CU for f16 and int8 keys at head_dim <= 128 and <= 4 query heads a KV head, two otherwise."""
+    lib = X.lib()
+    n = 65536
+    two = int(lib.xs_hip_attention_rows_split(1, 8, n))  # two workgroups a CU over 8 KV heads
+    three = -(-3 * (two * 8 // 2) // 8)
+    assert two >= 1
+    assert int(lib.xs_hip_attention_rows_split_kv(X.KV_FLOAT, X.F16, 1, 32, 8, n, 128)) == min(three, 256)
+    assert int(lib.xs_hip_attention_rows_split_kv(X.KV_I8, X.F32, 1, 32, 8, n, 128)) == min(three, 256)
+    for args in ((X.KV_TURBO4, X.F32, 1, 32, 8, n, 128), (X.KV_FLOAT, X.F32, 1, 32, 8, n, 128),
+                 (X.KV_FLOAT, X.F16, 1, 64, 8, n, 128), (X.KV_FLOAT, X.F16, 1, 32, 8, n, 256)):
+        assert int(lib.xs_hip_attention_rows_split_kv(*args)) == two, args
+    # short caches: at least half a tile of keys a split
+    assert int(lib.xs_hip_attention_rows_split_kv(X.KV_FLOAT, X.F16, 1, 32, 8, 300, 128)) == 3
+    assert int(lib.xs_hip_attention_rows_split_kv(X.KV_FLOAT, X.F16, 1, 32, 8, 0, 128)) == 1
+
+
 # ---- the split combine and merge over the reference's partial-row layout -------------------------------------------
 
 def _partials(scores, v, bounds):

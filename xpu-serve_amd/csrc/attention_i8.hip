@@ -630,6 +630,14 @@ constexpr int kRowsTile = 256;
 
 // The storage formats, as template arguments: TurboQuant bits 2, 3, 4; 8: int8 codes; 16: f16; 32: f32.
 constexpr bool is_turbo(int f) { return f <= 4; }
+
+// Workgroups a CU the rows kernel is compiled for (its four waves a workgroup put as many waves on each SIMD): three
+// where the scores run on the matrix cores at head_dim <= 128 with up to 4 query heads a KV head (f16 and int8 keys),
+// which then load half as many value rows and key blocks at once to fit 168 registers; two otherwise, as the
+// registers fall (TurboQuant and f32 keys need the registers of their lane-wise decode; more heads, their sums). Measured on MI355X at 65,536 keys x 8 KV heads, 32 query heads, head_dim 128, each at its best
+// split: f16 rows 58.8 us at three (split 96) against 63.9 at two (split 64); int8 keys with turbo4 values 52.7 against
+// 57.6; turbo4 keys at three spill registers and took 64.4 against 50.6.
+constexpr int rows_waves(int kf, int d, int g) { return (kf == 16 || kf == 8) && d <= 128 && g <= 4 ? 3 : 2; }
 // Bytes of 8 LV values of a row in format f (one group: 128 values for TurboQuant).
 constexpr int group_bytes_of(int f, int lv) { return is_turbo(f) ? turbo::group_bytes(f) : 8 * lv * f / 8; }
 
@@ -863,7 +871,7 @@ __device__ __forceinline__ half8_t as_half8(const uint32_t* w) {
 
 // KF, VF: the keys' and the values' formats (both 16 or both 32; or VF TurboQuant with KF the same or 8).
 template <int KF, int VF, int G, int D, bool CAP>
-__global__ __launch_bounds__(256) void attention_rows_kernel(AttnArgs a, const uint8_t* kc, const void* ks,
+__global__ __launch_bounds__(256, rows_waves(KF, D, G) == 3 ? 3 : 1) void attention_rows_kernel(AttnArgs a, const uint8_t* kc, const void* ks,
                                                              const uint8_t* vc, const uint16_t* vn) {
     using namespace turbo;
     static_assert((KF == VF && !is_turbo(KF) && KF != 8) || (is_turbo(VF) && (KF == VF || KF == 8)), "format pair");
@@ -874,8 +882,9 @@ __global__ __launch_bounds__(256) void attention_rows_kernel(AttnArgs a, const u
     constexpr int kD8 = D / kLaneValues;    // 8-dim slices a row
     constexpr int kS = 256 / kD8;           // key subsets of the weighted sum
     constexpr int kRowsPerThread = kRowsTile / kS;  // value rows a thread adds up a tile (8 to 64)
-    // Of them, loaded together: about 32 words of registers.
-    constexpr int kVB = 32 / ValueSlice<VF>::kWords < 16 ? 32 / ValueSlice<VF>::kWords : 16;
+    // Of them, loaded together: about 32 words of registers (16 at three waves a SIMD).
+    constexpr int kVW = rows_waves(KF, D, G) == 3 ? 16 : 32;
+    constexpr int kVB = kVW / ValueSlice<VF>::kWords < 16 ? kVW / ValueSlice<VF>::kWords : 16;
     constexpr int kVPref = kVB < kRowsPerThread ? kVB : kRowsPerThread;
     constexpr int kSets = 256 / 8;          // 8-lane sets that score keys
     constexpr int kKeysPerSet = kRowsTile / kSets;
@@ -889,7 +898,7 @@ __global__ __launch_bounds__(256) void attention_rows_kernel(AttnArgs a, const u
     constexpr bool kQReg = !kMfma && G * kNG * kLV <= 64;  // the query values a key lane needs, in registers
     constexpr int kSteps = D / 32;  // 32-dim steps of a key row
     constexpr int kAW = KF == 16 ? 4 : KF == 8 ? 2 : KF == 3 ? 2 : 1;  // words of a lane's A operand a step, as stored
-    constexpr int kABlk = kSteps * kAW * 4 <= 64 ? 4 : 2;              // 16-key blocks whose keys are loaded together
+    constexpr int kABlk = kSteps * kAW * 4 <= 64 && rows_waves(KF, D, G) == 2 ? 4 : 2;  // 16-key blocks loaded together
     constexpr int kKGB = group_bytes_of(KF, kLV);
     constexpr int kVGB = group_bytes_of(VF, kLV);
     constexpr int kTab = is_turbo(VF) ? TurboTable<(is_turbo(VF) ? VF : 4)>::kEntries *
@@ -1331,6 +1340,21 @@ int launch_g(hipStream_t s, const AttnArgs& a) {
     return check_launch("xs_hip_attention_i8");
 }
 
+// The split of the rows kernel's keys that puts per_cu workgroups on each CU, each at least half a tile of keys.
+// Measured on MI355X, one query token, 32 query and 8 KV heads, head_dim 128, f16 rows at two workgroups a CU: 65536
+// keys 54 us at split 64 (68 at 256, 64 at 32), 16384 keys 23 us at 64, 4096 keys 14 us at 32, 1024 keys 14 us at 8
+// or 16. A split that is not a whole number of rounds of the CUs leaves a partial round (f16 rows at three a CU: split
+// 96, 58.8 us; 80, 63.9; 112, 78.6).
+int64_t rows_split(int per_cu, int64_t tokens, int64_t kv_heads, int64_t kv_len) {
+    if (tokens <= 0 || kv_heads <= 0 || kv_len <= 0) return 1;
+    const int64_t units = tokens * kv_heads;
+    int64_t split = (per_cu * static_cast<int64_t>(device_cus()) + units - 1) / units;
+    const int64_t by_len = (kv_len + kRowsTile / 2 - 1) / (kRowsTile / 2);
+    if (split > by_len) split = by_len;
+    if (split > kMaxSplit) split = kMaxSplit;
+    return split < 1 ? 1 : split;
+}
+
 }  // namespace
 }  // namespace xs_hip
 
@@ -1356,16 +1380,23 @@ int64_t xs_hip_attention_i8_split(int64_t tokens, int64_t kv_heads, int64_t kv_l
 }
 
 int64_t xs_hip_attention_rows_split(int64_t tokens, int64_t kv_heads, int64_t kv_len) {
-    if (tokens <= 0 || kv_heads <= 0 || kv_len <= 0) return 1;
-    // About two workgroups a CU, each at least half a tile of keys. Measured on MI355X, one query token, 32 query and 8
-    // KV heads, head_dim 128, f16 rows: 65536 keys 54 us at split 64 (68 at 256, 64 at 32), 16384 keys 23 us at 64,
-    // 4096 keys 14 us at 32, 1024 keys 14 us at 8 or 16.
-    const int64_t units = tokens * kv_heads;
-    int64_t split = (2 * static_cast<int64_t>(device_cus()) + units - 1) / units;
-    const int64_t by_len = (kv_len + kRowsTile / 2 - 1) / (kRowsTile / 2);
-    if (split > by_len) split = by_len;
-    if (split > kMaxSplit) split = kMaxSplit;
-    return split < 1 ? 1 : split;
+    return rows_split(2, tokens, kv_heads, kv_len);
+}
+
+int64_t xs_hip_attention_rows_split_kv(xs_kv_format k_format, xs_dtype kv_dtype, int64_t tokens, int64_t q_heads,
+                                       int64_t kv_heads, int64_t kv_len, int64_t head_dim) {
+    int kf = 0;
+    switch (k_format) {
+        case XS_KV_FLOAT: kf = kv_dtype == XS_F16 ? 16 : 32; break;
+        case XS_KV_I8: kf = 8; break;
+        case XS_KV_TURBO4: kf = 4; break;
+        case XS_KV_TURBO3: kf = 3; break;
+        case XS_KV_TURBO2: kf = 2; break;
+        default: kf = 32; break;
+    }
+    const int64_t g = kv_heads > 0 && q_heads > 0 ? q_heads / kv_heads : 8;
+    return rows_split(rows_waves(kf, static_cast<int>(head_dim < 512 ? head_dim : 512), static_cast<int>(g < 8 ? g : 8)),
+                      tokens, kv_heads, kv_len);
 }
 
 size_t xs_hip_attention_i8_scratch(int64_t tokens, int64_t q_heads, int64_t head_dim, int64_t split) {

@@ -1033,8 +1033,10 @@ Program::RunPlan& Program::plan_for(int64_t T, std::span<const std::string> only
             const Dims& k = g_.type(nd.inputs[1]).shape;
             // The split grows with the keys: sized for max_context, enough for every L of the session, whichever
             // reader (int8 or float rows) runs.
-            const int64_t split = std::max(xs_hip_attention_i8_split(q[0], k[1], max_len),
-                                           xs_hip_attention_rows_split(q[0], k[1], max_len));
+            const int64_t split = std::max({xs_hip_attention_i8_split(q[0], k[1], max_len),
+                                            xs_hip_attention_rows_split(q[0], k[1], max_len),
+                                            xs_hip_attention_rows_split_kv(XS_KV_FLOAT, XS_F16, q[0], q[1], k[1],
+                                                                           max_len, q[2])});
             bytes = xs_hip_attention_i8_scratch(q[0], q[1], q[2], split);
         }
         if (bytes == 0) continue;
@@ -1392,7 +1394,8 @@ void Program::launch(size_t i, const RunPlan& p, int64_t T, int64_t L, int64_t r
             const Dims& qs = in_shape(q);
             const int64_t keys = replay_cap > 0 ? replay_cap : L;
             const int64_t split = kv.both_i8() ? xs_hip_attention_i8_split(qs[0], kv.heads, keys)
-                                               : xs_hip_attention_rows_split(qs[0], kv.heads, keys);
+                                               : xs_hip_attention_rows_split_kv(kv_abi(kv.kf), abi(kv.rows), qs[0],
+                                                                                qs[1], kv.heads, keys, kv.dim);
             auto* out_p = reinterpret_cast<float*>(ptr(p, Value{static_cast<int32_t>(i), 0}));
             char* scratch = split > 1 ? s_.arena().get() + p.block_offset[static_cast<size_t>(p.scratch[i])] : nullptr;
             if (kv.rows != DType::I8) {  // the Float format's rows

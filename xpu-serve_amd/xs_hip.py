@@ -136,10 +136,12 @@ _SIGS = {
                                       _F, _I64, _INT, _I64, _P],
     "xs_hip_attention_i8_split": [_I64, _I64, _I64],
     "xs_hip_attention_rows_split": [_I64, _I64, _I64],
+    "xs_hip_attention_rows_split_kv": [_INT, _INT, _I64, _I64, _I64, _I64, _I64],
     "xs_hip_attention_i8_scratch": [_I64, _I64, _I64, _I64],
 }
 _RESTYPES = {"xs_hip_topk_scratch": C.c_size_t, "xs_hip_softmax_scratch": C.c_size_t,
-             "xs_hip_attention_i8_split": C.c_int64, "xs_hip_attention_rows_split": C.c_int64, "xs_hip_attention_i8_scratch": C.c_size_t,
+             "xs_hip_attention_i8_split": C.c_int64, "xs_hip_attention_rows_split": C.c_int64,
+             "xs_hip_attention_rows_split_kv": C.c_int64, "xs_hip_attention_i8_scratch": C.c_size_t,
              "xs_hip_last_error": C.c_char_p, "xs_hip_set_spin_limit": None,
              "xs_hip_argmax_scratch": C.c_size_t}
 
@@ -393,7 +395,7 @@ def attention(q: DeviceTensor, k: DeviceTensor, v: DeviceTensor, kv_heads: int, 
     tokens, q_heads, d = q.shape
     kv_len = k.numel // (kv_heads * d)
     if split <= 0:
-        split = int(lib().xs_hip_attention_rows_split(tokens, kv_heads, kv_len))
+        split = int(lib().xs_hip_attention_rows_split_kv(KV_FLOAT, k.dtype, tokens, q_heads, kv_heads, kv_len, d))
     out = DeviceTensor.empty(F32, q.shape)
     nbytes = int(lib().xs_hip_attention_i8_scratch(tokens, q_heads, d, split))
     scratch = DeviceBuffer(nbytes) if nbytes else None
@@ -414,8 +416,10 @@ def attention_quantized(q: DeviceTensor, k_format: int, k_codes: DeviceTensor, k
     tokens, q_heads, d = q.shape
     if split <= 0:
         both_i8 = k_format == KV_I8 and v_format == KV_I8
-        split = int((lib().xs_hip_attention_i8_split if both_i8 else lib().xs_hip_attention_rows_split)(
-            tokens, kv_heads, kv_len))
+        if both_i8:
+            split = int(lib().xs_hip_attention_i8_split(tokens, kv_heads, kv_len))
+        else:
+            split = int(lib().xs_hip_attention_rows_split_kv(k_format, F32, tokens, q_heads, kv_heads, kv_len, d))
     out = DeviceTensor.empty(F32, q.shape)
     nbytes = int(lib().xs_hip_attention_i8_scratch(tokens, q_heads, d, split))
     scratch = DeviceBuffer(nbytes) if nbytes else None
