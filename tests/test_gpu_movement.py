@@ -85,6 +85,30 @@ def test_transpose_refuses_a_non_permutation():
                    shape.ctypes.data_as(C.c_void_p), p.ctypes.data_as(C.c_void_p))
 
 
+def test_transpose_past_2_31_units():
+    """A transpose of 2^31 + 6 one-byte units (the innermost axis moved): more units than one launch's grid holds, so
+    two launches at offsets, with 64-bit index arithmetic. Checked against numpy's own transpose."""
+    n = (1 << 30) + 3
+    x = (np.arange(2 * n, dtype=np.uint64) % 251).astype(np.uint8).reshape(n, 2)
+    x[-1] = (7, 9)
+    step(f"transpose u8 ({n}, 2) -> (2, {n})")
+    got = X.transpose(dev(x, X.U8), (1, 0)).numpy()
+    assert got.shape == (2, n)
+    assert np.array_equal(got[0], x[:, 0]) and np.array_equal(got[1], x[:, 1])
+
+
+def test_concat_past_2_31_units():
+    """Two [2^30 + 3, 1] u8 parts joined along the last axis: 2^31 + 6 one-byte units, two launches at offsets."""
+    n = (1 << 30) + 3
+    a = (np.arange(n, dtype=np.uint64) % 251).astype(np.uint8).reshape(n, 1)
+    b = (np.arange(n, dtype=np.uint64) % 241).astype(np.uint8).reshape(n, 1)
+    b[-1] = 200
+    step(f"concat u8 2 x ({n}, 1) along the last axis")
+    got = X.concat([dev(a, X.U8), dev(b, X.U8)], 1).numpy()
+    assert got.shape == (n, 2)
+    assert np.array_equal(got[:, 0], a[:, 0]) and np.array_equal(got[:, 1], b[:, 0])
+
+
 @pytest.mark.parametrize("dtype", [np.float32, np.float16, np.int64])
 def test_concat(ora, dtype):
     rng = np.random.default_rng(530 + np.dtype(dtype).itemsize)
