@@ -623,7 +623,26 @@ OP_ORDER = ["swiglu_bias", "swiglu_bias_strided", "rmsnorm_residual", "rmsnorm_r
             "attention_f16_decode", "attention_turbo4_decode", "attention_i8_turbo4_decode", "layer_norm", "l2_clip",
             "reduce_sum_rows", "reduce_sum_cols", "unary_softcap", "kv_turbo4_quantize", "kv_turbo4_dequantize",
             "topk_shortlist", "topk_moe_router", "topk_draft_candidates", "gather_embedding", "transpose_heads",
-            "concat_gate_up"]
+            "concat_gate_up", "slice_gate"]
+
+
+def op_slice_gate():
+    """The gate half (columns 0..9727) of config 1's fused [2048, 19456] bf16 buffer copied out to [2048, 9728]
+    (xs_hip_copy_rows, the Slice of the session)."""
+    a = W.config1().arrays
+    g0, u0 = X.DeviceTensor.from_numpy(a["gate"], X.BF16), X.DeviceTensor.from_numpy(a["up"], X.BF16)
+    fused0 = X.concat([g0, u0], 1)
+
+    def mk():
+        s = (dcopy(fused0), X.DeviceTensor.empty(X.BF16, (2048, 9728)))
+        need(s[1], 2048 * 9728 * 2, "slice out")
+        return s
+
+    def go(s, stream):
+        x, y = s
+        X.call("xs_hip_copy_rows", stream, vp(x), 19456 * 2, vp(y), 9728 * 2, 2048, 9728 * 2)
+    return Op("slice_gate", W.ALGO_BYTES["slice_gate"], W.ALGO_BYTES["slice_gate"] // 2 * 3, mk, go, 1,
+              "copy_rows_kernel")
 
 
 def build_ops(only):
@@ -657,7 +676,7 @@ def build_ops(only):
                "topk_moe_router": lambda: op_topk("topk_moe_router"),
                "topk_draft_candidates": lambda: op_topk("topk_draft_candidates"),
                "gather_embedding": op_gather_embedding, "transpose_heads": op_transpose_heads,
-               "concat_gate_up": op_concat_gate_up}[name]()
+               "concat_gate_up": op_concat_gate_up, "slice_gate": op_slice_gate}[name]()
 
 
 # ---------------------------------------------------------------------------------------------------------------

@@ -70,13 +70,16 @@ __global__ __launch_bounds__(kCopyBlock) void copy_kernel(const u32x4* __restric
 
 // y[r, :] = x[r, :] for rows of `cols` elements of type E, rows `xs` / `ys` bytes apart: grid (column tiles, row
 // groups), each workgroup walking its rows gridDim.y apart.
+// Non-temporal loads and stores: the gate half of config 1's fused [2048, 19456] bf16 buffer in 14.4 us against
+// 17.1 us with plain ones, on MI355X (a 40 MiB copy: 14.0 us).
 template <typename E>
 __global__ __launch_bounds__(kBlock) void copy_rows_kernel(const char* __restrict__ x, int64_t xs, char* __restrict__ y,
                                                            int64_t ys, int64_t rows, int64_t cols) {
     const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
     if (c >= cols) return;
     for (int64_t r = blockIdx.y; r < rows; r += gridDim.y)
-        reinterpret_cast<E*>(y + r * ys)[c] = reinterpret_cast<const E*>(x + r * xs)[c];
+        __builtin_nontemporal_store(__builtin_nontemporal_load(reinterpret_cast<const E*>(x + r * xs) + c),
+                                    reinterpret_cast<E*>(y + r * ys) + c);
 }
 
 }  // namespace

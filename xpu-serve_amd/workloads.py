@@ -106,6 +106,8 @@ ALGO_BYTES: Dict[str, int] = {
     "gather_embedding": 2048 * 2560 * (2 + 4) + 2048 * 8,
     "transpose_heads": 2 * 8192 * 32 * 128 * 2,
     "concat_gate_up": 2 * 2 * 2048 * 9728 * 2,
+    # Slice: the gate half of config 1's fused [2048, 19456] bf16 buffer copied out to [2048, 9728]
+    "slice_gate": 2 * 2048 * 9728 * 2,
     "attention_f16_decode": 2 * 65536 * 8 * 128 * 2 + 2 * 32 * 128 * 4,
     "attention_turbo4_decode": 2 * (65536 * 8 * 64 + 65536 * 8 * 2) + 2 * 32 * 128 * 4,
     "attention_i8_turbo4_decode": 65536 * 8 * (128 + 4) + 65536 * 8 * (64 + 2) + 2 * 32 * 128 * 4,
