@@ -722,7 +722,7 @@ struct KeyLane {
         } else {
 #pragma unroll
             for (int i = 0; i < kWords / 4; ++i) {
-                const u32x4 v = ld128(gc + 4 * kWords * l8 + 16 * i);
+                const u32x4 v = ld128_nt(gc + 4 * kWords * l8 + 16 * i);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) w[4 * i + j] = v[j];
             }
@@ -766,7 +766,7 @@ struct ValueSlice {
         } else {
 #pragma unroll
             for (int i = 0; i < kWords / 4; ++i) {
-                const u32x4 v = ld128(gc + 4 * kWords * vlane + 16 * i);
+                const u32x4 v = ld128_nt(gc + 4 * kWords * vlane + 16 * i);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) w[4 * i + j] = v[j];
             }
@@ -1028,7 +1028,7 @@ __global__ __launch_bounds__(256, rows_waves(KF, D, G) == 3 ? 3 : 1) void attent
 #pragma unroll
                     for (int st = 0; st < kSteps; ++st) {
                         if constexpr (KF == 16) {
-                            const u32x4 v = ld128(kc + 2 * (row * D + 32 * st + kq));
+                            const u32x4 v = ld128_nt(kc + 2 * (row * D + 32 * st + kq));
 #pragma unroll
                             for (int i = 0; i < 4; ++i) araw[bb][st][i] = v[i];
                         } else if constexpr (KF == 8) {
